@@ -1,0 +1,276 @@
+#!/usr/bin/env python3
+"""Benchmark of libortho_amd's fused dual GEMM on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one forward of the dual GEMM (one kernel launch) over one batch:
+the headline workload is BASELINE.json's configs[1] at M=1 (OrthoLinear
+4096 -> 11008, INT4 group-128, ortho 1 % uniform, alpha = 1), the decode
+regime the GB/s metric is quoted on.  Inputs are resident in HBM before the
+timed region; the weights rotate over enough copies (>= 16, > 512 MB) that
+no step finds its weights in the 256 MB Infinity Cache.  The K timed steps
+are one replay of a HIP graph holding exactly K launches (launch cost on the
+host is not what is measured), bracketed by synchronisation.
+
+Printed: one JSON line with the contract fields plus
+  roofline      the decode kernel: algorithmic bytes per launch / its average
+                launch duration (HIP event pair around every launch, eager,
+                on the launch stream) against 8 TB/s
+  cpu_baseline  the reference CPU forward restated (oracle/cpu_baseline.c,
+                reference flags, 1 pinned core) on a bounded sample
+  secondary     the rest of the metric: M in {2,4,8,16} GB/s, and the
+                prefill TFLOP/s at M=2048 (4096->11008 and 4096->4096)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "dual-GEMM GB/s (M=1) & TFLOP/s (M=2048) at 4096x11008, % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk, dense
+ROTATE_MIN_BYTES = 512 << 20
+ROTATE_MIN_COPIES = 16
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="budget for the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------- CPU leg
+
+def cpu_baseline(layer, x, alpha, budget_s):
+    """Single-core timing of the restated reference CPU forward on the same
+    layer and input (FP16 -> FP32 conversion outside the timed region)."""
+    from oracle import oracle
+    if not os.path.exists(os.path.join(ROOT, "oracle", "liboracle.so")):
+        oracle.build()
+    cpu = sorted(os.sched_getaffinity(0))[0]
+    old = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {cpu})
+    try:
+        xs = x.astype(np.float32)
+        t1, _ = oracle.baseline_time(layer.q, layer.scales, layer.row_ptr, layer.col, layer.vals,
+                                     xs, alpha, 0, 1)
+        iters = max(3, min(200, int(budget_s / max(t1, 1e-6))))
+        t, _ = oracle.baseline_time(layer.q, layer.scales, layer.row_ptr, layer.col, layer.vals,
+                                    xs, alpha, 2, iters)
+    finally:
+        os.sched_setaffinity(0, old)
+    return t, iters
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------- GPU leg
+
+class Rotation:
+    """R device copies of one layer (distinct addresses, identical data)."""
+
+    def __init__(self, layer, torch, min_copies=ROTATE_MIN_COPIES, min_bytes=ROTATE_MIN_BYTES,
+                 plan=False):
+        from libortho_amd import _C_ops, workloads as W
+        d = W.to_device(layer)
+        per = sum(t.numel() * t.element_size() for t in d.values())
+        self.n = max(min_copies, -(-min_bytes // per))
+        self.copies = [d] + [{k: v.clone() for k, v in d.items()} for _ in range(self.n - 1)]
+        self.plans = [None] * self.n
+        if plan:
+            self.plans = [_C_ops.build_plan(c["q"], c["scales"], c["vals"], c["col"], c["row_ptr"],
+                                            layer.K) for c in self.copies]
+
+    def call(self, i, x, y, alpha):
+        from libortho_amd import _C_ops
+        c = self.copies[i % self.n]
+        _C_ops.forward_planned(c["q"], c["scales"], c["vals"], c["col"], c["row_ptr"], x, y, alpha,
+                               self.plans[i % self.n])
+
+
+def time_workload(torch, layer, M, alpha, steps, warmup, plan=False, per_launch=True):
+    """Returns dict(ms_per_step, launch_us, kernel) for `steps` forwards."""
+    from libortho_amd import _C_ops, workloads as W
+    rot = Rotation(layer, torch, plan=plan)
+    x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda()
+    y = torch.empty(M, layer.N, dtype=torch.float16, device="cuda")
+    for i in range(warmup):
+        rot.call(i, x, y, alpha)
+    torch.cuda.synchronize()
+    kernel = _C_ops.last_kernel()
+    assert torch.isfinite(y).all().item(), "non-finite output"
+
+    # per-launch event pairs (eager): average launch duration on the stream
+    launch_us = None
+    if per_launch:
+        n = min(steps, 400)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(n)]
+        for i in range(n):
+            ev[i][0].record()
+            rot.call(i, x, y, alpha)
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        launch_us = 1e3 * float(np.mean([a.elapsed_time(b) for a, b in ev]))
+
+    # K steps captured in one graph, replayed once untimed and once timed
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        rot.call(0, x, y, alpha)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            rot.call(i, x, y, alpha)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    del g
+    return dict(ms_per_step=ms, launch_us=launch_us, kernel=kernel, copies=rot.n)
+
+
+def load_traffic(workload: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE,
+    WRITE_SIZE, copy-kernel calibrated), committed in profiles/traffic.json."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        return json.load(open(p)).get(workload)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; the dual GEMM shards by output rows "
+              "with no collective (see DESIGN.md), and multi-GPU runs are not part of it",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from libortho_amd import workloads as W
+    layer = W.config_layer("c2")
+    M, alpha = 1, 1.0
+    x0 = W.make_x(M, layer.K, 7000 + M)
+    bytes_step = W.algorithmic_bytes(layer, M, alpha)
+    flops_step = W.algorithmic_flops(layer, M, alpha)
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline: c2 M=1 alpha=1, restated orth_layer_forward, 1 core ...")
+        t_cpu, iters = cpu_baseline(layer, x0, alpha, args.cpu_seconds)
+        cpu = {"value": round(bytes_step / t_cpu / 1e9, 4), "unit": "GB/s", "cores": 1,
+               "kind": "port",
+               "sample": f"c2 M=1 alpha=1 (the headline workload, whole layer), {iters} timed "
+                         f"calls after 2 warmups, {t_cpu * 1e3:.2f} ms/call, same algorithmic "
+                         f"bytes; oracle/cpu_baseline.c with the reference's -O3 -ffast-math "
+                         f"-funroll-loops; host: {cpu_model()}, nproc={os.cpu_count()}",
+               "ms_per_call": round(t_cpu * 1e3, 3)}
+        log(f"  {t_cpu * 1e3:.2f} ms/call over {iters} calls")
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    from libortho_amd import _lib
+    info = _lib.device_info(0)
+    log(f"device: {info['arch']}, {info['compute_units']} CUs, clock {info['clock_khz'] / 1e3:.0f} MHz")
+
+    log(f"decode c2 M=1: warmup {args.warmup}, steps {args.steps} ...")
+    r = time_workload(torch, layer, M, alpha, args.steps, args.warmup)
+    gbs = bytes_step / (r["ms_per_step"] * 1e-3) / 1e9
+    achieved = bytes_step / (r["launch_us"] * 1e-6) / 1e9
+    log(f"  graph {r['ms_per_step'] * 1e3:.2f} us/step -> {gbs:.0f} GB/s; "
+        f"event-pair launch {r['launch_us']:.2f} us -> {achieved:.0f} GB/s; kernel {r['kernel']}")
+
+    secondary = []
+    if not args.no_secondary:
+        for m in (2, 4, 8, 16):
+            rr = time_workload(torch, layer, m, alpha, args.steps, 10)
+            b = W.algorithmic_bytes(layer, m, alpha)
+            secondary.append({"workload": f"c2 M={m}", "kernel": rr["kernel"],
+                              "us_per_step": round(rr["ms_per_step"] * 1e3, 3),
+                              "GB/s": round(b / (rr["ms_per_step"] * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(b / (rr["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "launch_us": round(rr["launch_us"], 3)})
+            log(f"  {secondary[-1]}")
+        for name, lay in (("4096->11008", layer), ("4096->4096 (c3)", W.config_layer("c3"))):
+            for a in (1.0, 0.0):
+                rr = time_workload(torch, lay, 2048, a, 20, 3, plan=True, per_launch=False)
+                f = W.algorithmic_flops(lay, 2048, a)
+                tf = f / (rr["ms_per_step"] * 1e-3) / 1e12
+                secondary.append({"workload": f"prefill {name} M=2048 alpha={a}",
+                                  "kernel": rr["kernel"],
+                                  "us_per_step": round(rr["ms_per_step"] * 1e3, 2),
+                                  "TFLOP/s": round(tf, 1),
+                                  "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
+                log(f"  {secondary[-1]}")
+
+    workload = "c2_m1_alpha1"
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded PCG64; INT4 weights, FP16 scales/values/activations)",
+        "config": {"workload": "OrthoLinear 4096->11008 (BASELINE configs[1]), M=1 decode, "
+                               "INT4 group-128 FP16 scales, ortho 1% uniform FP16, alpha=1",
+                   "in_features": layer.K, "out_features": layer.N, "tokens": M,
+                   "group_size": 128, "ortho_nnz": layer.nnz, "alpha": alpha,
+                   "bytes_per_step": bytes_step, "flops_per_step": flops_step,
+                   "weight_copies_rotated": r["copies"], "kernel": r["kernel"],
+                   "timing": "K launches in one HIP graph, one timed replay"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(workload),
+                     "launch_us": round(r["launch_us"], 3),
+                     "bytes_per_launch": bytes_step},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+        "device": {k: info[k] for k in ("arch", "compute_units", "clock_khz")},
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

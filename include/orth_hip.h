@@ -1,0 +1,178 @@
+/*
+ * libortho_amd -- C ABI of the MI355X (gfx950) fused dual GEMM
+ *
+ *   y[m,n] = sum_k x[m,k] * q[n,k] * s[n, k/G]
+ *          + [alpha > 0 && nnz > 0] * alpha * sum_{j in row n} v_j * x[m, c_j]
+ *
+ * A dense signed-INT4 "Base" (two nibbles per byte, FP16 scales per output
+ * row or per group of G input columns) plus a sparse "Ortho" correction in
+ * CSR form, in one launch.  All pointers are device pointers unless stated;
+ * calls are asynchronous on the stream passed in (NULL = the null stream)
+ * and never synchronise the device.  Plain C types only: no HIP or torch
+ * types appear in the signatures (a stream is passed as void*).
+ *
+ * Replaces the reference's C ABI, /root/reference/include/ortho.h:22-159,
+ * and its CUDA entry points, /root/reference/src/dual_gemm.cu:295-372 and
+ * /root/reference/src/dual_gemm_tensor_core.cu:342-428.
+ */
+#ifndef ORTH_HIP_H
+#define ORTH_HIP_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of the buffers a layer points to. */
+typedef enum {
+    ORTH_DT_F16 = 0,
+    ORTH_DT_BF16 = 1,
+    ORTH_DT_F32 = 2
+} orth_dtype_t;
+
+/* Status codes.  Every entry point returns one; the message of the last
+ * failure on the calling thread is in orth_hip_last_error().
+ * Replaces the reference's 0 / -1 returns (src/dual_gemm.cu:301-303,361-371). */
+typedef enum {
+    ORTH_OK = 0,
+    ORTH_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad shape, bad dtype     */
+    ORTH_ERR_UNSUPPORTED = 2,      /* valid request this build cannot serve  */
+    ORTH_ERR_HIP = 3,              /* a HIP runtime call failed              */
+    ORTH_ERR_NO_DEVICE = 4         /* no usable gfx950 device                */
+} orth_status_t;
+
+/* The packed Base.  Mirrors orth_base_t, /root/reference/include/ortho.h:22-28,
+ * with the scale element type and the number of scale groups made explicit.
+ *   q_weight  uint8 [out_features, in_features/2]; element (n,k) is nibble
+ *             n*K+k: byte (n*K+k)/2, low nibble for even k, two's complement
+ *             (/root/reference/src/ortho.c:315-325)
+ *   q_scales  [out_features, scale_groups] of scale_dtype (F16 or F32);
+ *             G = in_features / scale_groups; scale_groups == 1 is the
+ *             reference's per-row scale (/root/reference/torch_bind/ortho_linear.py:60) */
+typedef struct {
+    const void *q_weight;
+    const void *q_scales;
+    int32_t q_bits;          /* must be 4 */
+    int32_t scale_dtype;     /* orth_dtype_t: ORTH_DT_F16 or ORTH_DT_F32 */
+    int64_t scale_groups;    /* K / G, >= 1, divides in_features */
+    int64_t in_features;     /* K, even, > 0 */
+    int64_t out_features;    /* N, > 0 */
+} orth_hip_base_t;
+
+/* The sparse Ortho in CSR form.  Mirrors the CSR half of orth_ortho_t,
+ * /root/reference/include/ortho.h:41-53 (the deprecated uint16 COO index is
+ * not supported), as packed by /root/reference/tools/sieve.py:119-152.
+ *   row_ptr      int32 [out_features + 1]; may be NULL when count == 0
+ *   col_indices  int32 [count]; entries with col < 0 or col >= K are skipped
+ *                (the reference's guard, /root/reference/src/dual_gemm.cu:124)
+ *   values       [count] of value_dtype (F16 or F32) */
+typedef struct {
+    const int32_t *row_ptr;
+    const int32_t *col_indices;
+    const void *values;
+    int32_t value_dtype;     /* orth_dtype_t: ORTH_DT_F16 or ORTH_DT_F32 */
+    int32_t reserved;
+    int64_t count;           /* nnz */
+} orth_hip_ortho_t;
+
+/* The dual-manifold layer.  Mirrors orth_layer_t,
+ * /root/reference/include/ortho.h:63-71: the ortho term is applied iff
+ * alpha > 0 and count > 0 (/root/reference/src/ortho.c:343), so a zero or
+ * negative alpha gives the Base alone. */
+typedef struct {
+    orth_hip_base_t base;
+    orth_hip_ortho_t ortho;
+    float alpha;
+} orth_hip_layer_t;
+
+/* Sets layer->alpha.  Replaces orth_layer_set_alpha,
+ * /root/reference/include/ortho.h:91 (/root/reference/src/ortho.c:111-115). */
+void orth_layer_hip_set_alpha(orth_hip_layer_t *layer, float alpha);
+
+/* Host-side validation of a forward call, with no device access: returns
+ * ORTH_OK or the status orth_layer_forward_hip would return for these
+ * arguments before launching anything.  No reference counterpart (the
+ * reference validates nothing, /root/reference/torch_bind/bindings.cpp:19-43). */
+int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void *output,
+                         int64_t batch_size, int32_t io_dtype);
+
+/* Forward pass y = Base(x) + alpha * Ortho(x).
+ *   input   [batch_size, in_features] of io_dtype (F16, BF16 or F32), row-major
+ *   output  [batch_size, out_features] of io_dtype, written in full
+ * Picks the decode kernel (batch <= 16), the MFMA prefill kernel (batch > 16)
+ * or a general kernel for shapes and dtypes the fast kernels do not take.
+ * A prefill launch without a plan builds one in stream-ordered temporary
+ * memory.  Replaces orth_layer_forward_cuda, /root/reference/include/ortho.h:141-144
+ * (/root/reference/src/dual_gemm.cu:295-372), the body of the torch binding
+ * /root/reference/torch_bind/bindings.cpp:9-44, and the CPU entry
+ * orth_layer_forward, /root/reference/include/ortho.h:132-135. */
+int orth_layer_forward_hip(const orth_hip_layer_t *layer, const void *input, void *output,
+                           int64_t batch_size, int32_t io_dtype, void *stream);
+
+/* Same, with a prebuilt ortho plan (orth_ortho_plan_build) for the prefill
+ * kernel; plan may be NULL.  The plan must have been built from this layer's
+ * current CSR buffers.  No reference counterpart: the plan is a derived
+ * layout of the CSR of /root/reference/tools/sieve.py:119-152. */
+int orth_layer_forward_hip_planned(const orth_hip_layer_t *layer, const void *plan,
+                                   int64_t plan_bytes, const void *input, void *output,
+                                   int64_t batch_size, int32_t io_dtype, void *stream);
+
+/* Size in bytes of the ortho plan for this layer (0 when count == 0), or a
+ * negative orth_status_t on invalid arguments. */
+int64_t orth_ortho_plan_bytes(const orth_hip_layer_t *layer);
+
+/* Builds the ortho plan into caller-owned device memory and waits for it
+ * (load-time call: it synchronises the stream to report CSR errors).
+ * Returns ORTH_ERR_INVALID_ARGUMENT for a row_ptr that is not monotone or
+ * does not end at count.  Derived layout of the CSR of
+ * /root/reference/tools/sieve.py:119-152; no reference counterpart. */
+int orth_ortho_plan_build(const orth_hip_layer_t *layer, void *plan, int64_t plan_bytes,
+                          void *stream);
+
+/* Writes the dequantised Base, out[n*K+k] = float(q[n,k]) * float(s[n,k/G]),
+ * as FP32 [out_features, in_features] (exact: |q| <= 8 times an FP16 scale
+ * fits in 24 bits).  Debug/parity entry; replaces the per-element
+ * "(float)unpack_int4(...) * scale" of /root/reference/src/ortho.c:360-363
+ * and unpack_int4 of /root/reference/src/dual_gemm.cu:30-40. */
+int orth_base_dequant_hip(const orth_hip_layer_t *layer, float *out, void *stream);
+
+/* Device facts.  Replaces check_tensor_core_support,
+ * /root/reference/src/dual_gemm_tensor_core.cu:342-350. */
+typedef struct {
+    char arch[64];            /* e.g. "gfx950:sramecc+:xnack-" */
+    int32_t is_gfx950;        /* 1 when the fast kernels can run */
+    int32_t compute_units;
+    int32_t wavefront_size;
+    int32_t lds_bytes_per_block;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width;
+    int32_t l2_bytes;
+    int64_t global_mem_bytes;
+} orth_hip_device_info_t;
+
+int orth_hip_device_info(int device, orth_hip_device_info_t *info);
+
+/* Kernel choice override for benchmarking and tests: 0 = automatic (the
+ * default), 1 = decode, 2 = prefill, 3 = general.  A forced kernel that
+ * cannot take a call returns ORTH_ERR_UNSUPPORTED.  Process-wide. */
+int orth_hip_set_kernel_policy(int policy);
+int orth_hip_get_kernel_policy(void);
+
+/* The kernel the calling thread's last successful forward launched:
+ * 1 decode, 2 prefill, 3 general, 0 none. */
+int orth_hip_last_kernel(void);
+
+/* Message of the calling thread's last failure ("" if none). */
+const char *orth_hip_last_error(void);
+
+/* ABI version of this header (major * 100 + minor). */
+int orth_hip_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORTH_HIP_H */

@@ -1,0 +1,193 @@
+"""``libortho._C_ops`` for MI355X: the operator boundary of the dual GEMM.
+
+Drop-in for the reference's torch extension, whose only entry point is
+
+    forward(q_weight, q_scales, ortho_values, ortho_col_indices,
+            ortho_row_ptr, input, output, alpha) -> None
+
+(/root/reference/torch_bind/bindings.cpp:9-48).  Same eight positional
+arguments, same meaning, ``output`` written in place, returns ``None``.
+Unlike the reference binding (which cannot dispatch, bindings.cpp:39-43, and
+reads FP16 buffers as FP32, :24,30) this one checks every tensor the way the
+reference's draft binding intended (docs/202511271753/libortho_ops.cpp:17-20,
+49-53) and raises ``RuntimeError`` with the reason, then calls the C ABI of
+include/orth_hip.h on torch's current stream for ``input.device``.
+
+Tensor contract:
+  q_weight          uint8  [N, K/2]   packed signed INT4 (low nibble = even k)
+  q_scales          fp16|fp32 [N] (per row) or [N, K/G] (group G)
+  ortho_values      fp16|fp32 [nnz]
+  ortho_col_indices int32  [nnz]
+  ortho_row_ptr     int32  [N+1]  (may be empty when nnz == 0)
+  input             fp16|bf16|fp32 [M, K] contiguous
+  output            same dtype as input, [M, N] contiguous
+  alpha             float; ortho applied iff alpha > 0 and nnz > 0
+
+Torch appears only here, as plumbing (device pointers, dtypes, streams); the
+library signatures carry plain pointers and sizes.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float16: _lib.DT_F16, torch.bfloat16: _lib.DT_BF16, torch.float32: _lib.DT_F32}
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _ptr(t: torch.Tensor):
+    return ctypes.c_void_p(t.data_ptr()) if t.numel() > 0 else None
+
+
+def make_layer(q_weight: torch.Tensor, q_scales: torch.Tensor, ortho_values: torch.Tensor,
+               ortho_col_indices: torch.Tensor, ortho_row_ptr: torch.Tensor, K: int, N: int,
+               alpha: float, device: torch.device) -> _lib.OrthHipLayer:
+    """Validate the weight tensors and describe them as an orth_hip_layer_t."""
+    for name, t in (("q_weight", q_weight), ("q_scales", q_scales),
+                    ("ortho_values", ortho_values), ("ortho_col_indices", ortho_col_indices),
+                    ("ortho_row_ptr", ortho_row_ptr)):
+        _req(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+        _req(t.numel() == 0 or t.device == device,
+             f"{name} is on {t.device} but input is on {device}")
+        _req(t.is_contiguous(), f"{name} must be contiguous")
+    _req(K > 0 and K % 2 == 0, f"in_features must be positive and even (got {K})")
+    _req(q_weight.dtype == torch.uint8, f"q_weight must be uint8 (got {q_weight.dtype})")
+    _req(tuple(q_weight.shape) == (N, K // 2),
+         f"q_weight must have shape ({N}, {K // 2}) (got {tuple(q_weight.shape)})")
+    _req(q_scales.dtype in (torch.float16, torch.float32),
+         f"q_scales must be float16 or float32 (got {q_scales.dtype})")
+    if q_scales.dim() == 1:
+        _req(q_scales.shape[0] == N, f"q_scales must have {N} rows (got {tuple(q_scales.shape)})")
+        groups = 1
+    else:
+        _req(q_scales.dim() == 2 and q_scales.shape[0] == N,
+             f"q_scales must be [{N}] or [{N}, K/G] (got {tuple(q_scales.shape)})")
+        groups = int(q_scales.shape[1])
+        _req(groups >= 1 and K % groups == 0,
+             f"q_scales has {groups} groups, which does not divide in_features {K}")
+    nnz = int(ortho_values.numel())
+    _req(ortho_col_indices.numel() == nnz,
+         f"ortho_col_indices has {ortho_col_indices.numel()} entries, ortho_values {nnz}")
+    if nnz > 0:
+        _req(ortho_values.dtype in (torch.float16, torch.float32),
+             f"ortho_values must be float16 or float32 (got {ortho_values.dtype})")
+        _req(ortho_col_indices.dtype == torch.int32,
+             f"ortho_col_indices must be int32 (got {ortho_col_indices.dtype})")
+        _req(ortho_row_ptr.dtype == torch.int32,
+             f"ortho_row_ptr must be int32 (got {ortho_row_ptr.dtype})")
+        _req(ortho_row_ptr.numel() == N + 1,
+             f"ortho_row_ptr must have {N + 1} entries (got {ortho_row_ptr.numel()})")
+    layer = _lib.OrthHipLayer()
+    layer.base.q_weight = _ptr(q_weight)
+    layer.base.q_scales = _ptr(q_scales)
+    layer.base.q_bits = 4
+    layer.base.scale_dtype = _DT[q_scales.dtype]
+    layer.base.scale_groups = groups
+    layer.base.in_features = K
+    layer.base.out_features = N
+    layer.ortho.count = nnz
+    if nnz > 0:
+        layer.ortho.row_ptr = _ptr(ortho_row_ptr)
+        layer.ortho.col_indices = _ptr(ortho_col_indices)
+        layer.ortho.values = _ptr(ortho_values)
+        layer.ortho.value_dtype = _DT[ortho_values.dtype]
+    layer.alpha = float(alpha)
+    return layer
+
+
+def _check_io(input: torch.Tensor, output: torch.Tensor):
+    _req(isinstance(input, torch.Tensor) and isinstance(output, torch.Tensor),
+         "input and output must be tensors")
+    _req(input.is_cuda, "input must be on a ROCm GPU (libortho_amd has no CPU path)")
+    _req(output.device == input.device, "output must be on the same device as input")
+    _req(input.dim() == 2 and output.dim() == 2, "input and output must be 2-D [M, K] / [M, N]")
+    _req(input.dtype in _DT, f"input dtype {input.dtype} is not float16, bfloat16 or float32")
+    _req(output.dtype == input.dtype,
+         f"output dtype {output.dtype} must equal input dtype {input.dtype}")
+    _req(input.is_contiguous() and output.is_contiguous(), "input and output must be contiguous")
+    _req(output.shape[0] == input.shape[0],
+         f"output has {output.shape[0]} rows, input {input.shape[0]}")
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def forward(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input, output,
+            alpha) -> None:
+    """y = Base(x) + alpha * Ortho(x), written into ``output`` in place."""
+    forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input,
+                    output, alpha, None)
+
+
+def forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input,
+                    output, alpha, plan) -> None:
+    """``forward`` with an ortho plan from :func:`build_plan` (or None)."""
+    _check_io(input, output)
+    K, N = int(input.shape[1]), int(output.shape[1])
+    dev = input.device
+    layer = make_layer(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, K, N,
+                       float(alpha), dev)
+    L = _lib.lib()
+    with torch.cuda.device(dev):
+        if plan is not None and plan.numel() > 0:
+            _req(plan.device == dev and plan.dtype == torch.uint8, "plan must be a uint8 tensor on input's device")
+            rc = L.orth_layer_forward_hip_planned(ctypes.byref(layer), _ptr(plan), plan.numel(),
+                                                  _ptr(input), _ptr(output), int(input.shape[0]),
+                                                  _DT[input.dtype], _stream(dev))
+        else:
+            rc = L.orth_layer_forward_hip(ctypes.byref(layer), _ptr(input), _ptr(output),
+                                          int(input.shape[0]), _DT[input.dtype], _stream(dev))
+    _lib.check(rc)
+
+
+def build_plan(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr,
+               in_features: int):
+    """Build the ortho plan (derived layout of the CSR used by the prefill
+    kernel) into a new uint8 tensor on the weights' device.  Returns None when
+    the layer has no ortho entries or its shape takes no plan."""
+    dev = q_weight.device
+    _req(dev.type == "cuda", "build_plan needs the weights on a ROCm GPU")
+    N = int(q_weight.shape[0])
+    layer = make_layer(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr,
+                       int(in_features), N, 1.0, dev)
+    L = _lib.lib()
+    nbytes = L.orth_ortho_plan_bytes(ctypes.byref(layer))
+    if nbytes <= 0:
+        return None
+    plan = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(L.orth_ortho_plan_build(ctypes.byref(layer), _ptr(plan), plan.numel(),
+                                           _stream(dev)))
+    return plan
+
+
+def dequant(q_weight, q_scales, in_features: int) -> torch.Tensor:
+    """FP32 [N, K] dequantised Base, float(q) * float(s), on the GPU."""
+    dev = q_weight.device
+    _req(dev.type == "cuda", "dequant needs the weights on a ROCm GPU")
+    N = int(q_weight.shape[0])
+    empty_f = torch.empty(0, dtype=torch.float16, device=dev)
+    empty_i = torch.empty(0, dtype=torch.int32, device=dev)
+    layer = make_layer(q_weight, q_scales, empty_f, empty_i, empty_i, int(in_features), N, 0.0, dev)
+    out = torch.empty((N, int(in_features)), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().orth_base_dequant_hip(ctypes.byref(layer), _ptr(out), _stream(dev)))
+    return out
+
+
+def last_kernel() -> str:
+    """Kernel used by this thread's last forward: decode, prefill or general."""
+    return _lib.last_kernel()
+
+
+set_kernel_policy = _lib.set_kernel_policy
+get_kernel_policy = _lib.get_kernel_policy
+device_info = _lib.device_info

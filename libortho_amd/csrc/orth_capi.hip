@@ -1,0 +1,348 @@
+// Host side of the C ABI declared in include/orth_hip.h: argument
+// validation, kernel choice, temporary plans and error reporting.
+//
+// Replaces the reference's host wrappers /root/reference/src/dual_gemm.cu:295-372
+// (which launch on the legacy default stream and synchronise the device on
+// every call) and /root/reference/torch_bind/bindings.cpp:9-44 (which checks
+// nothing and drops the return code).  Here every call is validated on the
+// host, launched asynchronously on the caller's stream, and reported through
+// a status code plus a per-thread message.
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "orth_common.h"
+
+namespace orth {
+hipError_t launch_general(const ForwardArgs &a, hipStream_t stream);
+hipError_t launch_dequant(const ForwardArgs &a, float *out, hipStream_t stream);
+bool decode_supported(const ForwardArgs &a);
+hipError_t launch_decode(const ForwardArgs &a, hipStream_t stream);
+bool prefill_supported(const ForwardArgs &a);
+bool plan_supported(const ForwardArgs &a);
+int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz);
+hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t stream);
+hipError_t plan_read_flags(const void *plan, hipStream_t stream, uint32_t *flags);
+hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream);
+hipError_t prefill_prepare_device();
+hipError_t plan_prepare_device();
+}  // namespace orth
+
+using namespace orth;
+
+namespace {
+
+thread_local std::string t_error;
+thread_local int t_last_kernel = KERNEL_NONE;
+
+int policy_from_env() {
+    const char *e = std::getenv("ORTH_KERNEL_POLICY");
+    if (!e) return 0;
+    if (!std::strcmp(e, "decode")) return 1;
+    if (!std::strcmp(e, "prefill")) return 2;
+    if (!std::strcmp(e, "general")) return 3;
+    return 0;
+}
+
+std::atomic<int> g_policy{policy_from_env()};
+
+int fail(int status, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    t_error = buf;
+    return status;
+}
+
+int fail_hip(hipError_t e, const char *what) {
+    return fail(ORTH_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+bool valid_dtype(int32_t d) { return d == ORTH_DT_F16 || d == ORTH_DT_BF16 || d == ORTH_DT_F32; }
+
+// Validates a layer (and, when check_io, the activations) and fills args.
+int resolve(const orth_hip_layer_t *L, const void *input, void *output, int64_t batch,
+            int32_t io_dtype, bool check_io, ForwardArgs &a) {
+    if (!L) return fail(ORTH_ERR_INVALID_ARGUMENT, "layer is NULL");
+    const orth_hip_base_t &b = L->base;
+    const orth_hip_ortho_t &o = L->ortho;
+    if (!b.q_weight) return fail(ORTH_ERR_INVALID_ARGUMENT, "base.q_weight is NULL");
+    if (!b.q_scales) return fail(ORTH_ERR_INVALID_ARGUMENT, "base.q_scales is NULL");
+    if (b.q_bits != 4)
+        return fail(ORTH_ERR_UNSUPPORTED, "base.q_bits is %d; only 4-bit weights are supported", b.q_bits);
+    if (b.in_features <= 0 || (b.in_features & 1))
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "in_features must be positive and even (got %lld)",
+                    (long long)b.in_features);
+    if (b.out_features <= 0)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "out_features must be positive (got %lld)",
+                    (long long)b.out_features);
+    if (b.in_features > ((int64_t)1 << 40) / b.out_features)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "in_features * out_features is too large");
+    if (b.scale_groups < 1 || b.in_features % b.scale_groups != 0)
+        return fail(ORTH_ERR_INVALID_ARGUMENT,
+                    "scale_groups (%lld) must be >= 1 and divide in_features (%lld)",
+                    (long long)b.scale_groups, (long long)b.in_features);
+    if (b.scale_dtype != ORTH_DT_F16 && b.scale_dtype != ORTH_DT_F32)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "scale_dtype must be F16 or F32 (got %d)", b.scale_dtype);
+    if (o.count < 0) return fail(ORTH_ERR_INVALID_ARGUMENT, "ortho.count is negative");
+    if (o.count >= ((int64_t)1 << 31))
+        return fail(ORTH_ERR_UNSUPPORTED, "ortho.count exceeds the int32 CSR index range");
+    if (o.count > 0) {
+        if (!o.row_ptr || !o.col_indices || !o.values)
+            return fail(ORTH_ERR_INVALID_ARGUMENT, "ortho has %lld entries but a NULL CSR buffer",
+                        (long long)o.count);
+        if (o.value_dtype != ORTH_DT_F16 && o.value_dtype != ORTH_DT_F32)
+            return fail(ORTH_ERR_INVALID_ARGUMENT, "ortho.value_dtype must be F16 or F32 (got %d)",
+                        o.value_dtype);
+    }
+    if (check_io) {
+        if (batch < 0) return fail(ORTH_ERR_INVALID_ARGUMENT, "batch_size is negative");
+        if (!valid_dtype(io_dtype))
+            return fail(ORTH_ERR_INVALID_ARGUMENT, "io_dtype must be F16, BF16 or F32 (got %d)", io_dtype);
+        if (batch > 0 && (!input || !output))
+            return fail(ORTH_ERR_INVALID_ARGUMENT, "input or output is NULL");
+        if (batch > ((int64_t)1 << 40) / b.in_features || batch > ((int64_t)1 << 40) / b.out_features)
+            return fail(ORTH_ERR_INVALID_ARGUMENT, "batch_size is too large");
+    }
+    a.q = static_cast<const uint8_t *>(b.q_weight);
+    a.scales = b.q_scales;
+    a.scale_dtype = b.scale_dtype;
+    a.ngroups = b.scale_groups;
+    a.G = b.in_features / b.scale_groups;
+    a.row_ptr = o.row_ptr;
+    a.col = o.col_indices;
+    a.vals = o.values;
+    a.val_dtype = o.value_dtype;
+    a.nnz = o.count;
+    a.x = input;
+    a.y = output;
+    a.io_dtype = io_dtype;
+    a.M = batch;
+    a.K = b.in_features;
+    a.N = b.out_features;
+    a.alpha = L->alpha;
+    // the reference's gate: alpha > 0 && count > 0 (src/ortho.c:343); NaN -> off
+    a.has_ortho = (L->alpha > 0.0f && o.count > 0) ? 1 : 0;
+    t_error.clear();
+    return ORTH_OK;
+}
+
+// Per-device check that the current device is a gfx950 (the only code object
+// this library carries) and one-time kernel attribute set-up.
+struct DeviceState {
+    int checked = 0;  // 0 unknown, 1 ok, -1 not gfx950
+    char arch[64] = {0};
+};
+std::mutex g_dev_mu;
+DeviceState g_dev[64];
+
+int current_device_ok(int *dev_out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(ORTH_ERR_NO_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= 64) return fail(ORTH_ERR_NO_DEVICE, "device index %d out of range", dev);
+    if (dev_out) *dev_out = dev;
+    DeviceState &st = g_dev[dev];
+    if (st.checked == 0) {
+        std::lock_guard<std::mutex> lk(g_dev_mu);
+        if (st.checked == 0) {
+            hipDeviceProp_t p;
+            e = hipGetDeviceProperties(&p, dev);
+            if (e != hipSuccess) return fail_hip(e, "hipGetDeviceProperties");
+            std::snprintf(st.arch, sizeof(st.arch), "%s", p.gcnArchName);
+            const bool ok = std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+            if (ok) {
+                e = prefill_prepare_device();
+                if (e == hipSuccess) e = plan_prepare_device();
+                if (e != hipSuccess) return fail_hip(e, "kernel attribute set-up");
+            }
+            st.checked = ok ? 1 : -1;
+        }
+    }
+    if (st.checked < 0)
+        return fail(ORTH_ERR_NO_DEVICE, "device %d is %s; this library carries gfx950 code only", dev,
+                    st.arch);
+    return ORTH_OK;
+}
+
+int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
+                 const void *input, void *output, int64_t batch, int32_t io_dtype, void *stream_v) {
+    ForwardArgs a;
+    int rc = resolve(layer, input, output, batch, io_dtype, true, a);
+    if (rc != ORTH_OK) return rc;
+    if (plan && plan_bytes < plan_bytes_for(a.N, a.K, a.nnz))
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "plan_bytes %lld is smaller than the plan size %lld",
+                    (long long)plan_bytes, (long long)plan_bytes_for(a.N, a.K, a.nnz));
+    if (batch == 0) {
+        t_last_kernel = KERNEL_NONE;
+        return ORTH_OK;
+    }
+    rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipStream_t stream = static_cast<hipStream_t>(stream_v);
+
+    const int policy = g_policy.load(std::memory_order_relaxed);
+    const bool dec_ok = decode_supported(a);
+    const bool pre_ok = prefill_supported(a);
+    int kernel;
+    switch (policy) {
+        case 1:
+            if (!dec_ok) return fail(ORTH_ERR_UNSUPPORTED, "decode kernel forced but it cannot take this call");
+            kernel = KERNEL_DECODE;
+            break;
+        case 2:
+            if (!pre_ok) return fail(ORTH_ERR_UNSUPPORTED, "prefill kernel forced but it cannot take this call");
+            kernel = KERNEL_PREFILL;
+            break;
+        case 3:
+            kernel = KERNEL_GENERAL;
+            break;
+        default:
+            kernel = dec_ok ? KERNEL_DECODE : (pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL);
+    }
+
+    hipError_t e = hipSuccess;
+    if (kernel == KERNEL_DECODE) {
+        e = launch_decode(a, stream);
+    } else if (kernel == KERNEL_PREFILL) {
+        if (a.has_ortho && !plan) {
+            // stream-ordered temporary plan: allocated, built, used and freed
+            // in stream order, so the call stays asynchronous
+            const int64_t pb = plan_bytes_for(a.N, a.K, a.nnz);
+            void *tmp = nullptr;
+            e = hipMallocAsync(&tmp, (size_t)pb, stream);
+            if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (temporary ortho plan)");
+            e = launch_plan_build(a, tmp, stream);
+            if (e == hipSuccess) e = launch_prefill(a, tmp, stream);
+            hipError_t f = hipFreeAsync(tmp, stream);
+            if (e == hipSuccess) e = f;
+        } else {
+            e = launch_prefill(a, a.has_ortho ? plan : nullptr, stream);
+        }
+    } else {
+        e = launch_general(a, stream);
+    }
+    if (e != hipSuccess) return fail_hip(e, "kernel launch");
+    t_last_kernel = kernel;
+    return ORTH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void orth_layer_hip_set_alpha(orth_hip_layer_t *layer, float alpha) {
+    if (layer) layer->alpha = alpha;
+}
+
+int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void *output,
+                         int64_t batch_size, int32_t io_dtype) {
+    ForwardArgs a;
+    return resolve(layer, input, output, batch_size, io_dtype, true, a);
+}
+
+int orth_layer_forward_hip(const orth_hip_layer_t *layer, const void *input, void *output,
+                           int64_t batch_size, int32_t io_dtype, void *stream) {
+    return forward_impl(layer, nullptr, 0, input, output, batch_size, io_dtype, stream);
+}
+
+int orth_layer_forward_hip_planned(const orth_hip_layer_t *layer, const void *plan,
+                                   int64_t plan_bytes, const void *input, void *output,
+                                   int64_t batch_size, int32_t io_dtype, void *stream) {
+    return forward_impl(layer, plan, plan_bytes, input, output, batch_size, io_dtype, stream);
+}
+
+int64_t orth_ortho_plan_bytes(const orth_hip_layer_t *layer) {
+    ForwardArgs a;
+    int rc = resolve(layer, nullptr, nullptr, 0, ORTH_DT_F16, false, a);
+    if (rc != ORTH_OK) return -rc;
+    if (a.nnz > 0 && !plan_supported(a))
+        return -(int64_t)fail(ORTH_ERR_UNSUPPORTED,
+                              "no ortho plan for in_features %lld (needs a multiple of 64, at most 12288)",
+                              (long long)a.K);
+    return plan_bytes_for(a.N, a.K, a.nnz);
+}
+
+int orth_ortho_plan_build(const orth_hip_layer_t *layer, void *plan, int64_t plan_bytes,
+                          void *stream_v) {
+    ForwardArgs a;
+    int rc = resolve(layer, nullptr, nullptr, 0, ORTH_DT_F16, false, a);
+    if (rc != ORTH_OK) return rc;
+    if (a.nnz == 0) return ORTH_OK;
+    if (!plan_supported(a))
+        return fail(ORTH_ERR_UNSUPPORTED, "no ortho plan for in_features %lld", (long long)a.K);
+    if (!plan) return fail(ORTH_ERR_INVALID_ARGUMENT, "plan is NULL");
+    if (plan_bytes < plan_bytes_for(a.N, a.K, a.nnz))
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "plan_bytes %lld is smaller than the plan size %lld",
+                    (long long)plan_bytes, (long long)plan_bytes_for(a.N, a.K, a.nnz));
+    rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipStream_t stream = static_cast<hipStream_t>(stream_v);
+    hipError_t e = launch_plan_build(a, plan, stream);
+    if (e != hipSuccess) return fail_hip(e, "plan build launch");
+    uint32_t flags = 0;
+    e = plan_read_flags(plan, stream, &flags);
+    if (e != hipSuccess) return fail_hip(e, "plan build");
+    if (flags & 2u)
+        return fail(ORTH_ERR_INVALID_ARGUMENT,
+                    "ortho.row_ptr is not monotone within [0, count] (malformed CSR)");
+    return ORTH_OK;
+}
+
+int orth_base_dequant_hip(const orth_hip_layer_t *layer, float *out, void *stream) {
+    ForwardArgs a;
+    int rc = resolve(layer, nullptr, nullptr, 0, ORTH_DT_F16, false, a);
+    if (rc != ORTH_OK) return rc;
+    if (!out) return fail(ORTH_ERR_INVALID_ARGUMENT, "out is NULL");
+    rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipError_t e = launch_dequant(a, out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "dequant launch");
+    return ORTH_OK;
+}
+
+int orth_hip_device_info(int device, orth_hip_device_info_t *info) {
+    if (!info) return fail(ORTH_ERR_INVALID_ARGUMENT, "info is NULL");
+    std::memset(info, 0, sizeof(*info));
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) return fail(ORTH_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= count)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "device %d out of range (count %d)", device, count);
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, device);
+    if (e != hipSuccess) return fail_hip(e, "hipGetDeviceProperties");
+    std::snprintf(info->arch, sizeof(info->arch), "%s", p.gcnArchName);
+    info->is_gfx950 = std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+    info->compute_units = p.multiProcessorCount;
+    info->wavefront_size = p.warpSize;
+    info->lds_bytes_per_block = (int32_t)p.sharedMemPerBlock;
+    info->clock_khz = p.clockRate;
+    info->memory_clock_khz = p.memoryClockRate;
+    info->memory_bus_width = p.memoryBusWidth;
+    info->l2_bytes = p.l2CacheSize;
+    info->global_mem_bytes = (int64_t)p.totalGlobalMem;
+    return ORTH_OK;
+}
+
+int orth_hip_set_kernel_policy(int policy) {
+    if (policy < 0 || policy > 3) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..3");
+    g_policy.store(policy);
+    return ORTH_OK;
+}
+
+int orth_hip_get_kernel_policy(void) { return g_policy.load(); }
+
+int orth_hip_last_kernel(void) { return t_last_kernel; }
+
+const char *orth_hip_last_error(void) { return t_error.c_str(); }
+
+int orth_hip_abi_version(void) { return 100; }
+
+}  // extern "C"

@@ -1,0 +1,173 @@
+// Device-side building blocks shared by the gfx950 dual-GEMM kernels.
+//
+// Packed Base layout (the API layout, /root/reference/src/ortho.c:315-325 and
+// /root/reference/torch_bind/ortho_linear.py:107-120): element (n, k) of the
+// [N, K] INT4 matrix is nibble n*K+k, stored in byte (n*K+k)/2, low nibble for
+// even k, two's complement.  One 32-bit word therefore holds 8 consecutive k
+// of one row: nibble i of the word (bits 4i..4i+3) is k0+i.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "orth_hip.h"
+
+namespace orth {
+
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Which kernel served a forward call (orth_hip_last_kernel()).
+enum KernelId { KERNEL_NONE = 0, KERNEL_DECODE = 1, KERNEL_PREFILL = 2, KERNEL_GENERAL = 3 };
+
+// Everything a forward launch needs, resolved on the host.
+struct ForwardArgs {
+    const uint8_t *q;        // [N, K/2]
+    const void *scales;      // [N, ngroups]
+    int scale_dtype;
+    int64_t ngroups;
+    int64_t G;               // K / ngroups
+    const int32_t *row_ptr;  // [N+1]
+    const int32_t *col;      // [nnz]
+    const void *vals;        // [nnz]
+    int val_dtype;
+    int64_t nnz;
+    const void *x;           // [M, K]
+    void *y;                 // [M, N]
+    int io_dtype;
+    int64_t M, K, N;
+    float alpha;
+    int has_ortho;           // alpha > 0 && nnz > 0 (/root/reference/src/ortho.c:343)
+};
+
+// ---------------------------------------------------------------- scalars
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    // round to nearest even; NaN stays NaN
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Load element i of a buffer of the given orth_dtype_t as float.
+__device__ __forceinline__ float load_as_f32(const void *p, int dtype, int64_t i) {
+    if (dtype == ORTH_DT_F16) return (float)((const f16 *)p)[i];
+    if (dtype == ORTH_DT_BF16) return bf16_bits_to_f32(((const uint16_t *)p)[i]);
+    return ((const float *)p)[i];
+}
+
+__device__ __forceinline__ void store_from_f32(void *p, int dtype, int64_t i, float v) {
+    if (dtype == ORTH_DT_F16) ((f16 *)p)[i] = (f16)v;
+    else if (dtype == ORTH_DT_BF16) ((uint16_t *)p)[i] = f32_to_bf16_bits(v);
+    else ((float *)p)[i] = v;
+}
+
+// Sign-extend a 4-bit two's complement nibble.
+__device__ __forceinline__ int sext4(uint32_t nib) { return (int)(nib ^ 8u) - 8; }
+
+// CSR row range [rs, re), clamped into [0, nnz] so a malformed row_ptr can
+// never address outside the index arrays.
+__device__ __forceinline__ void csr_row_range(const int32_t *row_ptr, int64_t n, int64_t nnz,
+                                              int32_t &rs, int32_t &re) {
+    int64_t a = row_ptr[n], b = row_ptr[n + 1];
+    a = a < 0 ? 0 : (a > nnz ? nnz : a);
+    b = b < a ? a : (b > nnz ? nnz : b);
+    rs = (int32_t)a;
+    re = (int32_t)b;
+}
+
+// ------------------------------------------------------ INT4 -> FP16 words
+//
+// Magic-number conversion: OR-ing a 4-bit value u into the low mantissa bits
+// of binary16 1024.0 (0x6400) gives exactly 1024 + u; OR-ing it into bits
+// 4..7 gives 1024 + 16u.  After flipping bit 3 of every nibble (u = q + 8)
+// a packed-half subtract or fused multiply-add recovers q exactly.
+
+// "Interleaved" order: from one packed word produce four f16x2 words holding
+// k-pairs (0,4) (1,5) (2,6) (3,7).  Six integer ops + four packed-half ops
+// for 8 weights; the matching activation operand must use the same order
+// (see permute_x8).
+__device__ __forceinline__ void int4x8_to_f16_interleaved(uint32_t w, uint32_t out[4]) {
+    const uint32_t wf = w ^ 0x88888888u;
+    const uint32_t t = wf >> 8;
+    uint32_t p0 = (wf & 0x000F000Fu) | 0x64006400u;  // 1024+u0 | 1024+u4
+    uint32_t p1 = (wf & 0x00F000F0u) | 0x64006400u;  // 1024+16u1 | 1024+16u5
+    uint32_t p2 = (t & 0x000F000Fu) | 0x64006400u;   // 1024+u2 | 1024+u6
+    uint32_t p3 = (t & 0x00F000F0u) | 0x64006400u;   // 1024+16u3 | 1024+16u7
+    const f16x2 bias = {(f16)-1032.0f, (f16)-1032.0f};
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const f16x2 bias16 = {(f16)-72.0f, (f16)-72.0f};
+    f16x2 h0 = __builtin_bit_cast(f16x2, p0) + bias;                          // exact
+    f16x2 h1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p1), sixteenth, bias16);
+    f16x2 h2 = __builtin_bit_cast(f16x2, p2) + bias;
+    f16x2 h3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p3), sixteenth, bias16);
+    out[0] = __builtin_bit_cast(uint32_t, h0);
+    out[1] = __builtin_bit_cast(uint32_t, h1);
+    out[2] = __builtin_bit_cast(uint32_t, h2);
+    out[3] = __builtin_bit_cast(uint32_t, h3);
+}
+
+// Reorder 8 consecutive fp16 (as 4 words (0,1)(2,3)(4,5)(6,7)) into the
+// interleaved order (0,4)(1,5)(2,6)(3,7) used by int4x8_to_f16_interleaved.
+__device__ __forceinline__ u32x4 permute_x8(u32x4 d) {
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);  // lo halves of d0, d2
+    r.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);  // hi halves of d0, d2
+    r.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
+    r.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+    return r;
+}
+
+// Position of element r (0..7) of an 8-chunk in the interleaved order.
+__device__ __forceinline__ int interleaved_pos(int r) { return ((r & 3) << 1) | (r >> 2); }
+
+// "Natural" order: four f16x2 words holding k-pairs (0,1) (2,3) (4,5) (6,7),
+// each weight multiplied by the fp16 scale s (one rounding of the exact
+// product q*s).  Used where the activation tile is copied untouched.
+// Each 16-bit half of the packed word is duplicated into both halves of a
+// word (v_perm), then a per-half shift (v_pk_lshrrev_b16) moves nibble j
+// into bits 0..3 of the low half and nibble j+1 into bits 0..3 of the high.
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void int4x8_to_f16_scaled(uint32_t w, f16x2 s2, uint32_t out[4]) {
+    const uint32_t wf = w ^ 0x88888888u;
+    const u16x2 lo = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(wf, wf, 0x01000100u));
+    const u16x2 hi = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(wf, wf, 0x03020302u));
+    const u16x2 sh01 = {0, 4}, sh23 = {8, 12};
+    const uint32_t p0 = (__builtin_bit_cast(uint32_t, lo >> sh01) & 0x000F000Fu) | 0x64006400u;
+    const uint32_t p1 = (__builtin_bit_cast(uint32_t, lo >> sh23) & 0x000F000Fu) | 0x64006400u;
+    const uint32_t p2 = (__builtin_bit_cast(uint32_t, hi >> sh01) & 0x000F000Fu) | 0x64006400u;
+    const uint32_t p3 = (__builtin_bit_cast(uint32_t, hi >> sh23) & 0x000F000Fu) | 0x64006400u;
+    const f16x2 bias = {(f16)-1032.0f, (f16)-1032.0f};
+    out[0] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p0) + bias) * s2);
+    out[1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p1) + bias) * s2);
+    out[2] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p2) + bias) * s2);
+    out[3] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p3) + bias) * s2);
+}
+
+// ------------------------------------------------------------ reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace orth

@@ -1,0 +1,461 @@
+// Prefill dual GEMM (batch M > 16) for gfx950, and the ortho plan builder.
+//
+// Design intent of /root/reference/src/dual_gemm_tensor_core.cu:215-337
+// (matrix-core base GEMM with the ortho term fused), built for CDNA4:
+//
+//  * Workgroup tile 256 tokens x 128 output rows, 4 waves in a 2x2 grid,
+//    each wave 128x64 with v_mfma_f32_32x32x16_f16 (FP32 accumulation).
+//    K advances in steps of 64 through double-buffered LDS tiles.
+//  * The activation tile is copied to LDS as is.  The INT4 weight tile is
+//    dequantised on the way in: each thread turns one 16-byte load (32
+//    nibbles of one row) into 32 FP16 weights q*s (one rounding of the exact
+//    product) and writes them to LDS.
+//  * The sparse ortho term is folded into that LDS weight tile before the
+//    MFMAs read it: the plan (a derived layout of the CSR, built once at load
+//    time) lists, per (128-row block, 64-column step), the entries that fall
+//    inside the tile, so each entry costs one LDS read-modify-write per 256
+//    tokens instead of a gather per token.  alpha <= 0 skips the fold on a
+//    uniform branch and never reads the plan.
+//  * The weight operand therefore is fp16(fp16(q*s) + alpha*v): within
+//    2^-11 relative of the exact weight, far inside the 1e-2*|y|_inf bound.
+//    (The decode kernel keeps q exact and scales FP32 partial sums; the
+//    dequant entry point gives the bit-exact FP32 weights.)
+//  * Tiles are mapped XCD-aware: consecutive workgroup ids land on different
+//    XCDs, so the tile order is remapped to give each XCD a contiguous run.
+#include "orth_common.h"
+
+namespace orth {
+
+// ----------------------------------------------------------------- plan
+//
+// Layout (all little-endian):
+//   PlanHeader (64 bytes)
+//   int32 offsets[nblocks][nksteps + 1]   absolute entry index per (block, step)
+//   uint32 entries[nnz]                   (row_in_block << 24) | (col_in_step << 16) | fp16 bits
+// Entries of one (block, step) are ordered by row then by CSR position.
+
+static const uint32_t kPlanMagic = 0x504f5254u;  // "TROP"
+static const uint32_t kPlanVersion = 1;
+static const int kPlanBN = 128;
+static const int kPlanBK = 64;
+static const uint32_t kPlanNonCanonical = 1u;  // duplicate or unsorted columns in a row
+static const uint32_t kPlanMalformed = 2u;     // row_ptr not monotone within [0, nnz]
+
+struct PlanHeader {
+    uint32_t magic, version;
+    int32_t bn, bk, nblocks, nksteps;
+    int64_t n, k, nnz;
+    uint32_t flags;
+    uint32_t pad[3];
+};
+static_assert(sizeof(PlanHeader) == 64, "plan header must be 64 bytes");
+
+int64_t plan_offsets_bytes(int64_t N, int64_t K) {
+    const int64_t nblocks = (N + kPlanBN - 1) / kPlanBN;
+    const int64_t nk = K / kPlanBK;
+    return ((nblocks * (nk + 1) * 4) + 15) & ~int64_t(15);
+}
+
+int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) {
+    if (nnz <= 0) return 0;
+    return (int64_t)sizeof(PlanHeader) + plan_offsets_bytes(N, K) + 4 * nnz;
+}
+
+// Largest K the plan builder's LDS counters take (int32 per (step, row)).
+static const int64_t kPlanMaxK = 12288;
+
+bool plan_supported(const ForwardArgs &a) {
+    return a.K % kPlanBK == 0 && a.K <= kPlanMaxK && a.nnz < ((int64_t)1 << 31);
+}
+
+__global__ void plan_init_kernel(PlanHeader *h, int nblocks, int nksteps, int64_t N, int64_t K,
+                                 int64_t nnz) {
+    if (threadIdx.x == 0) {
+        h->magic = kPlanMagic;
+        h->version = kPlanVersion;
+        h->bn = kPlanBN;
+        h->bk = kPlanBK;
+        h->nblocks = nblocks;
+        h->nksteps = nksteps;
+        h->n = N;
+        h->k = K;
+        h->nnz = nnz;
+        h->flags = 0;
+        for (int i = 0; i < 3; i++) h->pad[i] = 0;
+    }
+}
+
+__device__ __forceinline__ uint32_t value_bits_f16(const void *vals, int dtype, int64_t j) {
+    if (dtype == ORTH_DT_F16) return ((const uint16_t *)vals)[j];
+    const float v = load_as_f32(vals, dtype, j);
+    return __builtin_bit_cast(uint16_t, (f16)v);
+}
+
+// One workgroup per block of kPlanBN output rows.  Counting sort of the
+// block's CSR entries by 64-column step, stable in (row, CSR position).
+__global__ void __launch_bounds__(256) plan_build_kernel(ForwardArgs a, PlanHeader *h,
+                                                         int32_t *offsets, uint32_t *entries,
+                                                         int nksteps) {
+    extern __shared__ __align__(16) int32_t cnt[];  // [nksteps][BN], then partials[256]
+    int32_t *partials = cnt + nksteps * kPlanBN;
+    __shared__ int32_t s_flags;
+    __shared__ int32_t s_total;
+    const int tid = threadIdx.x;
+    const int64_t b = blockIdx.x;
+    const int L = nksteps * kPlanBN;
+    for (int i = tid; i < L; i += 256) cnt[i] = 0;
+    if (tid == 0) s_flags = 0;
+    __syncthreads();
+
+    const int r = tid;
+    const int64_t n = b * kPlanBN + r;
+    int32_t rs = 0, re = 0;
+    uint32_t myflags = 0;
+    if (r < kPlanBN && n < a.N) {
+        const int64_t ra = a.row_ptr[n], rb = a.row_ptr[n + 1];
+        if (ra < 0 || rb < ra || rb > a.nnz) myflags |= kPlanMalformed;
+        csr_row_range(a.row_ptr, n, a.nnz, rs, re);
+        int32_t prev = -1;
+        for (int32_t j = rs; j < re; j++) {
+            const int32_t c = a.col[j];
+            if (c >= 0 && c < a.K) {
+                cnt[(c / kPlanBK) * kPlanBN + r] += 1;
+                if (c <= prev) myflags |= kPlanNonCanonical;
+                prev = c;
+            }
+        }
+    }
+    if (myflags) atomicOr(&s_flags, (int32_t)myflags);
+    __syncthreads();
+
+    // exclusive scan of cnt in (step, row) order: per-thread segments
+    const int seg = (L + 255) / 256;
+    const int lo = tid * seg, hi = min(L, lo + seg);
+    int32_t local = 0;
+    for (int i = lo; i < hi; i++) local += cnt[i];
+    partials[tid] = local;
+    __syncthreads();
+    if (tid == 0) {
+        int32_t run = 0;
+        for (int i = 0; i < 256; i++) {
+            const int32_t v = partials[i];
+            partials[i] = run;
+            run += v;
+        }
+        s_total = run;
+    }
+    __syncthreads();
+    int32_t run = partials[tid];
+    for (int i = lo; i < hi; i++) {
+        const int32_t v = cnt[i];
+        cnt[i] = run;
+        run += v;
+    }
+    __syncthreads();
+
+    // the block's entries occupy [base, base + total) of the CSR index space
+    const int64_t nfirst = b * kPlanBN;
+    const int64_t nlast = min((int64_t)a.N, nfirst + kPlanBN);
+    int64_t base = a.row_ptr[nfirst], end = a.row_ptr[nlast];
+    base = base < 0 ? 0 : (base > a.nnz ? a.nnz : base);
+    end = end < base ? base : (end > a.nnz ? a.nnz : end);
+    const int64_t total = s_total;
+    const bool fits = base + total <= end;
+    int32_t *off = offsets + b * (nksteps + 1);
+    for (int kt = tid; kt <= nksteps; kt += 256) {
+        int64_t o = kt < nksteps ? cnt[kt * kPlanBN] : total;
+        off[kt] = (int32_t)(base + (fits ? o : 0));
+    }
+    __syncthreads();  // the placement below advances the same counters
+    if (fits && r < kPlanBN && n < a.N) {
+        for (int32_t j = rs; j < re; j++) {
+            const int32_t c = a.col[j];
+            if (c >= 0 && c < a.K) {
+                const int kt = c / kPlanBK;
+                const int32_t pos = cnt[kt * kPlanBN + r]++;
+                entries[base + pos] = ((uint32_t)r << 24) | ((uint32_t)(c - kt * kPlanBK) << 16) |
+                                      value_bits_f16(a.vals, a.val_dtype, j);
+            }
+        }
+    }
+    if (tid == 0) {
+        uint32_t f = (uint32_t)s_flags | (fits ? 0u : kPlanMalformed);
+        if (f) atomicOr(&h->flags, f);
+    }
+}
+
+hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t stream) {
+    const int nblocks = (int)((a.N + kPlanBN - 1) / kPlanBN);
+    const int nksteps = (int)(a.K / kPlanBK);
+    PlanHeader *h = static_cast<PlanHeader *>(plan);
+    int32_t *offsets = reinterpret_cast<int32_t *>(static_cast<char *>(plan) + sizeof(PlanHeader));
+    uint32_t *entries = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(offsets) +
+                                                     plan_offsets_bytes(a.N, a.K));
+    hipLaunchKernelGGL(plan_init_kernel, dim3(1), dim3(64), 0, stream, h, nblocks, nksteps, a.N,
+                       a.K, a.nnz);
+    const size_t lds = ((size_t)nksteps * kPlanBN + 256) * sizeof(int32_t);
+    hipLaunchKernelGGL(plan_build_kernel, dim3(nblocks), dim3(256), lds, stream, a, h, offsets,
+                       entries, nksteps);
+    return hipGetLastError();
+}
+
+// Reads the flags word of a built plan (host side, synchronous).
+hipError_t plan_read_flags(const void *plan, hipStream_t stream, uint32_t *flags) {
+    hipError_t e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return e;
+    PlanHeader h;
+    e = hipMemcpy(&h, plan, sizeof(h), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return e;
+    *flags = h.flags;
+    return hipSuccess;
+}
+
+// --------------------------------------------------------------- kernel
+
+struct PrefillArgs {
+    const uint8_t *q;
+    const f16 *scales;
+    int64_t ngroups, G;
+    const f16 *x;
+    f16 *y;
+    int64_t M, K, N;
+    float alpha;
+    int32_t nnz;
+    int fold;                 // apply the ortho plan
+    const PlanHeader *plan;
+    const int32_t *offsets;   // [nblocks][nksteps+1]
+    const uint32_t *entries;
+    int nbm, nbn;             // tile grid
+};
+
+constexpr int PF_BM = 256, PF_BN = 128, PF_BK = 64;
+constexpr int PF_LDK = PF_BK + 8;  // LDS row stride in halves (+16 bytes)
+constexpr int PF_A_BYTES = PF_BM * PF_LDK * 2;
+constexpr int PF_B_BYTES = PF_BN * PF_LDK * 2;
+constexpr int PF_LDS_BYTES = 2 * (PF_A_BYTES + PF_B_BYTES);
+static_assert(PF_BN == kPlanBN && PF_BK == kPlanBK, "plan tiling must match the kernel");
+
+// Registers holding one K-step's global loads for one thread.
+struct StepRegs {
+    u32x4 a[8];       // 8 x 16 bytes of activations
+    u32x4 b;          // 32 nibbles of one weight row
+    f16 s;            // that row's scale for this step
+    uint32_t e0;      // first plan entry of this thread (if any)
+    int32_t ebeg, eend;
+};
+
+__device__ __forceinline__ void prefill_load(const PrefillArgs &a, int t, int64_t m0, int64_t n0,
+                                             const int32_t *off_row, StepRegs &r) {
+    const int tid = threadIdx.x;
+    const int64_t k0 = (int64_t)t * PF_BK;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int idx = tid + 256 * i;
+        int64_t m = m0 + (idx >> 3);
+        m = m < a.M ? m : a.M - 1;
+        r.a[i] = *reinterpret_cast<const u32x4 *>(a.x + m * a.K + k0 + (idx & 7) * 8);
+    }
+    int64_t n = n0 + (tid >> 1);
+    n = n < a.N ? n : a.N - 1;
+    r.b = *reinterpret_cast<const u32x4 *>(a.q + n * (a.K >> 1) + (k0 >> 1) + (tid & 1) * 16);
+    r.s = a.scales[n * a.ngroups + k0 / a.G];
+    if (a.fold) {
+        // clamped: a stale or foreign plan can lose the ortho term but never
+        // read outside the entry array
+        r.ebeg = min(max(off_row[t], 0), a.nnz);
+        r.eend = min(max(off_row[t + 1], r.ebeg), a.nnz);
+        const int32_t e = r.ebeg + tid;
+        r.e0 = e < r.eend ? a.entries[e] : 0u;
+    }
+}
+
+__device__ __forceinline__ void prefill_store(const StepRegs &r, f16 *As, f16 *Bs) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int idx = tid + 256 * i;
+        *reinterpret_cast<u32x4 *>(As + (idx >> 3) * PF_LDK + (idx & 7) * 8) = r.a[i];
+    }
+    const f16x2 s2 = {r.s, r.s};
+    const uint32_t words[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    f16 *dst = Bs + (tid >> 1) * PF_LDK + (tid & 1) * 32;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        uint32_t o[4];
+        int4x8_to_f16_scaled(words[j], s2, o);
+        *reinterpret_cast<u32x4 *>(dst + 8 * j) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+}
+
+__device__ __forceinline__ void fold_one(f16 *Bs, uint32_t e, float alpha, bool canonical) {
+    const int r = (e >> 24) & (PF_BN - 1), c = (e >> 16) & (PF_BK - 1);  // always inside the tile
+    const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
+    f16 *p = Bs + r * PF_LDK + c;
+    if (canonical) {
+        *p = (f16)((float)*p + alpha * v);
+    } else {
+        // duplicate (row, col) entries may share a cell: CAS on its 32-bit word
+        uint32_t *w = reinterpret_cast<uint32_t *>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+        const int sh = (reinterpret_cast<uintptr_t>(p) & 2) ? 16 : 0;
+        uint32_t old = *w, assumed;
+        do {
+            assumed = old;
+            const f16 cur = __builtin_bit_cast(f16, (uint16_t)(assumed >> sh));
+            const uint16_t nv = __builtin_bit_cast(uint16_t, (f16)((float)cur + alpha * v));
+            const uint32_t upd = (assumed & ~(0xffffu << sh)) | ((uint32_t)nv << sh);
+            old = atomicCAS(w, assumed, upd);
+        } while (old != assumed);
+    }
+}
+
+__device__ __forceinline__ void prefill_fold(const PrefillArgs &a, const StepRegs &r, f16 *Bs,
+                                             bool canonical) {
+    const int tid = threadIdx.x;
+    if (r.ebeg + tid < r.eend) fold_one(Bs, r.e0, a.alpha, canonical);
+    for (int32_t e = r.ebeg + tid + 256; e < r.eend; e += 256) fold_one(Bs, a.entries[e], a.alpha, canonical);
+}
+
+__device__ __forceinline__ void prefill_mfma(const f16 *As, const f16 *Bs, int wm, int wn,
+                                             f32x16 (&acc)[4][2]) {
+    const int lane = threadIdx.x & 63;
+    const int lr = lane & 31, lk = (lane >> 5) * 8;
+#pragma unroll
+    for (int s = 0; s < PF_BK / 16; s++) {
+        f16x8 af[4], bf[2];
+#pragma unroll
+        for (int bm = 0; bm < 4; bm++)
+            af[bm] = *reinterpret_cast<const f16x8 *>(As + (wm * 128 + bm * 32 + lr) * PF_LDK + s * 16 + lk);
+#pragma unroll
+        for (int bn = 0; bn < 2; bn++)
+            bf[bn] = *reinterpret_cast<const f16x8 *>(Bs + (wn * 64 + bn * 32 + lr) * PF_LDK + s * 16 + lk);
+#pragma unroll
+        for (int bm = 0; bm < 4; bm++)
+#pragma unroll
+            for (int bn = 0; bn < 2; bn++)
+                acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[bm], bf[bn], acc[bm][bn], 0, 0, 0);
+    }
+}
+
+__global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    // buffer i of the activation / weight tiles
+    auto As = [&](int i) { return reinterpret_cast<f16 *>(smem + i * PF_A_BYTES); };
+    auto Bs = [&](int i) { return reinterpret_cast<f16 *>(smem + 2 * PF_A_BYTES + i * PF_B_BYTES); };
+
+    // XCD-aware tile order: workgroup ids are dealt round-robin to the 8
+    // XCDs; give each XCD a contiguous run of tiles (N-block fastest).
+    const int ntiles = a.nbm * a.nbn;
+    int tile = blockIdx.x;
+    if ((ntiles & 7) == 0) tile = (blockIdx.x & 7) * (ntiles >> 3) + (blockIdx.x >> 3);
+    const int bm_i = tile / a.nbn, bn_i = tile - bm_i * a.nbn;
+    const int64_t m0 = (int64_t)bm_i * PF_BM, n0 = (int64_t)bn_i * PF_BN;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nk = (int)(a.K / PF_BK);
+    const int32_t *off_row = a.fold ? a.offsets + (int64_t)bn_i * (nk + 1) : nullptr;
+    if (a.fold) {
+        // a plan built for another layer shape is ignored rather than trusted
+        const PlanHeader *h = a.plan;
+        if (h->magic != kPlanMagic || h->version != kPlanVersion || h->n != a.N || h->k != a.K ||
+            h->nnz != a.nnz)
+            a.fold = 0;
+    }
+    const bool canonical = !a.fold || (a.plan->flags & kPlanNonCanonical) == 0;
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int bm = 0; bm < 4; bm++)
+#pragma unroll
+        for (int bn = 0; bn < 2; bn++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[bm][bn][i] = 0.f;
+
+    StepRegs r;
+    prefill_load(a, 0, m0, n0, off_row, r);
+    prefill_store(r, As(0), Bs(0));
+    __syncthreads();
+    if (a.fold) prefill_fold(a, r, Bs(0), canonical);
+    __syncthreads();
+
+    for (int t = 0; t < nk; t++) {
+        const int cb = t & 1, nb = cb ^ 1;
+        const bool more = t + 1 < nk;
+        if (more) prefill_load(a, t + 1, m0, n0, off_row, r);
+        prefill_mfma(As(cb), Bs(cb), wm, wn, acc);
+        if (more) prefill_store(r, As(nb), Bs(nb));
+        __syncthreads();
+        if (more && a.fold) prefill_fold(a, r, Bs(nb), canonical);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds D[token 8(i/4) + 4(lane/32) + i%4][row lane%32]
+#pragma unroll
+    for (int bm = 0; bm < 4; bm++) {
+#pragma unroll
+        for (int bn = 0; bn < 2; bn++) {
+            const int64_t n = n0 + wn * 64 + bn * 32 + (lane & 31);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int64_t m = m0 + wm * 128 + bm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                if (m < a.M && n < a.N) a.y[m * a.N + n] = (f16)acc[bm][bn][i];
+            }
+        }
+    }
+}
+
+bool prefill_supported(const ForwardArgs &a) {
+    if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
+    if (a.K % PF_BK != 0) return false;
+    if (a.ngroups != 1 && a.G % PF_BK != 0) return false;
+    if (a.has_ortho && !plan_supported(a)) return false;
+    if ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.x)) & 15) return false;
+    const int64_t nbm = (a.M + PF_BM - 1) / PF_BM, nbn = (a.N + PF_BN - 1) / PF_BN;
+    if (nbm * nbn > ((int64_t)1 << 31) - 1) return false;
+    return true;
+}
+
+hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream) {
+    PrefillArgs p;
+    p.q = a.q;
+    p.scales = static_cast<const f16 *>(a.scales);
+    p.ngroups = a.ngroups;
+    p.G = a.G;
+    p.x = static_cast<const f16 *>(a.x);
+    p.y = static_cast<f16 *>(a.y);
+    p.M = a.M;
+    p.K = a.K;
+    p.N = a.N;
+    p.alpha = a.alpha;
+    p.nnz = (int32_t)a.nnz;
+    p.fold = a.has_ortho && plan != nullptr;
+    p.plan = static_cast<const PlanHeader *>(plan);
+    p.offsets = plan ? reinterpret_cast<const int32_t *>(static_cast<const char *>(plan) + sizeof(PlanHeader))
+                     : nullptr;
+    p.entries = plan ? reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(p.offsets) +
+                                                          plan_offsets_bytes(a.N, a.K))
+                     : nullptr;
+    p.nbm = (int)((a.M + PF_BM - 1) / PF_BM);
+    p.nbn = (int)((a.N + PF_BN - 1) / PF_BN);
+    const unsigned blocks = (unsigned)(p.nbm * p.nbn);
+    hipLaunchKernelGGL(prefill_kernel, dim3(blocks), dim3(256), PF_LDS_BYTES, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace orth
+
+namespace orth {
+
+// Kernels that use more than 64 KB of dynamic LDS must say so per device.
+hipError_t prefill_prepare_device() {
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(prefill_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS_BYTES);
+}
+
+hipError_t plan_prepare_device() {
+    const int bytes = (int)(((kPlanMaxK / kPlanBK) * kPlanBN + 256) * sizeof(int32_t));
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(plan_build_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
+}  // namespace orth

@@ -1,0 +1,5 @@
+"""PyTorch bindings (the reference's ``torch_bind`` package,
+/root/reference/torch_bind/__init__.py)."""
+from .ortho_linear import OrthoLinear
+
+__all__ = ["OrthoLinear"]

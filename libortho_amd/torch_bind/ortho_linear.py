@@ -1,0 +1,165 @@
+"""OrthoLinear: the dual-manifold linear layer, on MI355X.
+
+API-compatible with /root/reference/torch_bind/ortho_linear.py:30-168:
+
+  OrthoLinear(in_features, out_features, q_bits=4, bias=False, device=None, dtype=None)
+  .set_alpha(alpha)                                   the privacy kill switch
+  .load_from_weights(base_weight, ortho_weight, base_scales=None)
+  .forward(x)                                         y = Base(x) + alpha*Ortho(x) (+ bias)
+
+with the same buffers, names, dtypes and shapes, so a reference
+``state_dict`` loads unchanged:
+
+  base_weight        uint8  [out, in/2]  packed signed INT4, low nibble = even k
+  base_scales        fp16   [out]        (or [out, in/G] with the group extension)
+  ortho_values       fp16   [nnz]
+  ortho_col_indices  int32  [nnz]
+  ortho_row_ptr      int32  [out+1]      (empty until weights are loaded)
+
+Differences, all deliberate:
+  * ``group_size`` (keyword, default None = per-row scales as in the
+    reference) selects FP16 scales per group of G input columns.
+  * ``device`` is honoured for the buffers (the reference ignores it).
+  * ``forward`` on a CPU tensor raises instead of returning uninitialised
+    memory (the reference's CPU branch is ``pass``, :152-162); there is no
+    CPU path in this library.
+  * The prefill kernel's ortho plan (a derived layout of the CSR buffers) is
+    built on first use and cached; it is rebuilt whenever one of the three
+    CSR buffers is replaced or modified in place.  It is not a buffer and is
+    not saved in the state_dict.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from .. import _C_ops as _C
+from ..tools.sieve import pack_ortho_sparse
+
+HAS_C_OPS = True  # the reference's flag (:15-28); this package has no fallback
+
+# Below this many tokens the decode kernel serves the call and needs no plan.
+_PLAN_MIN_TOKENS = 17
+
+
+class OrthoLinear(nn.Module):
+    """Y = X @ W_base^T + alpha * (X @ W_ortho^T) (+ bias)."""
+
+    def __init__(self, in_features: int, out_features: int, q_bits: int = 4, bias: bool = False,
+                 device=None, dtype=None, group_size: Optional[int] = None):
+        super().__init__()
+        if q_bits != 4:
+            raise ValueError("OrthoLinear supports q_bits=4 only")
+        if in_features % 2 != 0:
+            raise ValueError("in_features must be even (two INT4 weights per byte)")
+        if group_size is not None and (group_size <= 0 or in_features % group_size != 0):
+            raise ValueError(f"group_size {group_size} must divide in_features {in_features}")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.q_bits = q_bits
+        self.group_size = group_size
+        scale_shape = (out_features,) if group_size is None else (out_features, in_features // group_size)
+        self.register_buffer("base_weight", torch.zeros(out_features, in_features // 2,
+                                                        dtype=torch.uint8, device=device))
+        self.register_buffer("base_scales", torch.zeros(scale_shape, dtype=torch.float16, device=device))
+        self.register_buffer("ortho_values", torch.tensor([], dtype=torch.float16, device=device))
+        self.register_buffer("ortho_col_indices", torch.tensor([], dtype=torch.int32, device=device))
+        self.register_buffer("ortho_row_ptr", torch.tensor([], dtype=torch.int32, device=device))
+        self.alpha = 1.0
+        if bias:
+            self.register_parameter("bias", nn.Parameter(
+                torch.zeros(out_features, dtype=dtype or torch.float32, device=device)))
+        else:
+            self.register_parameter("bias", None)
+        self._plan = None
+        self._plan_key = None
+
+    def set_alpha(self, alpha: float):
+        """The kill switch: the ortho term is applied iff alpha > 0."""
+        self.alpha = alpha
+
+    @torch.no_grad()
+    def load_from_weights(self, base_weight: torch.Tensor, ortho_weight: torch.Tensor,
+                          base_scales: Optional[torch.Tensor] = None):
+        """Quantise ``base_weight`` to INT4 and pack ``ortho_weight`` as CSR.
+
+        Follows /root/reference/torch_bind/ortho_linear.py:79-128: scales =
+        clamp(max|W| / 7, min=1e-6) per output row unless given; the FP16
+        copy is stored, but q = clamp(round(W / scales), -8, 7) uses the
+        scales as given; nibble pairs packed low = even index.  With
+        ``group_size`` the max is taken per group and ``base_scales`` may be
+        given as [out, in/G].
+        """
+        device = ortho_weight.device
+        N, K = self.out_features, self.in_features
+        if tuple(base_weight.shape) != (N, K) or tuple(ortho_weight.shape) != (N, K):
+            raise ValueError(f"weights must be [{N}, {K}]")
+        G = K if self.group_size is None else self.group_size
+        if base_scales is None:
+            grouped = base_weight.reshape(N, K // G, G)
+            scales = (grouped.abs().amax(dim=2) / 7.0).clamp(min=1e-6)
+            if self.group_size is None:
+                scales = scales.reshape(N)
+        else:
+            scales = base_scales
+        self.base_scales.data = scales.to(dtype=torch.float16, device=device)
+        s_full = scales.reshape(N, -1).to(base_weight.device)
+        s_full = s_full.repeat_interleave(K // s_full.shape[1], dim=1)
+        w_int = (base_weight / s_full).round().clamp(-8, 7).to(torch.int8)
+        w_flat = w_int.flatten()
+        packed = (w_flat[0::2] & 0x0F) | ((w_flat[1::2] & 0x0F) << 4)
+        self.base_weight.data = packed.to(torch.uint8).view(N, -1).to(device)
+
+        row_ptr, col_indices, values = pack_ortho_sparse(ortho_weight, format="csr")
+        self.ortho_row_ptr = row_ptr.to(device=device, dtype=torch.int32)
+        self.ortho_col_indices = col_indices.to(device=device, dtype=torch.int32)
+        self.ortho_values = values.to(device=device, dtype=torch.float16)
+        self._plan = None
+        self._plan_key = None
+
+    # ------------------------------------------------------------------ plan
+    def _csr_key(self):
+        ts = (self.ortho_values, self.ortho_col_indices, self.ortho_row_ptr)
+        return tuple((t.data_ptr(), t.numel(), t._version, str(t.device)) for t in ts)
+
+    def _ortho_plan(self):
+        """The cached prefill plan, rebuilt when the CSR buffers change."""
+        if self.ortho_values.numel() == 0 or not self.ortho_values.is_cuda:
+            return None
+        key = self._csr_key()
+        if self._plan_key != key:
+            self._plan = _C.build_plan(self.base_weight, self.base_scales, self.ortho_values,
+                                       self.ortho_col_indices, self.ortho_row_ptr, self.in_features)
+            self._plan_key = key
+        return self._plan
+
+    def _apply(self, fn, *args, **kwargs):
+        self._plan = None
+        self._plan_key = None
+        return super()._apply(fn, *args, **kwargs)
+
+    # --------------------------------------------------------------- forward
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        original_shape = x.shape
+        x_flat = x.reshape(-1, self.in_features)
+        batch_size = x_flat.shape[0]
+        output = torch.empty(batch_size, self.out_features, device=x.device, dtype=x.dtype)
+        if not x.is_cuda:
+            raise RuntimeError("OrthoLinear runs on a ROCm GPU only; move the module and the input "
+                               "to a cuda device (the reference's CPU branch returns uninitialised memory)")
+        plan = None
+        if self.alpha > 0 and batch_size >= _PLAN_MIN_TOKENS:
+            plan = self._ortho_plan()
+        _C.forward_planned(self.base_weight, self.base_scales, self.ortho_values,
+                           self.ortho_col_indices, self.ortho_row_ptr, x_flat.contiguous(), output,
+                           self.alpha, plan)
+        if self.bias is not None:
+            output += self.bias
+        return output.view(*original_shape[:-1], self.out_features)
+
+    def extra_repr(self) -> str:
+        g = "row" if self.group_size is None else self.group_size
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"q_bits={self.q_bits}, group={g}, nnz={self.ortho_values.numel()}, alpha={self.alpha}")

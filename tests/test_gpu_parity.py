@@ -1,0 +1,310 @@
+"""Parity of the HIP kernels with the CPU oracle, through the C ABI.
+
+Bar (from the benchmark brief): dequantised base weights bit-exact in FP32;
+outputs within max|err| <= 1e-2 * ||y||_inf of the FP64 accumulation of the
+reference formula (oracle.forward_f64).  Full BASELINE shapes are used; for
+M = 2048 the oracle checks a spread of token rows (rows of x are
+independent, so a subset is an exact check of those rows).
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from libortho_amd import _C_ops, _lib
+from libortho_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2  # max |err| <= TOL * ||y||_inf
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _dev(gpu):
+    torch.cuda.set_device(0)
+    yield
+    _lib.set_kernel_policy("auto")
+
+
+def run(layer, x_np, alpha, policy="auto", plan="auto", dtype=torch.float16, sdtype=None,
+        vdtype=None):
+    d = W.to_device(layer)
+    if sdtype is not None:
+        d["scales"] = d["scales"].to(sdtype)
+    if vdtype is not None:
+        d["vals"] = d["vals"].to(vdtype)
+    x = torch.from_numpy(np.asarray(x_np)).cuda().to(dtype)
+    y = torch.full((x.shape[0], layer.N), float("nan"), dtype=dtype, device="cuda")
+    p = None
+    if plan is True:
+        p = _C_ops.build_plan(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], layer.K)
+    _lib.set_kernel_policy(policy)
+    try:
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y,
+                               alpha, p)
+        kernel = _C_ops.last_kernel()
+    finally:
+        _lib.set_kernel_policy("auto")
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), kernel
+
+
+def oracle_y(oracle_mod, layer, x_np, alpha):
+    return oracle_mod.forward_f64(layer.q, layer.scales, layer.row_ptr, layer.col, layer.vals,
+                                  x_np, alpha)
+
+
+def assert_close(y, ref, tol=TOL, what=""):
+    assert np.isfinite(y).all(), f"{what}: non-finite output"
+    err = float(np.abs(y - ref).max())
+    yinf = float(np.abs(ref).max())
+    assert err <= tol * yinf, f"{what}: max|err| {err:.3e} > {tol} * ||y||_inf {yinf:.3e}"
+    return err / max(yinf, 1e-30)
+
+
+@pytest.fixture(scope="module")
+def c2():
+    return W.config_layer("c2")
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("cfg", ["c1", "c2"])
+def test_dequant_bit_exact(oracle_mod, cfg):
+    L = W.config_layer(cfg)
+    d = W.to_device(L)
+    got = _C_ops.dequant(d["q"], d["scales"], L.K).cpu().numpy()
+    expect = oracle_mod.dequant_f32(L.q, L.scales)
+    assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
+
+
+def test_dequant_odd_groups_bit_exact(oracle_mod):
+    L = W.make_layer(200, 37, 40, 0.0, seed=11)  # G = 40, K not a multiple of 64
+    d = W.to_device(L)
+    got = _C_ops.dequant(d["q"], d["scales"], L.K).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), oracle_mod.dequant_f32(L.q, L.scales).view(np.uint32))
+
+
+# ---------------------------------------------------------- decode (M <= 16)
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_decode_c2_sweep(oracle_mod, c2, M):
+    x = W.make_x(M, c2.K, 2000 + M)
+    y, k = run(c2, x, 1.0)
+    assert k == "decode"
+    assert_close(y, oracle_y(oracle_mod, c2, x, 1.0), what=f"c2 M={M}")
+
+
+@pytest.mark.parametrize("alpha", [0.0, 1.0])
+def test_decode_c1_per_row_scales(oracle_mod, alpha):
+    L = W.config_layer("c1")
+    x = W.make_x(1, L.K, 1001)
+    y, k = run(L, x, alpha)
+    assert k == "decode"
+    assert_close(y, oracle_y(oracle_mod, L, x, alpha), what=f"c1 alpha={alpha}")
+
+
+def test_decode_c4_skewed(oracle_mod):
+    L = W.config_layer("c4")
+    x = W.make_x(8, L.K, 4001)
+    y, k = run(L, x, 1.0)
+    assert k == "decode"
+    assert_close(y, oracle_y(oracle_mod, L, x, 1.0), what="c4")
+
+
+def test_decode_accuracy_is_tight(oracle_mod, c2):
+    # exact q in FP16, FP32 accumulation: the only sizeable error is the
+    # final FP16 rounding of y
+    x = W.make_x(1, c2.K, 2999)
+    y, _ = run(c2, x, 1.0)
+    ref = oracle_y(oracle_mod, c2, x, 1.0)
+    rel = np.abs(y - ref) / np.maximum(np.abs(ref), 1e-3)
+    assert np.abs(y - ref).max() <= 2e-3 * np.abs(ref).max()
+    assert np.median(rel) < 1e-3
+
+
+# ------------------------------------------------------- prefill (M > 16)
+
+@pytest.mark.parametrize("alpha", [0.0, 0.5, 1.0])
+@pytest.mark.parametrize("plan", [True, "auto"])
+def test_prefill_c3(oracle_mod, alpha, plan):
+    L = W.config_layer("c3")
+    x = W.make_x(2048, L.K, 3000)
+    y, k = run(L, x, alpha, plan=plan)
+    assert k == "prefill"
+    rows = np.array([0, 1, 255, 256, 511, 1000, 1023, 1024, 1500, 2046, 2047])
+    ref = oracle_y(oracle_mod, L, x[rows], alpha)
+    assert_close(y[rows], ref, what=f"c3 alpha={alpha} plan={plan}")
+
+
+def test_prefill_skewed_plan(oracle_mod):
+    # thousands of plan entries in one (row block, k step): the fold loops
+    L = W.config_layer("c4")
+    x = W.make_x(40, L.K, 4002)
+    y, k = run(L, x, 1.0, plan=True)
+    assert k == "prefill"
+    assert_close(y, oracle_y(oracle_mod, L, x, 1.0), what="c4 prefill")
+
+
+@pytest.mark.parametrize("M", [1, 32])
+def test_llama_block_c5(oracle_mod, M):
+    for L in W.llama_block():
+        x = W.make_x(M, L.K, 5100 + M)
+        y, k = run(L, x, 1.0, plan=True)
+        assert k == ("decode" if M == 1 else "prefill")
+        rows = np.arange(M) if M <= 8 else np.array([0, 7, 15, 16, 31])
+        assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"c5 {L.name} M={M}")
+
+
+# ----------------------------------------------------------------- edges
+
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 511, 512, 513])
+def test_ragged_shapes(oracle_mod, M):
+    L = W.make_layer(512, 1000, 128, 0.02, seed=70 + M)  # N not a multiple of 16 or 128
+    x = W.make_x(M, L.K, 71 + M)
+    y, k = run(L, x, 1.0)
+    assert k == ("decode" if M <= 16 else "prefill")
+    rows = np.unique(np.linspace(0, M - 1, min(M, 12)).astype(int))
+    assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"ragged M={M}")
+
+
+@pytest.mark.parametrize("K,G,M,expect", [
+    (64, None, 4, "general"), (64, None, 40, "prefill"), (200, 40, 3, "general"),
+    (200, 40, 50, "general"), (512, 64, 2, "general"), (512, 64, 64, "prefill"),
+    (12800, 128, 20, "general"),
+])
+def test_shapes_outside_the_fast_paths(oracle_mod, K, G, M, expect):
+    L = W.make_layer(K, 96, G, 0.03, seed=K + M)
+    x = W.make_x(M, K, K * 3 + M)
+    y, k = run(L, x, 1.0)
+    assert k == expect
+    assert_close(y, oracle_y(oracle_mod, L, x, 1.0), what=f"K={K} G={G} M={M}")
+
+
+@pytest.mark.parametrize("alpha", [-1.0, 0.0, -0.0, float("nan")])
+def test_alpha_gate_gives_base_only(oracle_mod, alpha):
+    L = W.make_layer(1024, 256, 128, 0.05, seed=90)
+    base = W.Layer(L.K, L.N, L.q, L.scales, np.zeros(L.N + 1, np.int32), np.zeros(0, np.int32),
+                   np.zeros(0, np.float16))
+    for M in (1, 64):
+        x = W.make_x(M, L.K, 91 + M)
+        y, _ = run(L, x, alpha)
+        y0, _ = run(base, x, 1.0)
+        assert np.array_equal(y, y0)
+        assert_close(y, oracle_y(oracle_mod, base, x, 1.0))
+
+
+def test_empty_ortho_and_single_dense_row(oracle_mod):
+    K, N = 1024, 300
+    L = W.make_layer(K, N, 128, 0.0, seed=95)
+    rp = np.zeros(N + 1, np.int32)
+    rp[1:] = K  # row 0 holds every column
+    dense = W.Layer(K, N, L.q, L.scales, rp, np.arange(K, dtype=np.int32),
+                    (np.random.default_rng(1).normal(0, 0.05, K)).astype(np.float16))
+    for M in (1, 5, 100):
+        x = W.make_x(M, K, 96 + M)
+        for lay in (L, dense):
+            y, _ = run(lay, x, 1.0, plan=lay is dense)
+            assert_close(y, oracle_y(oracle_mod, lay, x, 1.0), what=f"M={M}")
+
+
+def test_non_canonical_csr(oracle_mod):
+    # duplicate and unsorted columns, and out-of-range columns (skipped)
+    rng = np.random.default_rng(5)
+    K, N = 1024, 256
+    L = W.make_layer(K, N, 128, 0.0, seed=97)
+    counts = rng.integers(0, 12, size=N)
+    rp = np.zeros(N + 1, np.int32)
+    rp[1:] = np.cumsum(counts)
+    col = rng.integers(0, 40, size=rp[-1]).astype(np.int32)  # many duplicates, unsorted
+    col[::17] = K + 5
+    col[::23] = -3
+    vals = rng.normal(0, 0.05, rp[-1]).astype(np.float16)
+    lay = W.Layer(K, N, L.q, L.scales, rp, col, vals)
+    for M, plan in ((1, "auto"), (7, "auto"), (64, True), (64, "auto")):
+        x = W.make_x(M, K, 98 + M)
+        y, _ = run(lay, x, 1.0, plan=plan)
+        assert_close(y, oracle_y(oracle_mod, lay, x, 1.0), what=f"non-canonical M={M}")
+
+
+def test_malformed_row_ptr_is_contained(oracle_mod):
+    K, N = 512, 128
+    L = W.make_layer(K, N, 128, 0.02, seed=99)
+    rp = L.row_ptr.copy()
+    rp[10], rp[11] = rp[11] + 50, rp[10] - 50  # not monotone
+    bad = W.Layer(K, N, L.q, L.scales, rp, L.col, L.vals)
+    d = W.to_device(bad)
+    with pytest.raises(_lib.OrthoError, match="malformed"):
+        _C_ops.build_plan(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], K)
+    for M in (1, 64):
+        y, _ = run(bad, W.make_x(M, K, 5), 1.0)  # must not fault; result unspecified
+        assert y.shape == (M, N)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_other_activation_dtypes(oracle_mod, dtype):
+    L = W.make_layer(1024, 200, 128, 0.02, seed=101)
+    x = W.make_x(5, L.K, 102).astype(np.float32)
+    if dtype == torch.bfloat16:
+        x = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    y, k = run(L, x, 1.0, dtype=dtype)
+    assert k == "general"
+    assert_close(y, oracle_y(oracle_mod, L, x, 1.0))
+
+
+def test_fp32_scales_and_values(oracle_mod):
+    L = W.make_layer(1024, 200, 128, 0.02, seed=103)
+    x = W.make_x(3, L.K, 104)
+    y, k = run(L, x, 1.0, sdtype=torch.float32, vdtype=torch.float32)
+    assert k == "general"
+    assert_close(y, oracle_y(oracle_mod, L, x, 1.0))
+
+
+def test_reference_golden_vectors_on_gpu(oracle_mod):
+    # the reference's own test inputs and outputs (tests/golden), FP32 end to end
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_coo_cases.npz"))
+    for case in ("testcpu_a1", "testcpu_a0", "testcpu_empty", "rand_96x128_m3",
+                 "rand_40x200_m5", "rand_256x256_m1"):
+        f = {k.split("__", 1)[1]: g[k] for k in g.files if k.startswith(case + "__")}
+        N, K = f["q"].shape[0], f["q"].shape[1] * 2
+        idx = f["idx"].astype(np.int64)
+        rows, cols = idx // K, idx % K
+        order = np.argsort(rows, kind="stable")
+        rp = np.zeros(N + 1, np.int32)
+        rp[1:] = np.cumsum(np.bincount(rows[rows < N], minlength=N))
+        lay = W.Layer(K, N, f["q"], f["scales"], rp, cols[order].astype(np.int32),
+                      f["vals"][order])
+        d = W.to_device(lay)
+        x = torch.from_numpy(f["x"]).cuda()
+        y = torch.empty(x.shape[0], N, dtype=torch.float32, device="cuda")
+        _C_ops.forward(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y,
+                       float(f["alpha"]))
+        np.testing.assert_allclose(y.cpu().numpy(), f["y"], atol=1e-4, rtol=1e-5, err_msg=case)
+
+
+def test_forced_general_agrees_with_decode(oracle_mod, c2):
+    x = W.make_x(2, c2.K, 2100)
+    a, ka = run(c2, x, 1.0)
+    b, kb = run(c2, x, 1.0, policy="general")
+    assert (ka, kb) == ("decode", "general")
+    assert np.abs(a - b).max() <= 2e-3 * np.abs(b).max()
+
+
+def test_deterministic(c2):
+    x = W.make_x(1, c2.K, 2200)
+    a, _ = run(c2, x, 1.0)
+    b, _ = run(c2, x, 1.0)
+    assert np.array_equal(a, b)
+    L = W.config_layer("c3")
+    x = W.make_x(512, L.K, 3100)
+    a, _ = run(L, x, 1.0, plan=True)
+    b, _ = run(L, x, 1.0, plan=True)
+    assert np.array_equal(a, b)
+
+
+def test_empty_batch_is_a_no_op():
+    L = W.make_layer(256, 64, 128, 0.02, seed=7)
+    y, k = run(L, np.zeros((0, 256), np.float16), 1.0)
+    assert y.shape == (0, 64) and k == "none"
