@@ -87,33 +87,42 @@ __device__ __forceinline__ void csr_row_range(const int32_t *row_ptr, int64_t n,
 
 // ------------------------------------------------------ INT4 -> FP16 words
 //
-// Magic-number conversion: OR-ing a 4-bit value u into the low mantissa bits
-// of binary16 1024.0 (0x6400) gives exactly 1024 + u; OR-ing it into bits
-// 4..7 gives 1024 + 16u.  After flipping bit 3 of every nibble (u = q + 8)
-// a packed-half subtract or fused multiply-add recovers q exactly.
+// Magic-number conversion: a 4-bit value u placed in mantissa bits 0..3 of
+// binary16 1024.0 (0x6400) reads as exactly 1024 + u; placed in bits 4..7 of
+// binary16 64.0 (0x5400) it reads as exactly 64 + u (the unit in the last
+// place of 64 is 1/16).  With u = n ^ 8 = q + 8 for the two's complement
+// nibble n, q = (1024 + u) - 1032 = (64 + u) - 72 exactly.  The XOR by 8 is
+// folded into the constant: (w & M) ^ (C | 0x8<<shift) == ((w ^ 0x88888888) & M) | C
+// because the masked bits and C's bits do not overlap.
 
 // "Interleaved" order: from one packed word produce four f16x2 words holding
-// k-pairs (0,4) (1,5) (2,6) (3,7).  Six integer ops + four packed-half ops
-// for 8 weights; the matching activation operand must use the same order
-// (see permute_x8).
+// k-pairs (0,4) (1,5) (2,6) (3,7).  One shift, four and-xor (v_bitop3) and
+// four exact packed-half subtracts for 8 weights; the activation operand
+// must use the same order (see permute_x8).
 __device__ __forceinline__ void int4x8_to_f16_interleaved(uint32_t w, uint32_t out[4]) {
-    const uint32_t wf = w ^ 0x88888888u;
-    const uint32_t t = wf >> 8;
-    uint32_t p0 = (wf & 0x000F000Fu) | 0x64006400u;  // 1024+u0 | 1024+u4
-    uint32_t p1 = (wf & 0x00F000F0u) | 0x64006400u;  // 1024+16u1 | 1024+16u5
-    uint32_t p2 = (t & 0x000F000Fu) | 0x64006400u;   // 1024+u2 | 1024+u6
-    uint32_t p3 = (t & 0x00F000F0u) | 0x64006400u;   // 1024+16u3 | 1024+16u7
-    const f16x2 bias = {(f16)-1032.0f, (f16)-1032.0f};
-    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
-    const f16x2 bias16 = {(f16)-72.0f, (f16)-72.0f};
-    f16x2 h0 = __builtin_bit_cast(f16x2, p0) + bias;                          // exact
-    f16x2 h1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p1), sixteenth, bias16);
-    f16x2 h2 = __builtin_bit_cast(f16x2, p2) + bias;
-    f16x2 h3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p3), sixteenth, bias16);
-    out[0] = __builtin_bit_cast(uint32_t, h0);
-    out[1] = __builtin_bit_cast(uint32_t, h1);
-    out[2] = __builtin_bit_cast(uint32_t, h2);
-    out[3] = __builtin_bit_cast(uint32_t, h3);
+    const uint32_t t = w >> 8;
+    const uint32_t p0 = (w & 0x000F000Fu) ^ 0x64086408u;  // 1024+u0 | 1024+u4
+    const uint32_t p1 = (w & 0x00F000F0u) ^ 0x54805480u;  //   64+u1 |   64+u5
+    const uint32_t p2 = (t & 0x000F000Fu) ^ 0x64086408u;  // 1024+u2 | 1024+u6
+    const uint32_t p3 = (t & 0x00F000F0u) ^ 0x54805480u;  //   64+u3 |   64+u7
+    const f16x2 b1032 = {(f16)-1032.0f, (f16)-1032.0f};
+    const f16x2 b72 = {(f16)-72.0f, (f16)-72.0f};
+    out[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, p0) + b1032);
+    out[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, p1) + b72);
+    out[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, p2) + b1032);
+    out[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, p3) + b72);
+}
+
+// Same words without the bias: halves read 1024+u (k-pairs (0,4), (2,6))
+// and 64+u (k-pairs (1,5), (3,7)).  An MFMA over them yields
+// sum_k x_k q_k + 1032 * sum_{k even} x_k + 72 * sum_{k odd} x_k, and the two
+// activation sums are removed afterwards: five ops for 8 weights.
+__device__ __forceinline__ void int4x8_to_f16_biased(uint32_t w, uint32_t out[4]) {
+    const uint32_t t = w >> 8;
+    out[0] = (w & 0x000F000Fu) ^ 0x64086408u;
+    out[1] = (w & 0x00F000F0u) ^ 0x54805480u;
+    out[2] = (t & 0x000F000Fu) ^ 0x64086408u;
+    out[3] = (t & 0x00F000F0u) ^ 0x54805480u;
 }
 
 // Reorder 8 consecutive fp16 (as 4 words (0,1)(2,3)(4,5)(6,7)) into the

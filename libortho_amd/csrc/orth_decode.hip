@@ -5,245 +5,343 @@
 // serially per thread, one byte load per nibble); the work here is laid out
 // for CDNA4 instead:
 //
-//  * A workgroup of W waves owns RT = 16*R consecutive output rows.  K is cut
-//    into 128-wide chunks dealt round-robin to the waves (split-K inside the
-//    workgroup, reduced through LDS: deterministic, no atomics).
-//  * Per chunk and 16-row block every lane issues ONE 16-byte load: lane
-//    (row r = lane%16, quarter g = lane/16) takes bytes [64c + 16g, +16) of
-//    row r, so the 4 lanes of a row read its 64 contiguous bytes of the
-//    chunk.  All of a wave's chunk loads are issued before any are consumed.
-//  * Each 32-bit word (8 nibbles) becomes 8 exact FP16 integers in registers
-//    (int4x8_to_f16_interleaved) and feeds v_mfma_f32_16x16x32_f16 as the B
-//    operand; the activations (tokens padded to 16 with zeros) are the A
-//    operand, staged once per workgroup in LDS in the matching interleaved
-//    k order.  One MFMA consumes 8 nibbles per lane, so the tensor core does
-//    the K reduction and no cross-lane shuffles are needed for the base term.
-//  * Group scales (G a multiple of 128) are applied to FP32 partial sums per
-//    chunk: q stays exact in FP16 and q*s is never rounded.
-//  * Epilogue: the CSR rows of the workgroup's RT output rows are contiguous
-//    in col/values; 16-lane groups per row walk them with x from LDS, reduce
+//  * A workgroup of 4 waves owns 16 consecutive output rows (one contiguous
+//    16*K/2-byte block of the packed weights).  K is cut into 128-wide
+//    chunks; wave w takes the contiguous run [w*cpw, (w+1)*cpw) (split-K
+//    inside the workgroup, reduced through LDS: deterministic, no atomics).
+//  * Per chunk every lane issues ONE 16-byte nontemporal load: lane (row
+//    r = lane%16, quarter g = lane/16) takes bytes [64c + 16g, +16) of row r.
+//    Every load of the kernel is issued at entry, before anything waits, and
+//    none is scattered: measured on MI355X, per-lane 2- and 4-byte loads
+//    touching 16 rows per instruction cost more than the weight stream.
+//  * Each 32-bit word (8 nibbles) becomes 8 FP16 values in registers and
+//    feeds v_mfma_f32_16x16x32_f16 as the B operand; the activations (tokens
+//    padded to 16) are the A operand.  The tensor core does the K reduction.
+//  * Activations staged in LDS (small M*K), each wave staging only its own
+//    chunks (so no barrier precedes the main loop): the weights are
+//    converted with five bit operations into exact FP16 integers q+1032
+//    (even k) / q+72 (odd k), and the FP32 partial of each chunk is corrected
+//    by 1032*sum(x even) + 72*sum(x odd) of that chunk, computed while
+//    staging.  Activations read from global memory (larger M*K): the bias is
+//    subtracted in FP16, exactly.  Either way q is never rounded and q*s is
+//    never formed in FP16.
+//  * Group scales: G = 128 (one 32-bit load per lane per 8 chunks, broadcast
+//    by lane shuffles) or G = 128 * 2^j; per-row scales (G = K) are applied
+//    once at the end.
+//  * Sparse ortho term: the CSR entries of the workgroup's 16 rows are
+//    contiguous; they are loaded with 16-byte loads into LDS (bounds first,
+//    then the block), then 16 lanes per row sum v*x with x from LDS, reduce
 //    with lane shuffles and add alpha*sum after the base term, as
-//    /root/reference/src/dual_gemm.cu:212-221 does.  alpha <= 0 skips it on a
-//    uniform branch without touching the CSR arrays.
+//    /root/reference/src/dual_gemm.cu:212-221 does.  alpha <= 0 skips it on
+//    a uniform branch without touching the CSR arrays.
 #include "orth_common.h"
 
 namespace orth {
 
+constexpr int kDecodeW = 4;       // waves per workgroup
+constexpr int kDecodeNT = 64 * kDecodeW;
+constexpr int kDecodeESlots = 2;  // CSR entries staged per thread: 4 * slots
+constexpr int kDecodeEStaged = kDecodeESlots * 4 * kDecodeNT;
+
 struct DecodeArgs {
     const uint8_t *q;
     const f16 *scales;
-    int64_t ngroups;
-    int64_t G;
+    int ngroups;
+    int gshift;        // group of chunk c is c >> gshift (G = 128 << gshift)
+    int scale_pairs;   // group-128 scales readable as aligned 32-bit pairs
     const int32_t *row_ptr;
     const int32_t *col;
     const f16 *vals;
-    int64_t nnz;
+    int32_t nnz;
+    int csr_vec;       // col 16-byte and vals 8-byte aligned: vector staging
     const f16 *x;
     f16 *y;
     int M;
-    int nchunks;   // K / 128
-    int64_t K, N;
-    int xstride;   // LDS row stride of the staged activations, in halves
+    int nchunks;       // K / 128
+    int K;
+    int64_t N;
+    int cpw;           // chunks per wave, even, <= the CPW template bound
+    int xstride;       // LDS row stride of the staged activations, in halves
+    int lds_cr;        // byte offsets of the LDS regions
+    int lds_xs;
+    int lds_e;
     float alpha;
     int has_ortho;
 };
 
-template <int MT, bool GROUPED, bool XLDS, int W, int R, int PF>
-__global__ void __launch_bounds__(64 * W) decode_kernel(DecodeArgs a) {
-    constexpr int NT = 64 * W;
-    constexpr int RT = 16 * R;
-    constexpr int TPR = NT / RT;  // threads per output row in the sparse epilogue
-    static_assert(TPR >= 1 && TPR <= 64 && (TPR & (TPR - 1)) == 0, "bad epilogue split");
+// GMODE: 0 per-row scale (G == K); 1 G = 128 with scales readable as
+// aligned 32-bit pairs; 2 any G = 128 * 2^j (one 16-bit load per chunk).
+// CPW: compile-time bound of the chunks per wave (all issued at entry).
+// SPARSE: 0 no ortho term; 1 ortho term with the workgroup's CSR block
+// staged through LDS (16-byte aligned columns, nnz >= 4); 2 ortho term read
+// entry by entry in the epilogue.
+//
+// Every global load below is unconditional with a clamped, always valid
+// address: a load under a branch makes the compiler's wait-count insertion
+// fall back to waiting for all outstanding loads, which serialises the
+// kernel behind its own weight stream.
+template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE>
+__global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
+    constexpr int W = kDecodeW;
+    constexpr int NT = kDecodeNT;
+    constexpr int RT = 16;
+    constexpr int MI = MT < 4 ? MT : 4;        // live D rows per lane group (tokens 4g + i)
+    constexpr bool GROUPED = GMODE != 0;
+    constexpr int XIT = (CPW * 16 + 63) / 64;  // 16-byte activation pieces per lane per token
+    constexpr int SW = (CPW + 7) / 8;          // group-128 scale words per lane
+    constexpr int ES = kDecodeESlots;
 
     extern __shared__ __align__(16) unsigned char smem[];
-    float *red = reinterpret_cast<float *>(smem);           // [W][R][16][16]
-    float *sp = red + W * R * 256;                           // [MT][RT]
-    f16 *ss = reinterpret_cast<f16 *>(sp + MT * RT);         // [RT][ngroups] (GROUPED)
-    f16 *xs = ss + (GROUPED ? RT * a.ngroups : 0);           // [MT][xstride] (XLDS)
-    xs = reinterpret_cast<f16 *>((reinterpret_cast<uintptr_t>(xs) + 15) & ~uintptr_t(15));
+    float *red = reinterpret_cast<float *>(smem);              // [W][16][16] split-K partials
+    float *sp = red + W * 256;                                  // [MT][RT] sparse sums
+    float *cr = reinterpret_cast<float *>(smem + a.lds_cr);     // [MT][nchunks] bias sums (XLDS)
+    f16 *xs = reinterpret_cast<f16 *>(smem + a.lds_xs);         // [MT][xstride] activations
+    int32_t *ec = reinterpret_cast<int32_t *>(smem + a.lds_e);  // staged CSR columns
+    f16 *ev = reinterpret_cast<f16 *>(ec + kDecodeEStaged);     // staged CSR values
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int nl = lane & 15;  // B column (weight row) and A row (token) of this lane
     const int g = lane >> 4;   // which 32-k quarter of a chunk
     const int64_t n0 = (int64_t)blockIdx.x * RT;
-    const int64_t K = a.K;
+    const int K = a.K;
+    const int c_lo = wave * a.cpw;
+    const int nci = max(0, min(a.cpw, a.nchunks - c_lo));  // uniform
+    const int clast = a.nchunks - 1;                        // last valid chunk of a row
+    const int64_t rows_here = a.N - n0;
+    const int last_row = (int)(rows_here < 16 ? rows_here - 1 : 15);
+    const int my_row = min(nl, last_row);
 
-    // ---- issue this wave's first weight loads before anything else
-    const int nci = (a.nchunks - wave + W - 1) / W;  // chunks of this wave
-    const uint8_t *qrow[R];
+    // ---- activations of this wave's chunks (L2-resident), contiguous;
+    //      pieces past the wave's range re-read the last valid piece
+    u32x4 xreg[XLDS ? MT * XIT : 1];
+    const int xlast = a.nchunks * 16 - 1;  // last 16-byte piece of a token row
+    if (XLDS) {
 #pragma unroll
-    for (int rb = 0; rb < R; rb++) {
-        int64_t n = n0 + rb * 16 + nl;
-        n = n < a.N ? n : a.N - 1;
-        qrow[rb] = a.q + n * (K >> 1) + g * 16;
-    }
-    u32x4 wbuf[PF][R];
-    u32x4 abuf[XLDS ? 1 : PF][4];
-    const bool tok_ok = nl < a.M;  // rows of A beyond M are zero
-    const f16 *xrow = a.x + (int64_t)(tok_ok ? nl : 0) * K + g * 32;
+        for (int m = 0; m < MT; m++) {
+            const f16 *xr = a.x + (int64_t)min(m, a.M - 1) * K;
 #pragma unroll
-    for (int p = 0; p < PF; p++) {
-        if (p < nci) {
-            const int c = wave + W * p;
-#pragma unroll
-            for (int rb = 0; rb < R; rb++)
-                wbuf[p][rb] = *reinterpret_cast<const u32x4 *>(qrow[rb] + c * 64);
-            if (!XLDS) {
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    abuf[p][j] = tok_ok ? *reinterpret_cast<const u32x4 *>(xrow + c * 128 + 8 * j)
-                                        : u32x4{0, 0, 0, 0};
+            for (int it = 0; it < XIT; it++) {
+                const int pc = min(c_lo * 16 + lane + 64 * it, xlast);
+                xreg[m * XIT + it] = *reinterpret_cast<const u32x4 *>(xr + pc * 8);
             }
         }
     }
 
-    // ---- stage activations (interleaved k order) and group scales in LDS
+    // ---- CSR bounds: this thread's epilogue row, and the workgroup block
+    const int rl = tid >> 4, sub = tid & 15;
+    int32_t rs = 0, re = 0, e0 = 0, e1 = 0;
+    if (SPARSE) {
+        const int32_t r_lo = a.row_ptr[n0 + min(rl, last_row)];
+        const int32_t r_hi = a.row_ptr[n0 + min(rl, last_row) + 1];
+        const int32_t b_lo = a.row_ptr[n0];
+        const int32_t b_hi = a.row_ptr[n0 + last_row + 1];
+        rs = min(max(r_lo, 0), a.nnz);
+        re = min(max(r_hi, rs), a.nnz);
+        if (rl > last_row) re = rs;  // rows past N have no entries
+        e0 = min(max(b_lo, 0), a.nnz);
+        e1 = min(max(b_hi, e0), a.nnz);
+    }
+
+    // ---- per-row scale of the row this thread combines at the end
+    f16 srow = (f16)0.0f;
+    if (!GROUPED) srow = a.scales[n0 + min(tid & 15, last_row)];
+
+    // ---- group scales: lane (row nl, g) holds chunks 8i + 2g, 8i + 2g + 1
+    //      (GMODE 1), or one scale per chunk (GMODE 2)
+    const f16 *sbase = a.scales + (n0 + my_row) * (int64_t)a.ngroups;
+    uint32_t sw[SW];
+    f16 sh[GMODE == 2 ? CPW : 1];
+    if (GMODE == 1) {
+#pragma unroll
+        for (int i = 0; i < SW; i++)
+            sw[i] = *reinterpret_cast<const uint32_t *>(sbase + (min(c_lo + 8 * i + 2 * g, clast) & ~1));
+    } else if (GMODE == 2) {
+#pragma unroll
+        for (int p = 0; p < CPW; p++) sh[p] = sbase[min(c_lo + p, clast) >> a.gshift];
+    }
+
+    // ---- weights (nontemporal): uniform base + 32-bit lane offset + offset
+    const uint8_t *qrow = a.q + (n0 + my_row) * (int64_t)(K >> 1) + g * 16;
+    u32x4 wv[CPW];
+#pragma unroll
+    for (int p = 0; p < CPW; p++)
+        wv[p] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(qrow + min(c_lo + p, clast) * 64));
+
+    // ---- activations from global memory (no LDS staging): 64 bytes per
+    //      lane per chunk; A rows beyond M repeat row 0 (outputs unused)
+    u32x4 ag[XLDS ? 1 : CPW][4];
+    if (!XLDS) {
+        const f16 *xrow = a.x + (int64_t)(nl < a.M ? nl : 0) * K + g * 32;
+#pragma unroll
+        for (int p = 0; p < CPW; p++) {
+            const int c = min(c_lo + p, clast);
+#pragma unroll
+            for (int j = 0; j < 4; j++) ag[p][j] = *reinterpret_cast<const u32x4 *>(xrow + (c * 128 + 8 * j));
+        }
+    }
+
+    // ---- CSR block of the workgroup: 4 entries per thread per slot, from the
+    //      aligned start eb; the last aligned group of the arrays bounds it
+    const int32_t eb = e0 & ~3;
+    const int32_t last4 = (a.nnz - 4) & ~3;
+    u32x4 ecv[ES];
+    uint2 evv[ES];
+    if (SPARSE == 1) {
+#pragma unroll
+        for (int s = 0; s < ES; s++) {
+            const int32_t ic = min(eb + 4 * (tid + NT * s), last4);
+            ecv[s] = *reinterpret_cast<const u32x4 *>(a.col + ic);
+            evv[s] = *reinterpret_cast<const uint2 *>(a.vals + ic);
+        }
+    }
+
+    // ---- stage this wave's activations (interleaved k order) and their
+    //      per-chunk bias sums; only this wave reads them before the end
+    const int wpieces = nci * 16;
     if (XLDS) {
-        const int k8 = (int)(K >> 3);
-        for (int idx = tid; idx < MT * k8; idx += NT) {
-            const int m = idx / k8, c8 = idx - m * k8;
-            u32x4 v = {0, 0, 0, 0};
-            if (m < a.M) v = permute_x8(*reinterpret_cast<const u32x4 *>(a.x + (int64_t)m * K + c8 * 8));
-            *reinterpret_cast<u32x4 *>(xs + m * a.xstride + c8 * 8) = v;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+#pragma unroll
+            for (int it = 0; it < XIT; it++) {
+                {
+                    const int pc = lane + 64 * it;
+                    u32x4 v = xreg[m * XIT + it];
+                    if (m >= a.M) v = u32x4{0, 0, 0, 0};
+                    const f16x8 h = __builtin_bit_cast(f16x8, v);
+                    // even k weigh 1032, odd k weigh 72 (see int4x8_to_f16_biased)
+                    const float e = ((float)h[0] + (float)h[2]) + ((float)h[4] + (float)h[6]);
+                    const float o = ((float)h[1] + (float)h[3]) + ((float)h[5] + (float)h[7]);
+                    const float b = group_sum<16>(1032.0f * e + 72.0f * o);  // 16 pieces of a chunk
+                    if (pc < wpieces) {
+                        *reinterpret_cast<u32x4 *>(xs + (m * a.xstride + c_lo * 128 + pc * 8)) = permute_x8(v);
+                        if ((pc & 15) == 0) cr[m * a.nchunks + c_lo + (pc >> 4)] = b;
+                    }
+                }
+            }
         }
     }
-    if (GROUPED) {
-        const int total = RT * (int)a.ngroups;
-        for (int idx = tid; idx < total; idx += NT) {
-            const int r = idx / (int)a.ngroups, gg = idx - r * (int)a.ngroups;
-            int64_t n = n0 + r;
-            n = n < a.N ? n : a.N - 1;
-            ss[idx] = a.scales[n * a.ngroups + gg];
-        }
-    }
-    __syncthreads();
 
     // ---- main loop over this wave's chunks
-    f32x4 acc[R];
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    float bias_acc[MI];
 #pragma unroll
-    for (int rb = 0; rb < R; rb++) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    for (int base = 0; base < nci; base += PF) {
-        u32x4 cur[PF][R];
-        u32x4 acur[XLDS ? 1 : PF][4];
+    for (int i = 0; i < MI; i++) bias_acc[i] = 0.f;
+    const f16 *xs_lane = xs + ((nl & (MT - 1)) * a.xstride + g * 32 + c_lo * 128);
+    const float *cr_lane[MI];
 #pragma unroll
-        for (int p = 0; p < PF; p++) {
+    for (int i = 0; i < MI; i++) cr_lane[i] = cr + ((4 * g + i) & (MT - 1)) * a.nchunks + c_lo;
 #pragma unroll
-            for (int rb = 0; rb < R; rb++) cur[p][rb] = wbuf[p][rb];
-            if (!XLDS) {
+    for (int p = 0; p < CPW; p++) {
+        if (p < nci) {  // uniform
+            const uint32_t words[4] = {wv[p].x, wv[p].y, wv[p].z, wv[p].w};
+            f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int j = 0; j < 4; j++) acur[p][j] = abuf[p][j];
+            for (int j = 0; j < 4; j++) {
+                uint32_t b[4];
+                u32x4 av;
+                if (XLDS) {
+                    int4x8_to_f16_biased(words[j], b);
+                    av = *reinterpret_cast<const u32x4 *>(xs_lane + (p * 128 + 8 * j));
+                } else {
+                    int4x8_to_f16_interleaved(words[j], b);
+                    av = permute_x8(ag[p][j]);
+                }
+                const f16x8 afr = __builtin_bit_cast(f16x8, av);
+                const f16x8 bfr = __builtin_bit_cast(f16x8, u32x4{b[0], b[1], b[2], b[3]});
+                if (GROUPED)
+                    part = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr, bfr, part, 0, 0, 0);
+                else
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr, bfr, acc, 0, 0, 0);
             }
-        }
-        // prefetch the next batch
-#pragma unroll
-        for (int p = 0; p < PF; p++) {
-            if (base + PF + p < nci) {
-                const int c = wave + W * (base + PF + p);
-#pragma unroll
-                for (int rb = 0; rb < R; rb++)
-                    wbuf[p][rb] = *reinterpret_cast<const u32x4 *>(qrow[rb] + c * 64);
-                if (!XLDS) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        abuf[p][j] = tok_ok ? *reinterpret_cast<const u32x4 *>(xrow + c * 128 + 8 * j)
-                                            : u32x4{0, 0, 0, 0};
-                }
-            }
-        }
-#pragma unroll
-        for (int p = 0; p < PF; p++) {
-            if (base + p < nci) {
-                const int c = wave + W * (base + p);
-                f16x8 afr[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    u32x4 av;
-                    if (XLDS) {
-                        av = (nl < MT) ? *reinterpret_cast<const u32x4 *>(xs + nl * a.xstride + c * 128 + g * 32 + 8 * j)
-                                       : u32x4{0, 0, 0, 0};
-                    } else {
-                        av = permute_x8(acur[p][j]);
-                    }
-                    afr[j] = __builtin_bit_cast(f16x8, av);
+            if (GROUPED) {
+                float s;
+                if (GMODE == 1) {
+                    // scales of chunks 8i + 2g', +1 sit in lane 16g' + nl
+                    const uint32_t w2 = (uint32_t)__shfl((int)sw[p >> 3], 16 * ((p & 7) >> 1) + nl, 64);
+                    s = (float)__builtin_bit_cast(f16, (uint16_t)((p & 1) ? (w2 >> 16) : (w2 & 0xffffu)));
+                } else {
+                    s = (float)sh[p];
                 }
 #pragma unroll
-                for (int rb = 0; rb < R; rb++) {
-                    const u32x4 wv = cur[p][rb];
-                    const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-                    f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        uint32_t b[4];
-                        int4x8_to_f16_interleaved(words[j], b);
-                        const f16x8 bfr = __builtin_bit_cast(f16x8, u32x4{b[0], b[1], b[2], b[3]});
-                        if (GROUPED)
-                            part = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr[j], bfr, part, 0, 0, 0);
-                        else
-                            acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr[j], bfr, acc[rb], 0, 0, 0);
-                    }
-                    if (GROUPED) {
-                        const float s = (float)ss[(rb * 16 + nl) * a.ngroups + ((int64_t)c * 128) / a.G];
-                        acc[rb] += s * part;
-                    }
+                for (int i = 0; i < MI; i++) {
+                    float v = part[i];
+                    if (XLDS) v -= cr_lane[i][p];
+                    acc[i] += s * v;
                 }
+            } else if (XLDS) {
+#pragma unroll
+                for (int i = 0; i < MI; i++) bias_acc[i] += cr_lane[i][p];
             }
         }
     }
-
-    // ---- split-K partials to LDS: lane holds D[token 4g+i][row nl]
+    if (!GROUPED && XLDS) {
 #pragma unroll
-    for (int rb = 0; rb < R; rb++) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) red[((wave * R + rb) * 16 + (4 * g + i)) * 16 + nl] = acc[rb][i];
+        for (int i = 0; i < MI; i++) acc[i] -= bias_acc[i];
     }
 
-    // ---- sparse ortho term: TPR lanes per output row
-    if (a.has_ortho) {
-        const int rl = tid / TPR, sub = tid - rl * TPR;
-        const int64_t n = n0 + rl;
+    // ---- split-K partials and the staged CSR block to LDS
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[(wave * 16 + (4 * g + i)) * 16 + nl] = acc[i];
+    if (SPARSE == 1) {
+#pragma unroll
+        for (int s = 0; s < ES; s++) {
+            const int slot = 4 * (tid + NT * s);
+            *reinterpret_cast<u32x4 *>(ec + slot) = ecv[s];
+            *reinterpret_cast<uint2 *>(ev + slot) = evv[s];
+        }
+    }
+    __syncthreads();  // every wave's activation chunks and the CSR block are in LDS
+
+    // ---- sparse ortho term: 16 lanes per output row
+    if (SPARSE) {
+        // entries [eb, staged_hi) sit in LDS; the rest are read from memory
+        const int32_t staged_hi = SPARSE == 1 ? min(min(eb + kDecodeEStaged, last4 + 4), e1) : eb;
         float sacc[MT];
 #pragma unroll
         for (int m = 0; m < MT; m++) sacc[m] = 0.f;
-        if (n < a.N) {
-            int32_t rs, re;
-            csr_row_range(a.row_ptr, n, a.nnz, rs, re);
-            for (int32_t j = rs + sub; j < re; j += TPR) {
-                const int32_t c = a.col[j];
-                if (c >= 0 && c < K) {
-                    const float v = (float)a.vals[j];
+        for (int32_t j = rs + sub; j < re; j += 16) {
+            int32_t c;
+            float v;
+            if (j >= eb && j < staged_hi) {
+                c = ec[j - eb];
+                v = (float)ev[j - eb];
+            } else {
+                c = a.col[j];
+                v = (float)a.vals[j];
+            }
+            if (c >= 0 && c < K) {
 #pragma unroll
-                    for (int m = 0; m < MT; m++) {
-                        if (m < a.M) {
-                            float xv;
-                            if (XLDS) xv = (float)xs[m * a.xstride + (c & ~7) + interleaved_pos(c & 7)];
-                            else xv = (float)a.x[(int64_t)m * K + c];
-                            sacc[m] += v * xv;
-                        }
+                for (int m = 0; m < MT; m++) {
+                    if (m < a.M) {
+                        float xv;
+                        if (XLDS) xv = (float)xs[m * a.xstride + ((c & ~7) | interleaved_pos(c & 7))];
+                        else xv = (float)a.x[(int64_t)m * K + c];
+                        sacc[m] += v * xv;
                     }
                 }
             }
         }
 #pragma unroll
         for (int m = 0; m < MT; m++) {
-            const float s = group_sum<TPR>(sacc[m]);
+            const float s = group_sum<16>(sacc[m]);
             if (sub == 0) sp[m * RT + rl] = s;
         }
     }
     __syncthreads();
 
     // ---- combine split-K partials, scale, add alpha * sparse, store
-    for (int idx = tid; idx < MT * RT; idx += NT) {
-        const int m = idx / RT, rl = idx - m * RT;
-        const int64_t n = n0 + rl;
+    if (tid < MT * RT) {
+        const int m = tid >> 4, r = tid & 15;
+        const int64_t n = n0 + r;
         if (m < a.M && n < a.N) {
             float v = 0.f;
 #pragma unroll
-            for (int w = 0; w < W; w++) v += red[((w * R + (rl >> 4)) * 16 + m) * 16 + (rl & 15)];
-            if (!GROUPED) v *= (float)a.scales[n];
-            if (a.has_ortho) v += a.alpha * sp[m * RT + rl];
+            for (int w = 0; w < W; w++) v += red[(w * 16 + m) * 16 + r];
+            if (!GROUPED) v *= (float)srow;
+            if (SPARSE) v += a.alpha * sp[m * RT + r];
             a.y[(int64_t)m * a.N + n] = (f16)v;
         }
     }
@@ -251,39 +349,73 @@ __global__ void __launch_bounds__(64 * W) decode_kernel(DecodeArgs a) {
 
 // ------------------------------------------------------------------ host
 
-template <int MT, bool GROUPED, bool XLDS>
+template <int MT, int GMODE, bool XLDS, int CPW>
 static hipError_t launch_decode_t(const DecodeArgs &d, int64_t lds_bytes, hipStream_t stream) {
-    constexpr int W = 4, R = 1;
-    constexpr int PF = XLDS ? 8 : 4;
-    auto kern = decode_kernel<MT, GROUPED, XLDS, W, R, PF>;
-    const unsigned blocks = (unsigned)((d.N + 16 * R - 1) / (16 * R));
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * W), (uint32_t)lds_bytes, stream, d);
+    const unsigned blocks = (unsigned)((d.N + 15) / 16);
+    if (d.has_ortho && d.csr_vec)
+        hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, 1>), dim3(blocks), dim3(kDecodeNT),
+                           (uint32_t)lds_bytes, stream, d);
+    else if (d.has_ortho)
+        hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, 2>), dim3(blocks), dim3(kDecodeNT),
+                           (uint32_t)lds_bytes, stream, d);
+    else
+        hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, 0>), dim3(blocks), dim3(kDecodeNT),
+                           (uint32_t)lds_bytes, stream, d);
     return hipGetLastError();
 }
 
-template <bool GROUPED, bool XLDS>
+// Chunk-count bounds that can occur: the staged activation block is at most
+// 40 KB (so MT * K is bounded) and the global-memory A path takes CPW <= 8.
+template <int MT, int GMODE, bool XLDS>
+static hipError_t launch_decode_cpw(const DecodeArgs &d, int64_t lds, hipStream_t s) {
+    constexpr bool c16 = XLDS && MT <= 4;
+    constexpr bool c24 = XLDS && MT <= 2;
+    if (d.cpw <= 8) return launch_decode_t<MT, GMODE, XLDS, 8>(d, lds, s);
+    if (d.cpw <= 16 && c16) return launch_decode_t<MT, GMODE, XLDS, (c16 ? 16 : 8)>(d, lds, s);
+    if (c24) return launch_decode_t<MT, GMODE, XLDS, (c24 ? 24 : 8)>(d, lds, s);
+    return hipErrorInvalidValue;  // excluded by decode_supported()
+}
+
+template <int GMODE, bool XLDS>
 static hipError_t launch_decode_mt(int mt, const DecodeArgs &d, int64_t lds, hipStream_t s) {
     switch (mt) {
-        case 1: return launch_decode_t<1, GROUPED, XLDS>(d, lds, s);
-        case 2: return launch_decode_t<2, GROUPED, XLDS>(d, lds, s);
-        case 4: return launch_decode_t<4, GROUPED, XLDS>(d, lds, s);
-        case 8: return launch_decode_t<8, GROUPED, XLDS>(d, lds, s);
-        default: return launch_decode_t<16, GROUPED, XLDS>(d, lds, s);
+        case 1: return launch_decode_cpw<1, GMODE, XLDS>(d, lds, s);
+        case 2: return launch_decode_cpw<2, GMODE, XLDS>(d, lds, s);
+        case 4: return launch_decode_cpw<4, GMODE, XLDS>(d, lds, s);
+        case 8: return launch_decode_cpw<8, GMODE, XLDS>(d, lds, s);
+        default: return launch_decode_cpw<16, GMODE, XLDS>(d, lds, s);
     }
 }
 
 // Largest activation block staged in LDS; above it the A operand is read
-// straight from global memory (L2-resident) with a register prefetch.
+// straight from global memory (L2-resident), 64 bytes per lane per chunk.
 static const int64_t kDecodeXLdsMax = 40 * 1024;
+static const int kDecodeMaxCPW = 24;
+
+// Chunks per wave: an even count (group-128 scales come in pairs).
+static int decode_cpw(int64_t K) {
+    const int64_t nchunks = K / 128;
+    const int64_t c = (nchunks + kDecodeW - 1) / kDecodeW;
+    return (int)((c + 1) & ~int64_t(1));
+}
+
+static bool decode_xlds(int64_t M, int64_t K) {
+    int64_t mt = 1;
+    while (mt < M) mt <<= 1;
+    return mt * (K + 8) * 2 <= kDecodeXLdsMax;
+}
 
 bool decode_supported(const ForwardArgs &a) {
     if (a.M < 1 || a.M > 16) return false;
     if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
     if (a.has_ortho && a.val_dtype != ORTH_DT_F16) return false;
-    if (a.K % 128 != 0) return false;
-    if (a.ngroups != 1 && (a.G % 128 != 0)) return false;
-    if (a.K > (int64_t)1 << 24 || a.N > ((int64_t)1 << 31)) return false;
+    if (a.K % 128 != 0 || decode_cpw(a.K) > kDecodeMaxCPW || a.N > ((int64_t)1 << 31)) return false;
+    // group size 128 * 2^j (the group of a 128-wide chunk is a shift)
+    if (a.ngroups != 1 && (a.G % 128 != 0 || ((a.G / 128) & (a.G / 128 - 1)) != 0)) return false;
     if ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.x)) & 15) return false;
+    // the global-memory A operand keeps 64 bytes per lane per chunk in
+    // registers: at most 8 chunks per wave
+    if (!decode_xlds(a.M, a.K) && decode_cpw(a.K) > 8) return false;
     return true;
 }
 
@@ -291,18 +423,20 @@ hipError_t launch_decode(const ForwardArgs &a, hipStream_t stream) {
     DecodeArgs d;
     d.q = a.q;
     d.scales = static_cast<const f16 *>(a.scales);
-    d.ngroups = a.ngroups;
-    d.G = a.G;
+    d.ngroups = (int)a.ngroups;
     d.row_ptr = a.row_ptr;
     d.col = a.col;
     d.vals = static_cast<const f16 *>(a.vals);
-    d.nnz = a.nnz;
+    d.nnz = (int32_t)a.nnz;
+    d.csr_vec = a.nnz >= 4 && ((reinterpret_cast<uintptr_t>(a.col) & 15) == 0) &&
+                ((reinterpret_cast<uintptr_t>(a.vals) & 7) == 0);
     d.x = static_cast<const f16 *>(a.x);
     d.y = static_cast<f16 *>(a.y);
     d.M = (int)a.M;
     d.nchunks = (int)(a.K / 128);
-    d.K = a.K;
+    d.K = (int)a.K;
     d.N = a.N;
+    d.cpw = decode_cpw(a.K);
     d.xstride = (int)(a.K + 8);  // +16 bytes: rows start in different LDS banks
     d.alpha = a.alpha;
     d.has_ortho = a.has_ortho;
@@ -310,21 +444,27 @@ hipError_t launch_decode(const ForwardArgs &a, hipStream_t stream) {
     int mt = 1;
     while (mt < a.M) mt <<= 1;
     const bool grouped = a.ngroups != 1;
-    const int W = 4, R = 1;
-    int64_t lds = (int64_t)W * R * 256 * 4 + (int64_t)mt * 16 * R * 4;
-    if (grouped) lds += (int64_t)16 * R * a.ngroups * 2;
+    d.gshift = 0;
+    if (grouped)
+        while ((128LL << d.gshift) < a.G) d.gshift++;
+    d.scale_pairs = (a.ngroups % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.scales) & 3) == 0);
+    const bool xlds = decode_xlds(a.M, a.K);
+    int64_t lds = (int64_t)kDecodeW * 256 * 4 + (int64_t)mt * 16 * 4;
     lds = (lds + 15) & ~int64_t(15);
-    const int64_t xbytes = (int64_t)mt * d.xstride * 2;
-    const bool xlds = xbytes <= kDecodeXLdsMax;
-    if (xlds) lds += xbytes + 16;
+    d.lds_cr = (int)lds;
+    if (xlds) lds += (int64_t)mt * d.nchunks * 4;
+    lds = (lds + 15) & ~int64_t(15);
+    d.lds_xs = (int)lds;
+    if (xlds) lds += (int64_t)mt * d.xstride * 2;
+    lds = (lds + 15) & ~int64_t(15);
+    d.lds_e = (int)lds;
+    if (a.has_ortho && d.csr_vec) lds += (int64_t)kDecodeEStaged * (4 + 2);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
 
-    if (grouped) {
-        return xlds ? launch_decode_mt<true, true>(mt, d, lds, stream)
-                    : launch_decode_mt<true, false>(mt, d, lds, stream);
-    }
-    return xlds ? launch_decode_mt<false, true>(mt, d, lds, stream)
-                : launch_decode_mt<false, false>(mt, d, lds, stream);
+    const int gmode = !grouped ? 0 : (d.gshift == 0 && d.scale_pairs ? 1 : 2);
+    if (gmode == 1) return xlds ? launch_decode_mt<1, true>(mt, d, lds, stream) : launch_decode_mt<1, false>(mt, d, lds, stream);
+    if (gmode == 2) return xlds ? launch_decode_mt<2, true>(mt, d, lds, stream) : launch_decode_mt<2, false>(mt, d, lds, stream);
+    return xlds ? launch_decode_mt<0, true>(mt, d, lds, stream) : launch_decode_mt<0, false>(mt, d, lds, stream);
 }
 
 }  // namespace orth
