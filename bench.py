@@ -54,6 +54,11 @@ def parse():
                     help="budget for the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="eager launches for rocprofv3 --pmc: decode c2 M=1 (alpha 1 and 0), "
+                         "prefill c3 M=2048, then a plain device copy of known size")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn two --profile counter runs into profiles/traffic.json")
     return ap.parse_args()
 
 
@@ -153,6 +158,99 @@ def time_workload(torch, layer, M, alpha, steps, warmup, plan=False):
     return dict(ms_per_step=ms, kernel=kernel, copies=rot.n)
 
 
+COPY_BYTES = 512 << 20  # calibration copy: reads and writes exactly this many bytes
+PROFILE_DECODE_STEPS = 100
+PROFILE_PREFILL_STEPS = 5
+PROFILE_COPIES = 5
+
+
+def profile_run(torch):
+    """Eager launches (no graph) so that rocprofv3 --pmc sees one dispatch
+    per forward: decode c2 M=1 alpha=1, decode c2 M=1 alpha=0, prefill c3
+    M=2048 alpha=1 (planned), then PROFILE_COPIES device-to-device copies of
+    COPY_BYTES (the calibration for FETCH_SIZE / WRITE_SIZE)."""
+    from libortho_amd import workloads as W
+    c2 = W.config_layer("c2")
+    for alpha in (1.0, 0.0):
+        rot = Rotation(c2, torch)
+        x = torch.from_numpy(W.make_x(1, c2.K, 7001)).cuda()
+        y = torch.empty(1, c2.N, dtype=torch.float16, device="cuda")
+        for i in range(PROFILE_DECODE_STEPS):
+            rot.call(i, x, y, alpha)
+        torch.cuda.synchronize()
+        del rot
+    c3 = W.config_layer("c3")
+    rot = Rotation(c3, torch, min_copies=2, min_bytes=0, plan=True)
+    x = torch.from_numpy(W.make_x(2048, c3.K, 9048)).cuda()
+    y = torch.empty(2048, c3.N, dtype=torch.float16, device="cuda")
+    for i in range(PROFILE_PREFILL_STEPS):
+        rot.call(i, x, y, 1.0)
+    torch.cuda.synchronize()
+    del rot
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(PROFILE_COPIES):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "done", "decode_steps": PROFILE_DECODE_STEPS,
+                      "prefill_steps": PROFILE_PREFILL_STEPS, "copies": PROFILE_COPIES,
+                      "copy_bytes": COPY_BYTES}), flush=True)
+
+
+def _pmc_rows(path, counter):
+    import csv
+    rows = []
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] == counter:
+            rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def summarize_pmc(fetch_csv, write_csv):
+    """Per-launch HBM bytes of each orth kernel from two --profile runs under
+    rocprofv3 --pmc (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each
+    scaled by the bytes the same counter reports for the calibration copy
+    (the last PROFILE_COPIES copy dispatches, COPY_BYTES read and written)."""
+    from libortho_amd import workloads as W
+    out = {}
+    per = {}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _pmc_rows(path, counter)
+        copies = [v for _, name, v in rows if "copyBuffer" in name][-PROFILE_COPIES:]
+        assert len(copies) == PROFILE_COPIES, f"{path}: calibration copies not found"
+        factor = (sum(copies) / len(copies)) * 1024.0 / COPY_BYTES
+        kern = {}
+        for _, name, v in rows:
+            if "orth::" in name:
+                kern.setdefault(name, []).append(v)
+        per[counter] = (factor, kern)
+    c2, c3 = W.config_layer("c2"), W.config_layer("c3")
+    f_fac, f_k = per["FETCH_SIZE"]
+    w_fac, w_k = per["WRITE_SIZE"]
+    for name in f_k:
+        if name.startswith("void orth::decode_kernel"):
+            # template arg SPARSE (last) is 0 for the alpha = 0 launches
+            alpha = 0.0 if name.rstrip(")").endswith("0>(orth::DecodeArgs") else 1.0
+            key, algo = f"c2_m1_alpha{int(alpha)}", W.algorithmic_bytes(c2, 1, alpha)
+        elif "orth::prefill_kernel" in name:
+            key, algo = "c3_m2048_alpha1", W.algorithmic_bytes(c3, 2048, 1.0)
+        else:
+            continue
+        fk = sum(f_k[name]) / len(f_k[name])
+        wk = sum(w_k.get(name, [0.0])) / max(1, len(w_k.get(name, [])))
+        fb, wb = fk * 1024.0 / f_fac, wk * 1024.0 / w_fac
+        out[key] = {"kernel": name, "dispatches": len(f_k[name]),
+                    "fetch_kib_raw": round(fk, 2), "write_kib_raw": round(wk, 2),
+                    "fetch_factor": round(f_fac, 4), "write_factor": round(w_fac, 4),
+                    "fetch_bytes": int(fb), "write_bytes": int(wb), "bytes": int(fb + wb),
+                    "algorithmic_bytes": algo, "ratio_to_algorithmic": round((fb + wb) / algo, 4)}
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    json.dump(out, open(p, "w"), indent=1)
+    print(json.dumps(out, indent=1))
+
+
 def load_traffic(workload: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE,
     WRITE_SIZE, copy-kernel calibrated), committed in profiles/traffic.json."""
@@ -165,11 +263,19 @@ def load_traffic(workload: str):
 
 def main():
     args = parse()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the dual GEMM shards by output rows "
               "with no collective (see DESIGN.md), and multi-GPU runs are not part of it",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.profile:
+        import torch
+        profile_run(torch)
+        return
 
     from libortho_amd import workloads as W
     layer = W.config_layer("c2")
@@ -250,7 +356,7 @@ def main():
                    "timing": "K launches in one HIP graph, one timed replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic(workload),
+                     "traffic": (load_traffic(workload) or {}).get("bytes"),
                      "launch_us": round(r["ms_per_step"] * 1e3, 3),
                      "bytes_per_launch": bytes_step},
         "cpu_baseline": cpu,

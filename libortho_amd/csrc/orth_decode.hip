@@ -184,15 +184,18 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     }
 
     // ---- CSR block of the workgroup: 4 entries per thread per slot, from the
-    //      aligned start eb; the last aligned group of the arrays bounds it
+    //      aligned start eb.  Addresses are clamped to the workgroup's last
+    //      aligned group (threads past the block re-read one cached line) and
+    //      to the last aligned group of the arrays (in bounds).
     const int32_t eb = e0 & ~3;
     const int32_t last4 = (a.nnz - 4) & ~3;
+    const int32_t wlast4 = min(max((e1 - 1) & ~3, eb), last4);
     u32x4 ecv[ES];
     uint2 evv[ES];
     if (SPARSE == 1) {
 #pragma unroll
         for (int s = 0; s < ES; s++) {
-            const int32_t ic = min(eb + 4 * (tid + NT * s), last4);
+            const int32_t ic = min(eb + 4 * (tid + NT * s), wlast4);
             ecv[s] = *reinterpret_cast<const u32x4 *>(a.col + ic);
             evv[s] = *reinterpret_cast<const uint2 *>(a.vals + ic);
         }
