@@ -229,118 +229,176 @@ struct PrefillArgs {
 };
 
 constexpr int PF_BM = 256, PF_BN = 128, PF_BK = 64;
-constexpr int PF_LDK = PF_BK + 8;  // LDS row stride in halves (+16 bytes)
-constexpr int PF_A_BYTES = PF_BM * PF_LDK * 2;
-constexpr int PF_B_BYTES = PF_BN * PF_LDK * 2;
-constexpr int PF_LDS_BYTES = 2 * (PF_A_BYTES + PF_B_BYTES);
+constexpr int PF_NT = 512;                        // 8 waves: 4 along tokens x 2 along rows
+constexpr int PF_ROW = PF_BK;                     // halves per LDS row (no padding: swizzled)
+constexpr int PF_A_BYTES = PF_BM * PF_ROW * 2;    // one activation stage (32 KB)
+constexpr int PF_B_BYTES = PF_BN * PF_ROW * 2;    // one weight stage (16 KB)
+constexpr int PF_OFF_INTS = (int)(kPlanMaxK / kPlanBK + 1);
+constexpr int PF_LDS_BYTES = 2 * PF_A_BYTES + 2 * PF_B_BYTES + PF_OFF_INTS * 4 + PF_NT * 2;
 static_assert(PF_BN == kPlanBN && PF_BK == kPlanBK, "plan tiling must match the kernel");
+static_assert(PF_LDS_BYTES <= 160 * 1024, "prefill LDS budget");
 
-// Registers holding one K-step's global loads for one thread.
-struct StepRegs {
-    u32x4 a[8];       // 8 x 16 bytes of activations
-    u32x4 b;          // 32 nibbles of one weight row
-    f16 s;            // that row's scale for this step
-    uint32_t e0;      // first plan entry of this thread (if any)
-    int32_t ebeg, eend;
+// LDS tiles are rows of 8 chunks of 16 bytes; chunk c of row r sits at
+// c ^ ((r >> 1) & 7), so the 16 rows one ds_read_b128 phase touches (and
+// the 8 chunks of a row one write phase touches) fall in distinct banks.
+__device__ __forceinline__ int pf_swz(int r, int c) { return r * PF_ROW + ((c ^ ((r >> 1) & 7)) << 3); }
+
+// Register sets of the software pipeline: step u's activations, raw
+// weights and plan entries are loaded three steps before they are written
+// to LDS; three statically indexed sets rotate with the step (the loop is
+// unrolled by three), so a load is waited for two steps after its issue.
+struct PfA { u32x4 v[4]; };                       // 256 x 64 fp16 tile: 4 x 16 B per thread
+struct PfB { uint2 v; uint32_t s; };              // 16 nibbles of one weight row + its scale bits
+// (the scale is kept zero-extended in a register of its own: a 16-bit value
+// packed into half of a shared register would be waited for at its load)
+struct PfE { uint32_t e; };                       // this thread's plan entry of the step
+
+struct PfLane {
+    uint32_t xoff[4];  // byte offsets of this thread's activation chunks (step 0)
+    uint32_t qoff;     // byte offset of this thread's weight bytes (step 0)
+    uint32_t soff;     // element offset of this thread's weight row scales
+    int gshift;        // scale group of step u: u >> gshift (G = 64 << gshift; G = K: 31)
+    int arow[4], achunk[4];
 };
 
-__device__ __forceinline__ void prefill_load(const PrefillArgs &a, int t, int64_t m0, int64_t n0,
-                                             const int32_t *off_row, StepRegs &r) {
-    const int tid = threadIdx.x;
-    const int64_t k0 = (int64_t)t * PF_BK;
+__device__ __forceinline__ void pf_load_a(const PrefillArgs &a, const PfLane &L, int u, PfA &r) {
+    const char *base = reinterpret_cast<const char *>(a.x) + (int64_t)u * (PF_BK * 2);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int idx = tid + 256 * i;
-        int64_t m = m0 + (idx >> 3);
-        m = m < a.M ? m : a.M - 1;
-        r.a[i] = *reinterpret_cast<const u32x4 *>(a.x + m * a.K + k0 + (idx & 7) * 8);
-    }
-    int64_t n = n0 + (tid >> 1);
-    n = n < a.N ? n : a.N - 1;
-    r.b = *reinterpret_cast<const u32x4 *>(a.q + n * (a.K >> 1) + (k0 >> 1) + (tid & 1) * 16);
-    r.s = a.scales[n * a.ngroups + k0 / a.G];
-    if (a.fold) {
-        // clamped: a stale or foreign plan can lose the ortho term but never
-        // read outside the entry array
-        r.ebeg = min(max(off_row[t], 0), a.nnz);
-        r.eend = min(max(off_row[t + 1], r.ebeg), a.nnz);
-        const int32_t e = r.ebeg + tid;
-        r.e0 = e < r.eend ? a.entries[e] : 0u;
-    }
+    for (int i = 0; i < 4; i++) r.v[i] = *reinterpret_cast<const u32x4 *>(base + L.xoff[i]);
 }
 
-__device__ __forceinline__ void prefill_store(const StepRegs &r, f16 *As, f16 *Bs) {
-    const int tid = threadIdx.x;
+__device__ __forceinline__ void pf_load_b(const PrefillArgs &a, const PfLane &L, int u, PfB &r) {
+    const char *base = reinterpret_cast<const char *>(a.q) + (int64_t)u * (PF_BK / 2);
+    r.v = *reinterpret_cast<const uint2 *>(base + L.qoff);
+    r.s = reinterpret_cast<const uint16_t *>(a.scales)[L.soff + ((uint32_t)u >> L.gshift)];
+}
+
+// This thread's plan entry for step u (the range comes from the offsets
+// staged in LDS).  Threads past the range read entry 0, always valid when
+// the plan is applied, and drop it.
+__device__ __forceinline__ void pf_load_e(const PrefillArgs &a, const int32_t *offs, int u, PfE &r) {
+    const int32_t e = min(offs[u] + (int32_t)threadIdx.x, a.nnz - 1);
+    r.e = a.entries[max(e, 0)];
+}
+
+__device__ __forceinline__ void pf_store_a(const PfLane &L, const PfA &r, f16 *As) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int idx = tid + 256 * i;
-        *reinterpret_cast<u32x4 *>(As + (idx >> 3) * PF_LDK + (idx & 7) * 8) = r.a[i];
-    }
-    const f16x2 s2 = {r.s, r.s};
-    const uint32_t words[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-    f16 *dst = Bs + (tid >> 1) * PF_LDK + (tid & 1) * 32;
+    for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4 *>(As + pf_swz(L.arow[i], L.achunk[i])) = r.v[i];
+}
+
+__device__ __forceinline__ void pf_store_b(const PfB &r, f16 *Bs) {
+    const f16 sc = __builtin_bit_cast(f16, (uint16_t)r.s);
+    const f16x2 s2 = {sc, sc};
+    const int row = threadIdx.x >> 2, c0 = (threadIdx.x & 3) * 2;
+    const uint32_t words[2] = {r.v.x, r.v.y};
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < 2; j++) {
         uint32_t o[4];
         int4x8_to_f16_scaled(words[j], s2, o);
-        *reinterpret_cast<u32x4 *>(dst + 8 * j) = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<u32x4 *>(Bs + pf_swz(row, c0 + j)) = u32x4{o[0], o[1], o[2], o[3]};
     }
 }
 
-__device__ __forceinline__ void fold_one(f16 *Bs, uint32_t e, float alpha, bool canonical) {
+// Adds alpha * v to the weight cell of entry e; a thread with no entry
+// updates its own trash cell instead, so the common path has no branch.
+__device__ __forceinline__ void fold_fast(f16 *Bs, f16 *trash, uint32_t e, bool valid, float alpha) {
     const int r = (e >> 24) & (PF_BN - 1), c = (e >> 16) & (PF_BK - 1);  // always inside the tile
     const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
-    f16 *p = Bs + r * PF_LDK + c;
+    f16 *p = valid ? Bs + pf_swz(r, c >> 3) + (c & 7) : trash + threadIdx.x;
+    *p = (f16)((float)*p + alpha * v);
+}
+
+// Duplicate (row, col) entries may share a cell: CAS on its 32-bit word
+// (index arithmetic keeps the pointer in the LDS address space).
+__device__ __forceinline__ void fold_cas(f16 *Bs, uint32_t e, float alpha) {
+    const int r = (e >> 24) & (PF_BN - 1), c = (e >> 16) & (PF_BK - 1);
+    const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
+    const int cell = pf_swz(r, c >> 3) + (c & 7);
+    uint32_t *w = reinterpret_cast<uint32_t *>(Bs) + (cell >> 1);
+    const int sh = (cell & 1) ? 16 : 0;
+    uint32_t old = *w, assumed;
+    do {
+        assumed = old;
+        const f16 cur = __builtin_bit_cast(f16, (uint16_t)(assumed >> sh));
+        const uint16_t nv = __builtin_bit_cast(uint16_t, (f16)((float)cur + alpha * v));
+        const uint32_t upd = (assumed & ~(0xffffu << sh)) | ((uint32_t)nv << sh);
+        old = atomicCAS(w, assumed, upd);
+    } while (old != assumed);
+}
+
+// Folds step u's plan entries into the weight stage Bs.  The first 512
+// entries come from the prefetched register; a step with more (dense rows,
+// skewed outliers) reads the rest here.
+__device__ __forceinline__ void pf_fold(const PrefillArgs &a, const int32_t *offs, int u, const PfE &r,
+                                        f16 *Bs, f16 *trash, bool canonical) {
+    const int tid = threadIdx.x;
+    const int32_t lo = offs[u], hi = offs[u + 1];
     if (canonical) {
-        *p = (f16)((float)*p + alpha * v);
+        fold_fast(Bs, trash, r.e, lo + tid < hi, a.alpha);
+        // canonical entries are distinct cells: no ordering between passes
+        if (hi - lo > PF_NT)
+            for (int32_t e = lo + PF_NT + tid; e < hi; e += PF_NT) fold_fast(Bs, trash, a.entries[e], true, a.alpha);
     } else {
-        // duplicate (row, col) entries may share a cell: CAS on its 32-bit word
-        uint32_t *w = reinterpret_cast<uint32_t *>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
-        const int sh = (reinterpret_cast<uintptr_t>(p) & 2) ? 16 : 0;
-        uint32_t old = *w, assumed;
-        do {
-            assumed = old;
-            const f16 cur = __builtin_bit_cast(f16, (uint16_t)(assumed >> sh));
-            const uint16_t nv = __builtin_bit_cast(uint16_t, (f16)((float)cur + alpha * v));
-            const uint32_t upd = (assumed & ~(0xffffu << sh)) | ((uint32_t)nv << sh);
-            old = atomicCAS(w, assumed, upd);
-        } while (old != assumed);
+        if (lo + tid < hi) fold_cas(Bs, r.e, a.alpha);
+        for (int32_t e = lo + PF_NT + tid; e < hi; e += PF_NT) fold_cas(Bs, a.entries[e], a.alpha);
     }
 }
 
-__device__ __forceinline__ void prefill_fold(const PrefillArgs &a, const StepRegs &r, f16 *Bs,
-                                             bool canonical) {
-    const int tid = threadIdx.x;
-    if (r.ebeg + tid < r.eend) fold_one(Bs, r.e0, a.alpha, canonical);
-    for (int32_t e = r.ebeg + tid + 256; e < r.eend; e += 256) fold_one(Bs, a.entries[e], a.alpha, canonical);
-}
-
-__device__ __forceinline__ void prefill_mfma(const f16 *As, const f16 *Bs, int wm, int wn,
-                                             f32x16 (&acc)[4][2]) {
+__device__ __forceinline__ void pf_mfma(const f16 *As, const f16 *Bs, int wm, int wn,
+                                        f32x16 (&acc)[2][2]) {
     const int lane = threadIdx.x & 63;
-    const int lr = lane & 31, lk = (lane >> 5) * 8;
+    const int lr = lane & 31, kh = lane >> 5;
 #pragma unroll
     for (int s = 0; s < PF_BK / 16; s++) {
-        f16x8 af[4], bf[2];
+        f16x8 af[2], bf[2];
 #pragma unroll
-        for (int bm = 0; bm < 4; bm++)
-            af[bm] = *reinterpret_cast<const f16x8 *>(As + (wm * 128 + bm * 32 + lr) * PF_LDK + s * 16 + lk);
+        for (int bm = 0; bm < 2; bm++)
+            af[bm] = *reinterpret_cast<const f16x8 *>(As + pf_swz(wm * 64 + bm * 32 + lr, 2 * s + kh));
 #pragma unroll
         for (int bn = 0; bn < 2; bn++)
-            bf[bn] = *reinterpret_cast<const f16x8 *>(Bs + (wn * 64 + bn * 32 + lr) * PF_LDK + s * 16 + lk);
+            bf[bn] = *reinterpret_cast<const f16x8 *>(Bs + pf_swz(wn * 64 + bn * 32 + lr, 2 * s + kh));
 #pragma unroll
-        for (int bm = 0; bm < 4; bm++)
+        for (int bm = 0; bm < 2; bm++)
 #pragma unroll
             for (int bn = 0; bn < 2; bn++)
                 acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[bm], bf[bn], acc[bm][bn], 0, 0, 0);
     }
 }
 
-__global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
+// One pipeline step t (J = t mod 3, static): issue the loads of step t+3;
+// write step t+1's activations and dequantised weights to the free stages;
+// barrier; fold step t+1's plan entries into its weight stage while the
+// MFMAs consume step t's stages; barrier.
+template <bool FOLD, int J>
+__device__ __forceinline__ void pf_step(const PrefillArgs &a, const PfLane &L, int t, int nk, int wm,
+                                        int wn, f16 *As0, f16 *Bs0, const int32_t *offs, f16 *trash,
+                                        bool canonical, PfA (&ra)[3], PfB (&rb)[3], PfE (&re)[3],
+                                        f32x16 (&acc)[2][2]) {
+    constexpr int J1 = (J + 1) % 3;
+    // keep the scheduler from hoisting a later step's register work (which
+    // would wait for younger loads) above this step's barriers
+    __builtin_amdgcn_sched_barrier(0);
+    const int u = min(t + 3, nk - 1);
+    pf_load_a(a, L, u, ra[J]);
+    pf_load_b(a, L, u, rb[J]);
+    if (FOLD) pf_load_e(a, offs, u, re[J]);
+    f16 *A_n = As0 + ((t + 1) & 1) * (PF_A_BYTES / 2), *B_n = Bs0 + ((t + 1) & 1) * (PF_B_BYTES / 2);
+    pf_store_a(L, ra[J1], A_n);
+    pf_store_b(rb[J1], B_n);
+    __syncthreads();
+    if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_n, trash, canonical);
+    pf_mfma(As0 + (t & 1) * (PF_A_BYTES / 2), Bs0 + (t & 1) * (PF_B_BYTES / 2), wm, wn, acc);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool FOLD>
+__global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    // buffer i of the activation / weight tiles
-    auto As = [&](int i) { return reinterpret_cast<f16 *>(smem + i * PF_A_BYTES); };
-    auto Bs = [&](int i) { return reinterpret_cast<f16 *>(smem + 2 * PF_A_BYTES + i * PF_B_BYTES); };
+    f16 *As0 = reinterpret_cast<f16 *>(smem);
+    f16 *Bs0 = reinterpret_cast<f16 *>(smem + 2 * PF_A_BYTES);
+    int32_t *offs = reinterpret_cast<int32_t *>(smem + 2 * PF_A_BYTES + 2 * PF_B_BYTES);
+    f16 *trash = reinterpret_cast<f16 *>(offs + PF_OFF_INTS);
 
     // XCD-aware tile order: workgroup ids are dealt round-robin to the 8
     // XCDs; give each XCD a contiguous run of tiles (N-block fastest).
@@ -350,54 +408,92 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
     const int bm_i = tile / a.nbn, bn_i = tile - bm_i * a.nbn;
     const int64_t m0 = (int64_t)bm_i * PF_BM, n0 = (int64_t)bn_i * PF_BN;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int nk = (int)(a.K / PF_BK);
-    const int32_t *off_row = a.fold ? a.offsets + (int64_t)bn_i * (nk + 1) : nullptr;
-    if (a.fold) {
-        // a plan built for another layer shape is ignored rather than trusted
-        const PlanHeader *h = a.plan;
-        if (h->magic != kPlanMagic || h->version != kPlanVersion || h->n != a.N || h->k != a.K ||
-            h->nnz != a.nnz)
-            a.fold = 0;
-    }
-    const bool canonical = !a.fold || (a.plan->flags & kPlanNonCanonical) == 0;
 
-    f32x16 acc[4][2];
+    // per-thread offsets, fixed for the whole K loop (rows past M / N repeat
+    // the last row; their outputs are never stored)
+    PfLane L;
 #pragma unroll
-    for (int bm = 0; bm < 4; bm++)
+    for (int i = 0; i < 4; i++) {
+        const int idx = tid + PF_NT * i;
+        L.arow[i] = idx >> 3;
+        L.achunk[i] = idx & 7;
+        const int64_t m = min(m0 + L.arow[i], a.M - 1);
+        L.xoff[i] = (uint32_t)((m * a.K + L.achunk[i] * 8) * 2);
+    }
+    {
+        const int64_t n = min(n0 + (tid >> 2), a.N - 1);
+        L.qoff = (uint32_t)(n * (a.K >> 1) + (tid & 3) * 8);
+        L.soff = (uint32_t)(n * a.ngroups);
+        L.gshift = a.ngroups == 1 ? 31 : __builtin_ctzll(a.G / PF_BK);
+    }
+
+    bool canonical = true;
+    if (FOLD) {
+        // the plan's offsets of this tile's row block, clamped to [0, nnz]:
+        // a stale or foreign plan can lose the ortho term but never makes a
+        // read outside the entry array (a pair with hi < lo is an empty step,
+        // and every entry lands inside the tile).  A plan built for another
+        // layer shape is ignored rather than trusted.
+        const PlanHeader *h = a.plan;
+        const bool ok = h->magic == kPlanMagic && h->version == kPlanVersion && h->n == a.N &&
+                        h->k == a.K && h->nnz == a.nnz;
+        for (int i = tid; i <= nk; i += PF_NT)
+            offs[i] = ok ? min(max(a.offsets[(int64_t)bn_i * (nk + 1) + i], 0), a.nnz) : 0;
+        canonical = !ok || (h->flags & kPlanNonCanonical) == 0;
+        __syncthreads();
+    }
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int bm = 0; bm < 2; bm++)
 #pragma unroll
         for (int bn = 0; bn < 2; bn++)
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[bm][bn][i] = 0.f;
 
-    StepRegs r;
-    prefill_load(a, 0, m0, n0, off_row, r);
-    prefill_store(r, As(0), Bs(0));
+    // prologue: step 0 in its stages (folded); steps 1 and 2 in flight
+    PfA ra[3];
+    PfB rb[3];
+    PfE re[3];
+    pf_load_a(a, L, 0, ra[0]);
+    pf_load_b(a, L, 0, rb[0]);
+    if (FOLD) pf_load_e(a, offs, 0, re[0]);
+    pf_store_a(L, ra[0], As0);
+    pf_store_b(rb[0], Bs0);
     __syncthreads();
-    if (a.fold) prefill_fold(a, r, Bs(0), canonical);
+    if (FOLD) pf_fold(a, offs, 0, re[0], Bs0, trash, canonical);
+    pf_load_a(a, L, min(1, nk - 1), ra[1]);
+    pf_load_b(a, L, min(1, nk - 1), rb[1]);
+    pf_load_a(a, L, min(2, nk - 1), ra[2]);
+    pf_load_b(a, L, min(2, nk - 1), rb[2]);
+    if (FOLD) {
+        pf_load_e(a, offs, min(1, nk - 1), re[1]);
+        pf_load_e(a, offs, min(2, nk - 1), re[2]);
+    }
     __syncthreads();
 
-    for (int t = 0; t < nk; t++) {
-        const int cb = t & 1, nb = cb ^ 1;
-        const bool more = t + 1 < nk;
-        if (more) prefill_load(a, t + 1, m0, n0, off_row, r);
-        prefill_mfma(As(cb), Bs(cb), wm, wn, acc);
-        if (more) prefill_store(r, As(nb), Bs(nb));
-        __syncthreads();
-        if (more && a.fold) prefill_fold(a, r, Bs(nb), canonical);
-        __syncthreads();
+    int t = 0;
+    for (; t + 3 <= nk; t += 3) {
+        pf_step<FOLD, 0>(a, L, t, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
+        pf_step<FOLD, 1>(a, L, t + 1, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
+        pf_step<FOLD, 2>(a, L, t + 2, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
     }
+    if (t < nk) pf_step<FOLD, 0>(a, L, t, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
+    if (t + 1 < nk) pf_step<FOLD, 1>(a, L, t + 1, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
 
     // epilogue: lane holds D[token 8(i/4) + 4(lane/32) + i%4][row lane%32]
+    const int lane = tid & 63;
 #pragma unroll
-    for (int bm = 0; bm < 4; bm++) {
+    for (int bm = 0; bm < 2; bm++) {
 #pragma unroll
         for (int bn = 0; bn < 2; bn++) {
             const int64_t n = n0 + wn * 64 + bn * 32 + (lane & 31);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const int64_t m = m0 + wm * 128 + bm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                const int64_t m = m0 + wm * 64 + bm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
                 if (m < a.M && n < a.N) a.y[m * a.N + n] = (f16)acc[bm][bn][i];
             }
         }
@@ -407,9 +503,12 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillArgs a) {
 bool prefill_supported(const ForwardArgs &a) {
     if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
     if (a.K % PF_BK != 0) return false;
-    if (a.ngroups != 1 && a.G % PF_BK != 0) return false;
+    if (a.ngroups != 1 && (a.G % PF_BK != 0 || ((a.G / PF_BK) & (a.G / PF_BK - 1)) != 0)) return false;
     if (a.has_ortho && !plan_supported(a)) return false;
     if ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.x)) & 15) return false;
+    // per-lane 32-bit byte offsets into x and q
+    if (a.M * a.K * 2 > (int64_t)UINT32_MAX || a.N * (a.K / 2) > (int64_t)UINT32_MAX) return false;
+    if (a.N * a.ngroups > (int64_t)UINT32_MAX) return false;
     const int64_t nbm = (a.M + PF_BM - 1) / PF_BM, nbn = (a.N + PF_BN - 1) / PF_BN;
     if (nbm * nbn > ((int64_t)1 << 31) - 1) return false;
     return true;
@@ -438,7 +537,12 @@ hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t st
     p.nbm = (int)((a.M + PF_BM - 1) / PF_BM);
     p.nbn = (int)((a.N + PF_BN - 1) / PF_BN);
     const unsigned blocks = (unsigned)(p.nbm * p.nbn);
-    hipLaunchKernelGGL(prefill_kernel, dim3(blocks), dim3(256), PF_LDS_BYTES, stream, p);
+    if (p.fold) {
+        if (p.nnz <= 0) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(prefill_kernel<true>, dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    } else {
+        hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    }
     return hipGetLastError();
 }
 
@@ -448,7 +552,10 @@ namespace orth {
 
 // Kernels that use more than 64 KB of dynamic LDS must say so per device.
 hipError_t prefill_prepare_device() {
-    return hipFuncSetAttribute(reinterpret_cast<const void *>(prefill_kernel),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(prefill_kernel<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS_BYTES);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(prefill_kernel<false>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS_BYTES);
 }
 
