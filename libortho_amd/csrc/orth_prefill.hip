@@ -234,7 +234,11 @@ constexpr int PF_ROW = PF_BK;                     // halves per LDS row (no padd
 constexpr int PF_A_BYTES = PF_BM * PF_ROW * 2;    // one activation stage (32 KB)
 constexpr int PF_B_BYTES = PF_BN * PF_ROW * 2;    // one weight stage (16 KB)
 constexpr int PF_OFF_INTS = (int)(kPlanMaxK / kPlanBK + 1);
-constexpr int PF_LDS_BYTES = 2 * PF_A_BYTES + 2 * PF_B_BYTES + PF_OFF_INTS * 4 + PF_NT * 2;
+constexpr int PF_A_STAGES = 2, PF_B_STAGES = 3;
+constexpr int PF_B_AT = PF_A_STAGES * PF_A_BYTES;              // LDS byte offsets of the regions
+constexpr int PF_OFF_AT = PF_B_AT + PF_B_STAGES * PF_B_BYTES;  // plan offsets of the tile's block
+constexpr int PF_TRASH_AT = PF_OFF_AT + PF_OFF_INTS * 4;       // one fold cell per thread
+constexpr int PF_LDS_BYTES = PF_TRASH_AT + PF_NT * 2;
 static_assert(PF_BN == kPlanBN && PF_BK == kPlanBK, "plan tiling must match the kernel");
 static_assert(PF_LDS_BYTES <= 160 * 1024, "prefill LDS budget");
 
@@ -243,10 +247,11 @@ static_assert(PF_LDS_BYTES <= 160 * 1024, "prefill LDS budget");
 // the 8 chunks of a row one write phase touches) fall in distinct banks.
 __device__ __forceinline__ int pf_swz(int r, int c) { return r * PF_ROW + ((c ^ ((r >> 1) & 7)) << 3); }
 
-// Register sets of the software pipeline: step u's activations, raw
-// weights and plan entries are loaded three steps before they are written
-// to LDS; three statically indexed sets rotate with the step (the loop is
-// unrolled by three), so a load is waited for two steps after its issue.
+// Register sets of the software pipeline: step u's activations and plan
+// entries are loaded three steps before they are written to LDS / folded,
+// its raw weights four steps before they are dequantised; three statically
+// indexed sets of each rotate with the step (the loop is unrolled by
+// three), so a load is waited for two steps after its issue.
 struct PfA { u32x4 v[4]; };                       // 256 x 64 fp16 tile: 4 x 16 B per thread
 struct PfB { uint2 v; uint32_t s; };              // 16 nibbles of one weight row + its scale bits
 // (the scale is kept zero-extended in a register of its own: a 16-bit value
@@ -277,7 +282,7 @@ __device__ __forceinline__ void pf_load_b(const PrefillArgs &a, const PfLane &L,
 // staged in LDS).  Threads past the range read entry 0, always valid when
 // the plan is applied, and drop it.
 __device__ __forceinline__ void pf_load_e(const PrefillArgs &a, const int32_t *offs, int u, PfE &r) {
-    const int32_t e = min(offs[u] + (int32_t)threadIdx.x, a.nnz - 1);
+    const int32_t e = min(max(offs[u], 0) + (int32_t)threadIdx.x, a.nnz - 1);
     r.e = a.entries[max(e, 0)];
 }
 
@@ -332,7 +337,9 @@ __device__ __forceinline__ void fold_cas(f16 *Bs, uint32_t e, float alpha) {
 __device__ __forceinline__ void pf_fold(const PrefillArgs &a, const int32_t *offs, int u, const PfE &r,
                                         f16 *Bs, f16 *trash, bool canonical) {
     const int tid = threadIdx.x;
-    const int32_t lo = offs[u], hi = offs[u + 1];
+    // (the staged offsets are already within [0, nnz]; clamping again keeps
+    // every entry read in bounds whatever the LDS holds)
+    const int32_t lo = max(offs[u], 0), hi = min(offs[u + 1], a.nnz);
     if (canonical) {
         fold_fast(Bs, trash, r.e, lo + tid < hi, a.alpha);
         // canonical entries are distinct cells: no ordering between passes
@@ -365,29 +372,29 @@ __device__ __forceinline__ void pf_mfma(const f16 *As, const f16 *Bs, int wm, in
     }
 }
 
-// One pipeline step t (J = t mod 3, static): issue the loads of step t+3;
-// write step t+1's activations and dequantised weights to the free stages;
-// barrier; fold step t+1's plan entries into its weight stage while the
-// MFMAs consume step t's stages; barrier.
+// One pipeline step t (J = t mod 3, static): issue the loads of steps t+3
+// (activations, plan entries) and t+4 (weights); write step t+1's
+// activations, dequantise step t+2's weights and fold step t+1's plan
+// entries (its weights were written one step ago) while the MFMAs consume
+// step t's stages; one barrier.  Activations use two LDS stages, weights
+// three, so no write touches a stage being read.
 template <bool FOLD, int J>
 __device__ __forceinline__ void pf_step(const PrefillArgs &a, const PfLane &L, int t, int nk, int wm,
                                         int wn, f16 *As0, f16 *Bs0, const int32_t *offs, f16 *trash,
                                         bool canonical, PfA (&ra)[3], PfB (&rb)[3], PfE (&re)[3],
                                         f32x16 (&acc)[2][2]) {
-    constexpr int J1 = (J + 1) % 3;
+    constexpr int J1 = (J + 1) % 3, J2 = (J + 2) % 3;
     // keep the scheduler from hoisting a later step's register work (which
-    // would wait for younger loads) above this step's barriers
+    // would wait for younger loads) above this step's barrier
     __builtin_amdgcn_sched_barrier(0);
-    const int u = min(t + 3, nk - 1);
-    pf_load_a(a, L, u, ra[J]);
-    pf_load_b(a, L, u, rb[J]);
-    if (FOLD) pf_load_e(a, offs, u, re[J]);
-    f16 *A_n = As0 + ((t + 1) & 1) * (PF_A_BYTES / 2), *B_n = Bs0 + ((t + 1) & 1) * (PF_B_BYTES / 2);
-    pf_store_a(L, ra[J1], A_n);
-    pf_store_b(rb[J1], B_n);
-    __syncthreads();
-    if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_n, trash, canonical);
-    pf_mfma(As0 + (t & 1) * (PF_A_BYTES / 2), Bs0 + (t & 1) * (PF_B_BYTES / 2), wm, wn, acc);
+    pf_load_a(a, L, min(t + 3, nk - 1), ra[J]);
+    pf_load_b(a, L, min(t + 4, nk - 1), rb[J1]);
+    if (FOLD) pf_load_e(a, offs, min(t + 3, nk - 1), re[J]);
+    f16 *B_t = Bs0 + J * (PF_B_BYTES / 2), *B_1 = Bs0 + J1 * (PF_B_BYTES / 2), *B_2 = Bs0 + J2 * (PF_B_BYTES / 2);
+    pf_store_a(L, ra[J1], As0 + ((t + 1) & 1) * (PF_A_BYTES / 2));
+    pf_store_b(rb[J2], B_2);
+    if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_1, trash, canonical);
+    pf_mfma(As0 + (t & 1) * (PF_A_BYTES / 2), B_t, wm, wn, acc);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
 }
@@ -396,9 +403,9 @@ template <bool FOLD>
 __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     f16 *As0 = reinterpret_cast<f16 *>(smem);
-    f16 *Bs0 = reinterpret_cast<f16 *>(smem + 2 * PF_A_BYTES);
-    int32_t *offs = reinterpret_cast<int32_t *>(smem + 2 * PF_A_BYTES + 2 * PF_B_BYTES);
-    f16 *trash = reinterpret_cast<f16 *>(offs + PF_OFF_INTS);
+    f16 *Bs0 = reinterpret_cast<f16 *>(smem + PF_B_AT);
+    int32_t *offs = reinterpret_cast<int32_t *>(smem + PF_OFF_AT);
+    f16 *trash = reinterpret_cast<f16 *>(smem + PF_TRASH_AT);
 
     // XCD-aware tile order: workgroup ids are dealt round-robin to the 8
     // XCDs; give each XCD a contiguous run of tiles (N-block fastest).
@@ -454,25 +461,31 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[bm][bn][i] = 0.f;
 
-    // prologue: step 0 in its stages (folded); steps 1 and 2 in flight
+    // prologue: step 0 in its stages (folded), step 1's weights dequantised;
+    // activations 1, 2, weights 2, 3 and plan entries 1, 2 in flight
     PfA ra[3];
     PfB rb[3];
     PfE re[3];
     pf_load_a(a, L, 0, ra[0]);
     pf_load_b(a, L, 0, rb[0]);
+    pf_load_b(a, L, min(1, nk - 1), rb[1]);
     if (FOLD) pf_load_e(a, offs, 0, re[0]);
     pf_store_a(L, ra[0], As0);
     pf_store_b(rb[0], Bs0);
+    pf_store_b(rb[1], Bs0 + PF_B_BYTES / 2);
     __syncthreads();
     if (FOLD) pf_fold(a, offs, 0, re[0], Bs0, trash, canonical);
+    // (issued in the loop's own order, so the wait counts at the loop head
+    // are the same from the prologue as from the back edge)
+    __builtin_amdgcn_sched_barrier(0);
     pf_load_a(a, L, min(1, nk - 1), ra[1]);
-    pf_load_b(a, L, min(1, nk - 1), rb[1]);
-    pf_load_a(a, L, min(2, nk - 1), ra[2]);
     pf_load_b(a, L, min(2, nk - 1), rb[2]);
-    if (FOLD) {
-        pf_load_e(a, offs, min(1, nk - 1), re[1]);
-        pf_load_e(a, offs, min(2, nk - 1), re[2]);
-    }
+    if (FOLD) pf_load_e(a, offs, min(1, nk - 1), re[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_load_a(a, L, min(2, nk - 1), ra[2]);
+    pf_load_b(a, L, min(3, nk - 1), rb[0]);
+    if (FOLD) pf_load_e(a, offs, min(2, nk - 1), re[2]);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
 
     int t = 0;
