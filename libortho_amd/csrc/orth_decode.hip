@@ -298,32 +298,54 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     }
     __syncthreads();  // every wave's activation chunks and the CSR block are in LDS
 
-    // ---- sparse ortho term: 16 lanes per output row
+    // ---- sparse ortho term: 16 lanes per output row.  Entries staged in
+    //      LDS are taken four per lane per pass: their column/value reads,
+    //      then their activation reads, are issued together (one LDS or L2
+    //      round trip each instead of one per entry); entries past the
+    //      staged block (very dense rows) are read from memory one by one.
     if (SPARSE) {
-        // entries [eb, staged_hi) sit in LDS; the rest are read from memory
+        constexpr int U = 4;
         const int32_t staged_hi = SPARSE == 1 ? min(min(eb + kDecodeEStaged, last4 + 4), e1) : eb;
+        const int32_t fast_hi = min(re, staged_hi);
         float sacc[MT];
 #pragma unroll
         for (int m = 0; m < MT; m++) sacc[m] = 0.f;
-        for (int32_t j = rs + sub; j < re; j += 16) {
-            int32_t c;
-            float v;
-            if (j >= eb && j < staged_hi) {
-                c = ec[j - eb];
-                v = (float)ev[j - eb];
-            } else {
-                c = a.col[j];
-                v = (float)a.vals[j];
+        for (int32_t j0 = rs + sub; j0 < fast_hi; j0 += 16 * U) {
+            int32_t c[U];
+            float v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int32_t j = j0 + 16 * u;
+                const int32_t li = min(j, fast_hi - 1) - eb;  // in [0, kDecodeEStaged)
+                c[u] = ec[li];
+                v[u] = (j < fast_hi) ? (float)ev[li] : 0.f;
             }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const bool ok = c[u] >= 0 && c[u] < K;
+                const int cc = ok ? c[u] : 0;
+                const float vv = ok ? v[u] : 0.f;
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    float xv;
+                    if (XLDS) xv = (float)xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))];
+                    else xv = (float)a.x[(int64_t)min(m, a.M - 1) * K + cc];
+                    sacc[m] += vv * xv;
+                }
+            }
+        }
+        // first entry of this lane's residue class (mod 16) at or past fast_hi
+        const int32_t d = fast_hi - (rs + sub);
+        for (int32_t j = rs + sub + (d > 0 ? (d + 15) / 16 * 16 : 0); j < re; j += 16) {
+            const int32_t c = a.col[j];
+            const float v = (float)a.vals[j];
             if (c >= 0 && c < K) {
 #pragma unroll
                 for (int m = 0; m < MT; m++) {
-                    if (m < a.M) {
-                        float xv;
-                        if (XLDS) xv = (float)xs[m * a.xstride + ((c & ~7) | interleaved_pos(c & 7))];
-                        else xv = (float)a.x[(int64_t)m * K + c];
-                        sacc[m] += v * xv;
-                    }
+                    float xv;
+                    if (XLDS) xv = (float)xs[m * a.xstride + ((c & ~7) | interleaved_pos(c & 7))];
+                    else xv = (float)a.x[(int64_t)min(m, a.M - 1) * K + c];
+                    sacc[m] += v * xv;
                 }
             }
         }
