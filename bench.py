@@ -314,7 +314,9 @@ def main():
     secondary = []
     if not args.no_secondary:
         for m in (2, 4, 8, 16):
-            rr = time_workload(torch, layer, m, alpha, args.steps, 10)
+            # from 5 tokens the mid-batch kernel reads the cached ortho plan,
+            # as OrthoLinear passes it
+            rr = time_workload(torch, layer, m, alpha, args.steps, 10, plan=m >= 5)
             b = W.algorithmic_bytes(layer, m, alpha)
             secondary.append({"workload": f"c2 M={m}", "kernel": rr["kernel"],
                               "us_per_step": round(rr["ms_per_step"] * 1e3, 3),

@@ -184,7 +184,8 @@ def dequant(q_weight, q_scales, in_features: int) -> torch.Tensor:
 
 
 def last_kernel() -> str:
-    """Kernel used by this thread's last forward: decode, prefill or general."""
+    """Kernel used by this thread's last forward: decode, skinny (5..64
+    tokens), prefill or general."""
     return _lib.last_kernel()
 
 

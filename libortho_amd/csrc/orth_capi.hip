@@ -11,9 +11,13 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "orth_common.h"
 
@@ -30,6 +34,9 @@ hipError_t plan_read_flags(const void *plan, hipStream_t stream, uint32_t *flags
 hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream);
 hipError_t prefill_prepare_device();
 hipError_t plan_prepare_device();
+bool skinny_supported(const ForwardArgs &a);
+int64_t skinny_workspace_bytes(const ForwardArgs &a, int cus);
+hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float *part, hipStream_t stream);
 }  // namespace orth
 
 using namespace orth;
@@ -45,6 +52,7 @@ int policy_from_env() {
     if (!std::strcmp(e, "decode")) return 1;
     if (!std::strcmp(e, "prefill")) return 2;
     if (!std::strcmp(e, "general")) return 3;
+    if (!std::strcmp(e, "skinny")) return 4;
     return 0;
 }
 
@@ -137,6 +145,7 @@ int resolve(const orth_hip_layer_t *L, const void *input, void *output, int64_t 
 // this library carries) and one-time kernel attribute set-up.
 struct DeviceState {
     int checked = 0;  // 0 unknown, 1 ok, -1 not gfx950
+    int cus = 256;
     char arch[64] = {0};
 };
 std::mutex g_dev_mu;
@@ -156,6 +165,7 @@ int current_device_ok(int *dev_out) {
             e = hipGetDeviceProperties(&p, dev);
             if (e != hipSuccess) return fail_hip(e, "hipGetDeviceProperties");
             std::snprintf(st.arch, sizeof(st.arch), "%s", p.gcnArchName);
+            st.cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
             const bool ok = std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
             if (ok) {
                 e = prefill_prepare_device();
@@ -171,6 +181,60 @@ int current_device_ok(int *dev_out) {
     return ORTH_OK;
 }
 
+// Split-K workspace of the mid-batch kernel, one per (device, stream): the
+// FP32 partials its reduction kernel sums.  Calls on one stream are ordered;
+// calls on different streams use different workspaces.  Allocation happens
+// on first use (and on growth) outside graph capture.  A stream captured
+// before it has a workspace borrows the device's largest one, so its graph
+// must not replay concurrently with calls on the stream that owns it.
+struct Workspace {
+    void *buf = nullptr;
+    int64_t part_bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, void *>, Workspace> g_ws;
+std::vector<void *> g_ws_retired;
+
+int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto it = g_ws.find({dev, static_cast<void *>(stream)});
+    if (it != g_ws.end() && it->second.buf && it->second.part_bytes >= part_bytes) {
+        *part = static_cast<float *>(it->second.buf);
+        return ORTH_OK;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return fail_hip(e, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone) {
+        // nothing can be allocated while a stream is captured: borrow the
+        // largest workspace of this device (frameworks capture on streams of
+        // their own, after eager warm-up calls on another)
+        const Workspace *best = nullptr;
+        for (const auto &kv : g_ws)
+            if (kv.first.first == dev && kv.second.buf && kv.second.part_bytes >= part_bytes &&
+                (!best || kv.second.part_bytes > best->part_bytes))
+                best = &kv.second;
+        if (!best)
+            return fail(ORTH_ERR_UNSUPPORTED,
+                        "the mid-batch kernel needs a %lld-byte workspace; run the call once outside "
+                        "graph capture first", (long long)part_bytes);
+        *part = static_cast<float *>(best->buf);
+        return ORTH_OK;
+    }
+    Workspace &w = g_ws[{dev, static_cast<void *>(stream)}];
+    if (w.buf) {
+        // a smaller buffer is retired, not freed: in-flight work or a
+        // captured graph may still use it
+        g_ws_retired.push_back(w.buf);
+        w = Workspace();
+    }
+    e = hipMalloc(&w.buf, (size_t)part_bytes);
+    if (e != hipSuccess) return fail_hip(e, "hipMalloc (mid-batch workspace)");
+    w.part_bytes = part_bytes;
+    *part = static_cast<float *>(w.buf);
+    return ORTH_OK;
+}
+
 int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
                  const void *input, void *output, int64_t batch, int32_t io_dtype, void *stream_v) {
     ForwardArgs a;
@@ -183,13 +247,18 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
         t_last_kernel = KERNEL_NONE;
         return ORTH_OK;
     }
-    rc = current_device_ok(nullptr);
+    int dev = 0;
+    rc = current_device_ok(&dev);
     if (rc != ORTH_OK) return rc;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
 
     const int policy = g_policy.load(std::memory_order_relaxed);
     const bool dec_ok = decode_supported(a);
     const bool pre_ok = prefill_supported(a);
+    // the mid-batch kernel needs an ortho plan for the ortho term; without
+    // one, batches the decode kernel takes go there (no plan to build)
+    const bool sk_ok = skinny_supported(a) && (!a.has_ortho || plan_supported(a));
+    const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok);
     int kernel;
     switch (policy) {
         case 1:
@@ -203,13 +272,41 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
         case 3:
             kernel = KERNEL_GENERAL;
             break;
+        case 4:
+            if (!sk_ok) return fail(ORTH_ERR_UNSUPPORTED, "mid-batch kernel forced but it cannot take this call");
+            kernel = KERNEL_SKINNY;
+            break;
         default:
-            kernel = dec_ok ? KERNEL_DECODE : (pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL);
+            if (dec_ok && a.M <= 4) kernel = KERNEL_DECODE;
+            else if (sk_pref) kernel = KERNEL_SKINNY;
+            else if (dec_ok) kernel = KERNEL_DECODE;
+            else kernel = pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL;
     }
 
     hipError_t e = hipSuccess;
     if (kernel == KERNEL_DECODE) {
         e = launch_decode(a, stream);
+    } else if (kernel == KERNEL_SKINNY) {
+        const int cus = g_dev[dev].cus;
+        const int64_t pbytes = skinny_workspace_bytes(a, cus);
+        float *part = nullptr;
+        if (pbytes > 0) {
+            rc = workspace_for(dev, stream, pbytes, &part);
+            if (rc != ORTH_OK) return rc;
+        }
+        if (a.has_ortho && !plan) {
+            // stream-ordered temporary plan, as for the prefill kernel
+            const int64_t pb = plan_bytes_for(a.N, a.K, a.nnz);
+            void *tmp = nullptr;
+            e = hipMallocAsync(&tmp, (size_t)pb, stream);
+            if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (temporary ortho plan)");
+            e = launch_plan_build(a, tmp, stream);
+            if (e == hipSuccess) e = launch_skinny(a, tmp, cus, part, stream);
+            hipError_t f = hipFreeAsync(tmp, stream);
+            if (e == hipSuccess) e = f;
+        } else {
+            e = launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
+        }
     } else if (kernel == KERNEL_PREFILL) {
         if (a.has_ortho && !plan) {
             // stream-ordered temporary plan: allocated, built, used and freed
@@ -332,7 +429,7 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info) {
 }
 
 int orth_hip_set_kernel_policy(int policy) {
-    if (policy < 0 || policy > 3) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..3");
+    if (policy < 0 || policy > 4) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..4");
     g_policy.store(policy);
     return ORTH_OK;
 }

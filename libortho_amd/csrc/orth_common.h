@@ -22,7 +22,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Which kernel served a forward call (orth_hip_last_kernel()).
-enum KernelId { KERNEL_NONE = 0, KERNEL_DECODE = 1, KERNEL_PREFILL = 2, KERNEL_GENERAL = 3 };
+enum KernelId { KERNEL_NONE = 0, KERNEL_DECODE = 1, KERNEL_PREFILL = 2, KERNEL_GENERAL = 3, KERNEL_SKINNY = 4 };
 
 // Everything a forward launch needs, resolved on the host.
 struct ForwardArgs {

@@ -351,32 +351,25 @@ __device__ __forceinline__ void pf_fold(const PrefillArgs &a, const int32_t *off
     }
 }
 
-// The MFMA operands of one K step: for each 16-wide k slice s, this lane's
-// 8 activations of token blocks bm and 8 weights of row blocks bn.
-struct PfFrag { f16x8 a[PF_BK / 16][2], b[PF_BK / 16][2]; };
-
-__device__ __forceinline__ void pf_frag_load(const f16 *As, const f16 *Bs, int wm, int wn, PfFrag &f) {
+__device__ __forceinline__ void pf_mfma(const f16 *As, const f16 *Bs, int wm, int wn,
+                                        f32x16 (&acc)[2][2]) {
     const int lane = threadIdx.x & 63;
     const int lr = lane & 31, kh = lane >> 5;
 #pragma unroll
     for (int s = 0; s < PF_BK / 16; s++) {
+        f16x8 af[2], bf[2];
 #pragma unroll
         for (int bm = 0; bm < 2; bm++)
-            f.a[s][bm] = *reinterpret_cast<const f16x8 *>(As + pf_swz(wm * 64 + bm * 32 + lr, 2 * s + kh));
+            af[bm] = *reinterpret_cast<const f16x8 *>(As + pf_swz(wm * 64 + bm * 32 + lr, 2 * s + kh));
 #pragma unroll
         for (int bn = 0; bn < 2; bn++)
-            f.b[s][bn] = *reinterpret_cast<const f16x8 *>(Bs + pf_swz(wn * 64 + bn * 32 + lr, 2 * s + kh));
-    }
-}
-
-__device__ __forceinline__ void pf_mfma(const PfFrag &f, f32x16 (&acc)[2][2]) {
-#pragma unroll
-    for (int s = 0; s < PF_BK / 16; s++)
+            bf[bn] = *reinterpret_cast<const f16x8 *>(Bs + pf_swz(wn * 64 + bn * 32 + lr, 2 * s + kh));
 #pragma unroll
         for (int bm = 0; bm < 2; bm++)
 #pragma unroll
             for (int bn = 0; bn < 2; bn++)
-                acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[s][bm], f.b[s][bn], acc[bm][bn], 0, 0, 0);
+                acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[bm], bf[bn], acc[bm][bn], 0, 0, 0);
+    }
 }
 
 // One pipeline step t (J = t mod 3, static): issue the loads of steps t+3
@@ -394,32 +387,14 @@ __device__ __forceinline__ void pf_step(const PrefillArgs &a, const PfLane &L, i
     // keep the scheduler from hoisting a later step's register work (which
     // would wait for younger loads) above this step's barrier
     __builtin_amdgcn_sched_barrier(0);
-    f16 *B_t = Bs0 + J * (PF_B_BYTES / 2), *B_1 = Bs0 + J1 * (PF_B_BYTES / 2), *B_2 = Bs0 + J2 * (PF_B_BYTES / 2);
-    // the fold targets step t+1's stage, written one step ago: independent
-    // of everything below, and kept out of its scheduling region (it has a
-    // rare-path branch)
-    if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_1, trash, canonical);
-    __builtin_amdgcn_sched_barrier(0);
     pf_load_a(a, L, min(t + 3, nk - 1), ra[J]);
     pf_load_b(a, L, min(t + 4, nk - 1), rb[J1]);
     if (FOLD) pf_load_e(a, offs, min(t + 3, nk - 1), re[J]);
-    PfFrag f;
-    pf_frag_load(As0 + (t & 1) * (PF_A_BYTES / 2), B_t, wm, wn, f);
+    f16 *B_t = Bs0 + J * (PF_B_BYTES / 2), *B_1 = Bs0 + J1 * (PF_B_BYTES / 2), *B_2 = Bs0 + J2 * (PF_B_BYTES / 2);
     pf_store_a(L, ra[J1], As0 + ((t + 1) & 1) * (PF_A_BYTES / 2));
     pf_store_b(rb[J2], B_2);
-    pf_mfma(f, acc);
-    // issue order: loads, the step's operand reads, then each MFMA followed
-    // by a few VALU ops and LDS writes of the next stages, so the dequant
-    // runs in the shadow of the matrix core
-    __builtin_amdgcn_sched_group_barrier(0x020, 7, 0);   // VMEM reads
-    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
-    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
-        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-    }
+    if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_1, trash, canonical);
+    pf_mfma(As0 + (t & 1) * (PF_A_BYTES / 2), B_t, wm, wn, acc);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
 }

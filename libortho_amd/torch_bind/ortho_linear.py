@@ -23,8 +23,8 @@ Differences, all deliberate:
   * ``forward`` on a CPU tensor raises instead of returning uninitialised
     memory (the reference's CPU branch is ``pass``, :152-162); there is no
     CPU path in this library.
-  * The prefill kernel's ortho plan (a derived layout of the CSR buffers) is
-    built on first use and cached; it is rebuilt whenever one of the three
+  * The ortho plan read by the mid-batch and prefill kernels (a derived
+    layout of the CSR buffers) is built on first use and cached; it is rebuilt whenever one of the three
     CSR buffers is replaced or modified in place.  It is not a buffer and is
     not saved in the state_dict.
 """
@@ -40,8 +40,9 @@ from ..tools.sieve import pack_ortho_sparse
 
 HAS_C_OPS = True  # the reference's flag (:15-28); this package has no fallback
 
-# Below this many tokens the decode kernel serves the call and needs no plan.
-_PLAN_MIN_TOKENS = 17
+# Below this many tokens the decode kernel serves the call and needs no plan;
+# from here on the mid-batch and prefill kernels read the ortho plan.
+_PLAN_MIN_TOKENS = 5
 
 
 class OrthoLinear(nn.Module):
@@ -125,7 +126,7 @@ class OrthoLinear(nn.Module):
         return tuple((t.data_ptr(), t.numel(), t._version, str(t.device)) for t in ts)
 
     def _ortho_plan(self):
-        """The cached prefill plan, rebuilt when the CSR buffers change."""
+        """The cached ortho plan, rebuilt when the CSR buffers change."""
         if self.ortho_values.numel() == 0 or not self.ortho_values.is_cuda:
             return None
         key = self._csr_key()

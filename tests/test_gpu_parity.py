@@ -87,14 +87,31 @@ def test_dequant_odd_groups_bit_exact(oracle_mod):
     assert np.array_equal(got.view(np.uint32), oracle_mod.dequant_f32(L.q, L.scales).view(np.uint32))
 
 
+def auto_kernel(M, planned=False):
+    """Kernel the dispatcher picks for fp16 I/O on the fast-path shapes: the
+    mid-batch kernel reads the ortho plan, so without one (and with an ortho
+    term) batches up to 16 stay on the decode kernel."""
+    if M <= 4 or (M <= 16 and not planned):
+        return "decode"
+    return "skinny" if M <= 64 else "prefill"
+
+
 # ---------------------------------------------------------- decode (M <= 16)
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_decode_c2_sweep(oracle_mod, c2, M):
     x = W.make_x(M, c2.K, 2000 + M)
     y, k = run(c2, x, 1.0)
-    assert k == "decode"
+    assert k == auto_kernel(M)
     assert_close(y, oracle_y(oracle_mod, c2, x, 1.0), what=f"c2 M={M}")
+
+
+@pytest.mark.parametrize("M", [8, 16])
+def test_decode_forced_at_larger_batches(oracle_mod, c2, M):
+    x = W.make_x(M, c2.K, 2100 + M)
+    y, k = run(c2, x, 1.0, policy="decode")
+    assert k == "decode"
+    assert_close(y, oracle_y(oracle_mod, c2, x, 1.0), what=f"c2 decode M={M}")
 
 
 @pytest.mark.parametrize("alpha", [0.0, 1.0])
@@ -106,12 +123,13 @@ def test_decode_c1_per_row_scales(oracle_mod, alpha):
     assert_close(y, oracle_y(oracle_mod, L, x, alpha), what=f"c1 alpha={alpha}")
 
 
-def test_decode_c4_skewed(oracle_mod):
+@pytest.mark.parametrize("policy", ["auto", "decode"])
+def test_c4_skewed(oracle_mod, policy):
     L = W.config_layer("c4")
     x = W.make_x(8, L.K, 4001)
-    y, k = run(L, x, 1.0)
-    assert k == "decode"
-    assert_close(y, oracle_y(oracle_mod, L, x, 1.0), what="c4")
+    y, k = run(L, x, 1.0, policy=policy, plan=True)
+    assert k == ("skinny" if policy == "auto" else "decode")
+    assert_close(y, oracle_y(oracle_mod, L, x, 1.0), what=f"c4 {policy}")
 
 
 def test_decode_accuracy_is_tight(oracle_mod, c2):
@@ -143,7 +161,7 @@ def test_prefill_skewed_plan(oracle_mod):
     # thousands of plan entries in one (row block, k step): the fold loops
     L = W.config_layer("c4")
     x = W.make_x(40, L.K, 4002)
-    y, k = run(L, x, 1.0, plan=True)
+    y, k = run(L, x, 1.0, policy="prefill", plan=True)
     assert k == "prefill"
     assert_close(y, oracle_y(oracle_mod, L, x, 1.0), what="c4 prefill")
 
@@ -153,9 +171,51 @@ def test_llama_block_c5(oracle_mod, M):
     for L in W.llama_block():
         x = W.make_x(M, L.K, 5100 + M)
         y, k = run(L, x, 1.0, plan=True)
-        assert k == ("decode" if M == 1 else "prefill")
+        assert k == auto_kernel(M, planned=True)
         rows = np.arange(M) if M <= 8 else np.array([0, 7, 15, 16, 31])
         assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"c5 {L.name} M={M}")
+
+
+# ------------------------------------------------- mid batches (5..64)
+
+@pytest.mark.parametrize("M", [5, 8, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("alpha,plan", [(1.0, True), (1.0, "auto"), (0.0, "auto")])
+def test_skinny_c2_sweep(oracle_mod, c2, M, alpha, plan):
+    x = W.make_x(M, c2.K, 2500 + M)
+    y, k = run(c2, x, alpha, plan=plan)
+    assert k == auto_kernel(M, planned=plan is True or alpha <= 0)
+    rows = np.unique(np.linspace(0, M - 1, min(M, 9)).astype(int))
+    assert_close(y[rows], oracle_y(oracle_mod, c2, x[rows], alpha), what=f"skinny c2 M={M} a={alpha}")
+
+
+@pytest.mark.parametrize("K,N,G,M", [
+    (4096, 4096, None, 32),   # per-row scales (c1 layout)
+    (2048, 640, 256, 12),     # G = 256: one 16-bit scale per chunk
+    (1152, 384, 128, 20),     # odd group count: scales not read as pairs
+    (1024, 43008, 128, 5),    # enough row blocks for one slice (no split K)
+    (11008, 4096, 128, 32),   # down_proj: K not a multiple of the slice
+])
+def test_skinny_scale_modes_and_slicing(oracle_mod, K, N, G, M):
+    L = W.make_layer(K, N, G, 0.01, seed=K + N + M)
+    x = W.make_x(M, K, 2600 + M)
+    y, k = run(L, x, 1.0, plan=True)
+    assert k == "skinny"
+    rows = np.unique(np.linspace(0, M - 1, min(M, 6)).astype(int))
+    assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"skinny K={K} N={N} G={G} M={M}")
+
+
+def test_skinny_workspace_reuse_and_determinism(oracle_mod, c2):
+    # the split-K counters reset themselves; the workspace grows with M
+    outs = {}
+    for M in (8, 32, 8, 32):
+        x = W.make_x(M, c2.K, 2700 + M)
+        y, k = run(c2, x, 1.0, plan=True)
+        assert k == "skinny"
+        if M in outs:
+            assert np.array_equal(y, outs[M])
+        else:
+            outs[M] = y
+            assert_close(y[:4], oracle_y(oracle_mod, c2, x[:4], 1.0), what=f"reuse M={M}")
 
 
 # ----------------------------------------------------------------- edges
@@ -165,7 +225,7 @@ def test_ragged_shapes(oracle_mod, M):
     L = W.make_layer(512, 1000, 128, 0.02, seed=70 + M)  # N not a multiple of 16 or 128
     x = W.make_x(M, L.K, 71 + M)
     y, k = run(L, x, 1.0)
-    assert k == ("decode" if M <= 16 else "prefill")
+    assert k == auto_kernel(M)
     rows = np.unique(np.linspace(0, M - 1, min(M, 12)).astype(int))
     assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"ragged M={M}")
 
