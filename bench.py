@@ -161,12 +161,15 @@ def time_workload(torch, layer, M, alpha, steps, warmup, plan=False):
 COPY_BYTES = 512 << 20  # calibration copy: reads and writes exactly this many bytes
 PROFILE_DECODE_STEPS = 100
 PROFILE_PREFILL_STEPS = 5
+PROFILE_SKINNY_STEPS = 100
+PROFILE_SKINNY_M = 8
 PROFILE_COPIES = 5
 
 
 def profile_run(torch):
     """Eager launches (no graph) so that rocprofv3 --pmc sees one dispatch
-    per forward: decode c2 M=1 alpha=1, decode c2 M=1 alpha=0, prefill c3
+    per forward: decode c2 M=1 alpha=1, decode c2 M=1 alpha=0, mid-batch c2
+    M=8 alpha=1 (planned; its kernel and the slice reduction), prefill c3
     M=2048 alpha=1 (planned), then PROFILE_COPIES device-to-device copies of
     COPY_BYTES (the calibration for FETCH_SIZE / WRITE_SIZE)."""
     from libortho_amd import workloads as W
@@ -179,6 +182,13 @@ def profile_run(torch):
             rot.call(i, x, y, alpha)
         torch.cuda.synchronize()
         del rot
+    rot = Rotation(c2, torch, plan=True)
+    x = torch.from_numpy(W.make_x(PROFILE_SKINNY_M, c2.K, 7008)).cuda()
+    y = torch.empty(PROFILE_SKINNY_M, c2.N, dtype=torch.float16, device="cuda")
+    for i in range(PROFILE_SKINNY_STEPS):
+        rot.call(i, x, y, 1.0)
+    torch.cuda.synchronize()
+    del rot
     c3 = W.config_layer("c3")
     rot = Rotation(c3, torch, min_copies=2, min_bytes=0, plan=True)
     x = torch.from_numpy(W.make_x(2048, c3.K, 9048)).cuda()
@@ -194,7 +204,8 @@ def profile_run(torch):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"profile": "done", "decode_steps": PROFILE_DECODE_STEPS,
-                      "prefill_steps": PROFILE_PREFILL_STEPS, "copies": PROFILE_COPIES,
+                      "skinny_steps": PROFILE_SKINNY_STEPS, "prefill_steps": PROFILE_PREFILL_STEPS,
+                      "copies": PROFILE_COPIES,
                       "copy_bytes": COPY_BYTES}), flush=True)
 
 
@@ -236,6 +247,13 @@ def summarize_pmc(fetch_csv, write_csv):
             key, algo = f"c2_m1_alpha{int(alpha)}", W.algorithmic_bytes(c2, 1, alpha)
         elif "orth::prefill_kernel" in name:
             key, algo = "c3_m2048_alpha1", W.algorithmic_bytes(c3, 2048, 1.0)
+        elif name.startswith("void orth::skinny_kernel"):
+            m = PROFILE_SKINNY_M
+            key, algo = f"c2_m{m}_alpha1", W.algorithmic_bytes(c2, m, 1.0)
+        elif "orth::skinny_reduce_kernel" in name:
+            # the slice reduction of the same forwards: its bytes count
+            # against the forward's algorithmic bytes in the combined entry
+            key, algo = f"c2_m{PROFILE_SKINNY_M}_alpha1_reduce", None
         else:
             continue
         fk = sum(f_k[name]) / len(f_k[name])
@@ -245,7 +263,14 @@ def summarize_pmc(fetch_csv, write_csv):
                     "fetch_kib_raw": round(fk, 2), "write_kib_raw": round(wk, 2),
                     "fetch_factor": round(f_fac, 4), "write_factor": round(w_fac, 4),
                     "fetch_bytes": int(fb), "write_bytes": int(wb), "bytes": int(fb + wb),
-                    "algorithmic_bytes": algo, "ratio_to_algorithmic": round((fb + wb) / algo, 4)}
+                    "algorithmic_bytes": algo,
+                    "ratio_to_algorithmic": round((fb + wb) / algo, 4) if algo else None}
+    mk, rk = f"c2_m{PROFILE_SKINNY_M}_alpha1", f"c2_m{PROFILE_SKINNY_M}_alpha1_reduce"
+    if mk in out and rk in out:
+        tot = out[mk]["bytes"] + out[rk]["bytes"]
+        out[mk + "_forward"] = {"kernels": [out[mk]["kernel"], out[rk]["kernel"]], "bytes": tot,
+                                "algorithmic_bytes": out[mk]["algorithmic_bytes"],
+                                "ratio_to_algorithmic": round(tot / out[mk]["algorithmic_bytes"], 4)}
     p = os.path.join(ROOT, "profiles", "traffic.json")
     json.dump(out, open(p, "w"), indent=1)
     print(json.dumps(out, indent=1))

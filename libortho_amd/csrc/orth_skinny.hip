@@ -68,6 +68,19 @@ struct SkinnyArgs {
     float *part;         // [S][M][N] partials (S > 1)
 };
 
+// v[i] for wave-uniform v and a runtime i in [0, L): a chain of selects, so
+// that v stays in registers (a runtime subscript moves the array to per-lane
+// scratch memory, which is written back through the L2 to HBM).  The
+// readfirstlane keeps the compiler from folding the chain back into a
+// subscripted load.
+template <int L>
+__device__ __forceinline__ int32_t pick(const int32_t (&v)[L], int i) {
+    int32_t r = __builtin_amdgcn_readfirstlane(v[0]);
+#pragma unroll
+    for (int k = 1; k < L; k++) r = i == k ? __builtin_amdgcn_readfirstlane(v[k]) : r;
+    return r;
+}
+
 // GMODE: 0 per-row scale (G == K); 1 G = 128, scales read as aligned pairs;
 // 2 any G = 128 * 2^j.  NTT: 16-token tiles.  CPS: chunk bound per slice.
 template <int NTT, int GMODE, int CPS, bool SPARSE>
@@ -113,7 +126,7 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
         for (int i = 0; i <= 2 * CPS; i++)
             soff[i] = min(max(a.poffs[ob + min(2 * kc0 + min(i, 2 * nci), a.nsteps)], 0), a.nnz);
         e_lo = soff[0];
-        e_hi = plan_ok ? max(soff[2 * nci], e_lo) : e_lo;
+        e_hi = plan_ok ? max(pick(soff, 2 * nci), e_lo) : e_lo;
         // monotone within [e_lo, e_hi] whatever the plan holds
 #pragma unroll
         for (int i = 0; i <= 2 * CPS; i++) soff[i] = min(max(soff[i], i ? soff[i - 1] : e_lo), e_hi);
@@ -259,10 +272,11 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
                 const int o = __shfl_up(incl, off, 64);
                 if (lane >= off) incl += o;
             }
-            const int base = soff[b] + incl - v0 - v1;  // before row 2 lane
+            const int32_t sb = pick(soff, b);
+            const int base = sb + incl - v0 - v1;       // before row 2 lane
             t[1 + 2 * lane] = base + v0;                // start of row 2 lane + 1
             t[2 + 2 * lane] = base + v0 + v1;           // start of row 2 lane + 2
-            if (lane == 0) t[0] = soff[b];
+            if (lane == 0) t[0] = sb;
         }
         __syncthreads();
         const int r = tid >> 2, tg = tid & 3;
