@@ -253,14 +253,20 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
         for (int i = tid; i < NB * 129; i += kSkNT) ridx[i] = 0;
         __syncthreads();
         const int32_t staged_hi = e_lo + min(e_hi - e_lo, kSkEStaged);
-        auto entry = [&](int32_t i) -> uint32_t { return i < staged_hi ? es[i - e_lo] : a.pents[i]; };
+        const uint32_t *pents = a.pents;
+        // Entries below staged_hi are read from LDS, the rest (slices of more
+        // than kSkEStaged entries) from memory, in loops of their own: one
+        // accessor for both would become a flat load, which waits for memory
+        // latency on every entry.
         // counts: entry i of bucket b (soff[b] <= i < soff[b+1]) adds 1 to (b, row + 1)
-        for (int32_t i = e_lo + tid; i < e_hi; i += kSkNT) {
+        auto count = [&](int32_t i, uint32_t e) {
             int b = 0;
 #pragma unroll
             for (int k = 1; k < NB; k++) b += i >= soff[k] ? 1 : 0;
-            atomicAdd(&ridx[b * 129 + 1 + (int)((entry(i) >> 24) & 0x7f)], 1);
-        }
+            atomicAdd(&ridx[b * 129 + 1 + (int)((e >> 24) & 0x7f)], 1);
+        };
+        for (int32_t i = e_lo + tid; i < staged_hi; i += kSkNT) count(i, es[i - e_lo]);
+        for (int32_t i = staged_hi + tid; i < e_hi; i += kSkNT) count(i, pents[i]);
         __syncthreads();
         // prefix sums: ridx[b][r] = first entry of row r in bucket b
         for (int b = wave; b < NB; b += kSkNT / 64) {
@@ -283,18 +289,21 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
         float sacc[MQ];
 #pragma unroll
         for (int i = 0; i < MQ; i++) sacc[i] = 0.f;
+        const int xstride = a.xstride;
+        auto fma_entry = [&](int st, uint32_t e) {
+            const int cl = st * kSkPlanBK + (int)((e >> 16) & 0x3f);  // column within the slice
+            const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
+            const int xi = (cl & ~7) | interleaved_pos(cl & 7);
+#pragma unroll
+            for (int i2 = 0; i2 < MQ; i2++) sacc[i2] += v * (float)xs[(tg + 4 * i2) * xstride + xi];
+        };
 #pragma unroll
         for (int st = 0; st < NB; st++) {
             // (buckets past the slice are empty: their offsets were clamped)
             const int32_t lo = max(ridx[st * 129 + r], e_lo), hi = min(ridx[st * 129 + r + 1], e_hi);
-            for (int32_t i = lo; i < hi; i++) {
-                const uint32_t e = entry(i);
-                const int cl = st * kSkPlanBK + (int)((e >> 16) & 0x3f);  // column within the slice
-                const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
-                const int xi = (cl & ~7) | interleaved_pos(cl & 7);
-#pragma unroll
-                for (int i2 = 0; i2 < MQ; i2++) sacc[i2] += v * (float)xs[(tg + 4 * i2) * a.xstride + xi];
-            }
+            const int32_t hs = min(hi, staged_hi);
+            for (int32_t i = lo; i < hs; i++) fma_entry(st, es[i - e_lo]);
+            for (int32_t i = max(lo, staged_hi); i < hi; i++) fma_entry(st, pents[i]);
         }
 #pragma unroll
         for (int i2 = 0; i2 < MQ; i2++) sp[r * MP + tg + 4 * i2] = sacc[i2];
@@ -340,21 +349,41 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
 // outputs of one token (N % 4 == 0) or one output (otherwise).
 __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f16 *y, int64_t MN, int S,
                                                             int vec4) {
+    // the partials were written by other XCDs and miss this L2: all loads of
+    // a group of 8 slices are issued before the first add (addresses clamped
+    // to the last slice, the extra ones not added), sums in slice order
+    constexpr int U = 8;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (vec4) {
         const int64_t o = t * 4;
         if (o >= MN) return;
-        f32x4 v = *reinterpret_cast<const f32x4 *>(part + o);
-        for (int s = 1; s < S; s++) {
-            const f32x4 w = *reinterpret_cast<const f32x4 *>(part + (int64_t)s * MN + o);
-            v += w;
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < S; s0 += U) {
+            f32x4 w[U];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                w[u] = *reinterpret_cast<const f32x4 *>(part + (int64_t)min(s0 + u, S - 1) * MN + o);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (s0 + u == 0) v = w[u];
+                else if (s0 + u < S) v += w[u];
+            }
         }
         const f16x2 lo = {(f16)v[0], (f16)v[1]}, hi = {(f16)v[2], (f16)v[3]};
         *reinterpret_cast<uint2 *>(y + o) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
     } else {
         if (t >= MN) return;
-        float v = part[t];
-        for (int s = 1; s < S; s++) v += part[(int64_t)s * MN + t];
+        float v = 0.f;
+        for (int s0 = 0; s0 < S; s0 += U) {
+            float w[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) w[u] = part[(int64_t)min(s0 + u, S - 1) * MN + t];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (s0 + u == 0) v = w[u];
+                else if (s0 + u < S) v += w[u];
+            }
+        }
         y[t] = (f16)v;
     }
 }

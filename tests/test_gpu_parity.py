@@ -204,6 +204,18 @@ def test_skinny_scale_modes_and_slicing(oracle_mod, K, N, G, M):
     assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"skinny K={K} N={N} G={G} M={M}")
 
 
+@pytest.mark.parametrize("M", [8, 40])
+def test_skinny_dense_ortho_past_the_staged_entries(oracle_mod, M):
+    # 25 % ortho density: ~8,000 plan entries per (row block, K slice), more
+    # than the kernel stages in LDS, so the rest are read from memory
+    L = W.make_layer(2048, 2048, 128, 0.25, seed=2800 + M)
+    x = W.make_x(M, L.K, 2900 + M)
+    y, k = run(L, x, 1.0, plan=True)
+    assert k == "skinny"
+    rows = np.unique(np.linspace(0, M - 1, min(M, 6)).astype(int))
+    assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"skinny dense ortho M={M}")
+
+
 def test_skinny_workspace_reuse_and_determinism(oracle_mod, c2):
     # the split-K counters reset themselves; the workspace grows with M
     outs = {}
