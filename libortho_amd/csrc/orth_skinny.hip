@@ -81,6 +81,20 @@ __device__ __forceinline__ int32_t pick(const int32_t (&v)[L], int i) {
     return r;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves: shifts
+// by 1, 2, 4, 8 within each row of 16 lanes, then row 0's total into row 1
+// and row 2's into row 3 (row_bcast:15), then the total of rows 0-1 into
+// rows 2-3 (row_bcast:31).  Lanes without a source take 0.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
+
 // GMODE: 0 per-row scale (G == K); 1 G = 128, scales read as aligned pairs;
 // 2 any G = 128 * 2^j.  NTT: 16-token tiles.  CPS: chunk bound per slice.
 template <int NTT, int GMODE, int CPS, bool SPARSE>
@@ -110,26 +124,16 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
     const int64_t my_n = min(wrow0 + nl, a.N - 1);               // clamped weight row
     const int K = a.K;
 
-    // ---- plan offsets of the slice's buckets (uniform, read before any
-    //      vector load so that the entry loads below wait for nothing else)
-    int32_t soff[2 * CPS + 1];
-    bool plan_ok = false;
-    int32_t e_lo = 0, e_hi = 0;
+    // ---- plan words, one vector load per wave issued before the other
+    //      loads (loads return in order, so waiting for it waits for nothing
+    //      else): lanes 0 .. 2 CPS read the slice's bucket offsets, lanes
+    //      32 .. 43 the plan header words 0 .. 11
+    int32_t pword = 0;
     if (SPARSE) {
-        const uint32_t *h = a.phdr;
-        plan_ok = h[0] == kSkPlanMagic && h[1] == 1u &&
-                  *reinterpret_cast<const int64_t *>(h + 6) == a.N &&
-                  *reinterpret_cast<const int64_t *>(h + 8) == (int64_t)K &&
-                  *reinterpret_cast<const int64_t *>(h + 10) == (int64_t)a.nnz;
         const int64_t ob = (int64_t)blk * (a.nsteps + 1);
-#pragma unroll
-        for (int i = 0; i <= 2 * CPS; i++)
-            soff[i] = min(max(a.poffs[ob + min(2 * kc0 + min(i, 2 * nci), a.nsteps)], 0), a.nnz);
-        e_lo = soff[0];
-        e_hi = plan_ok ? max(pick(soff, 2 * nci), e_lo) : e_lo;
-        // monotone within [e_lo, e_hi] whatever the plan holds
-#pragma unroll
-        for (int i = 0; i <= 2 * CPS; i++) soff[i] = min(max(soff[i], i ? soff[i - 1] : e_lo), e_hi);
+        const int32_t *src = lane < 32 ? a.poffs + (ob + min(2 * kc0 + min(lane, 2 * nci), a.nsteps))
+                                       : reinterpret_cast<const int32_t *>(a.phdr) + min(lane - 32, 11);
+        pword = *src;
     }
 
     // ---- activations of the slice: piece p = (m, c, j) covers 8 halves
@@ -164,11 +168,29 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
     for (int p = 0; p < CPS; p++)
         wv[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(qrow + min(kc0 + p, clast) * 64));
 
+    // ---- bucket offsets of the slice (uniform), checked against the header
+    int32_t soff[2 * CPS + 1];
+    int32_t e_lo = 0, e_hi = 0;
+    if (SPARSE) {
+        auto word = [&](int l) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane(pword, l); };
+        auto dword = [&](int l) -> int64_t { return (int64_t)(word(l) | ((uint64_t)word(l + 1) << 32)); };
+        const bool plan_ok = (word(32) == kSkPlanMagic) & (word(33) == 1u) & (dword(38) == a.N) &
+                             (dword(40) == (int64_t)K) & (dword(42) == (int64_t)a.nnz);
+#pragma unroll
+        for (int i = 0; i <= 2 * CPS; i++) soff[i] = min(max(__builtin_amdgcn_readlane(pword, i), 0), a.nnz);
+        e_lo = soff[0];
+        e_hi = plan_ok ? max(min(max(__builtin_amdgcn_readlane(pword, 2 * nci), 0), a.nnz), e_lo) : e_lo;
+        // monotone within [e_lo, e_hi] whatever the plan holds
+#pragma unroll
+        for (int i = 0; i <= 2 * CPS; i++) soff[i] = min(max(soff[i], i ? soff[i - 1] : e_lo), e_hi);
+    }
+
     // ---- the slice's plan entries (up to kSkEStaged; more are read from
-    //      memory in the sparse pass), addresses clamped into the array
+    //      memory in the sparse pass).  Addresses past the slice repeat its
+    //      last entry: no bytes beyond the slice's own are fetched.
     uint32_t ereg[SPARSE ? kSkESlots : 1];
     if (SPARSE) {
-        const int32_t elast = max(a.nnz - 1, 0);
+        const int32_t elast = min(max(e_hi - 1, e_lo), max(a.nnz - 1, 0));
 #pragma unroll
         for (int i = 0; i < kSkESlots; i++) ereg[i] = a.pents[min(e_lo + tid + kSkNT * i, elast)];
     }
@@ -190,6 +212,8 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
             if ((p & 15) == 0) cr[c * MP + m] = b;
         }
     }
+    if (SPARSE)
+        for (int i = tid; i < 2 * CPS * 129; i += kSkNT) ridx[i] = 0;
     __syncthreads();
 
     // ---- dense term: wave w, rows 16 w + nl, token tiles tt
@@ -248,36 +272,33 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
     constexpr int MQ = MP / 4;  // tokens per thread: tg, tg + 4, ...
     if (SPARSE) {
         constexpr int NB = 2 * CPS;  // buckets (64-column steps) of a slice
-#pragma unroll
-        for (int i = 0; i < kSkESlots; i++) es[tid + kSkNT * i] = ereg[i];
-        for (int i = tid; i < NB * 129; i += kSkNT) ridx[i] = 0;
-        __syncthreads();
         const int32_t staged_hi = e_lo + min(e_hi - e_lo, kSkEStaged);
         const uint32_t *pents = a.pents;
         // Entries below staged_hi are read from LDS, the rest (slices of more
         // than kSkEStaged entries) from memory, in loops of their own: one
         // accessor for both would become a flat load, which waits for memory
         // latency on every entry.
-        // counts: entry i of bucket b (soff[b] <= i < soff[b+1]) adds 1 to (b, row + 1)
+        // counts: entry i of bucket b (soff[b] <= i < soff[b+1]) adds 1 to
+        // (b, row + 1); the staged entries are counted from registers
         auto count = [&](int32_t i, uint32_t e) {
             int b = 0;
 #pragma unroll
             for (int k = 1; k < NB; k++) b += i >= soff[k] ? 1 : 0;
             atomicAdd(&ridx[b * 129 + 1 + (int)((e >> 24) & 0x7f)], 1);
         };
-        for (int32_t i = e_lo + tid; i < staged_hi; i += kSkNT) count(i, es[i - e_lo]);
+#pragma unroll
+        for (int i = 0; i < kSkESlots; i++) {
+            es[tid + kSkNT * i] = ereg[i];
+            const int32_t idx = e_lo + tid + kSkNT * i;
+            if (idx < staged_hi) count(idx, ereg[i]);
+        }
         for (int32_t i = staged_hi + tid; i < e_hi; i += kSkNT) count(i, pents[i]);
         __syncthreads();
         // prefix sums: ridx[b][r] = first entry of row r in bucket b
         for (int b = wave; b < NB; b += kSkNT / 64) {
             int32_t *t = ridx + b * 129;
             const int v0 = t[1 + 2 * lane], v1 = t[2 + 2 * lane];
-            int incl = v0 + v1;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int o = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += o;
-            }
+            const int incl = wave_inclusive_sum(v0 + v1);
             const int32_t sb = pick(soff, b);
             const int base = sb + incl - v0 - v1;       // before row 2 lane
             t[1 + 2 * lane] = base + v0;                // start of row 2 lane + 1
@@ -290,20 +311,51 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
 #pragma unroll
         for (int i = 0; i < MQ; i++) sacc[i] = 0.f;
         const int xstride = a.xstride;
-        auto fma_entry = [&](int st, uint32_t e) {
-            const int cl = st * kSkPlanBK + (int)((e >> 16) & 0x3f);  // column within the slice
+        auto fma_entry = [&](int cbase, uint32_t e) {
+            const int cl = cbase + (int)((e >> 16) & 0x3f);  // column within the slice
             const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
             const int xi = (cl & ~7) | interleaved_pos(cl & 7);
 #pragma unroll
             for (int i2 = 0; i2 < MQ; i2++) sacc[i2] += v * (float)xs[(tg + 4 * i2) * xstride + xi];
         };
+        // First pass: the first entry of every bucket of row r, GB buckets at
+        // a time, so that each round of LDS reads (bounds, entries,
+        // activations) is issued together.  An absent entry reads as value 0
+        // at column 0 of the slice (a column of a bucket past the host's
+        // chunk count would lie outside the staged activations).
+        constexpr int GB = (32 / MQ) < 2 ? 2 : (32 / MQ) > NB ? NB : (32 / MQ);
+        uint32_t more = 0;  // bit st: bucket st has entries the first pass did not take
 #pragma unroll
-        for (int st = 0; st < NB; st++) {
-            // (buckets past the slice are empty: their offsets were clamped)
+        for (int s0 = 0; s0 < NB; s0 += GB) {
+            int32_t lo[GB], hi[GB];
+#pragma unroll
+            for (int u = 0; u < GB; u++) {
+                const int st = min(s0 + u, NB - 1);
+                lo[u] = max(ridx[st * 129 + r], e_lo);
+                hi[u] = min(ridx[st * 129 + r + 1], e_hi);
+            }
+            uint32_t ev[GB];
+            int cb[GB];
+#pragma unroll
+            for (int u = 0; u < GB; u++) {
+                const bool ok = s0 + u < NB && lo[u] < hi[u] && lo[u] < staged_hi;
+                ev[u] = ok ? es[min(lo[u] - e_lo, kSkEStaged - 1)] : 0u;
+                cb[u] = ok ? (s0 + u) * kSkPlanBK : 0;
+                if (s0 + u < NB && hi[u] - lo[u] > (ok ? 1 : 0)) more |= 1u << (s0 + u);
+            }
+#pragma unroll
+            for (int u = 0; u < GB; u++) fma_entry(cb[u], ev[u]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // Second pass: the remaining entries, bucket by bucket
+        while (more) {
+            const int st = __builtin_ctz(more);
+            more &= more - 1;
             const int32_t lo = max(ridx[st * 129 + r], e_lo), hi = min(ridx[st * 129 + r + 1], e_hi);
             const int32_t hs = min(hi, staged_hi);
-            for (int32_t i = lo; i < hs; i++) fma_entry(st, es[i - e_lo]);
-            for (int32_t i = max(lo, staged_hi); i < hi; i++) fma_entry(st, pents[i]);
+            for (int32_t i = lo + 1; i < hs; i++) fma_entry(st * kSkPlanBK, es[i - e_lo]);
+            // past the staged block (the first entry too, when it lay there)
+            for (int32_t i = max(lo, staged_hi); i < hi; i++) fma_entry(st * kSkPlanBK, pents[i]);
         }
 #pragma unroll
         for (int i2 = 0; i2 < MQ; i2++) sp[r * MP + tg + 4 * i2] = sacc[i2];
