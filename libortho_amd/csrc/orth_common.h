@@ -171,12 +171,29 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// v of the lane `ctrl` names (a DPP pattern within rows of 16 lanes).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
+// Groups of 16 are the DPP rows: rotations by 8, 4, 2, 1 lanes within the
+// row (register moves, no LDS round trip) leave every lane with its row's
+// sum (each lane adds in its own order, so callers take one fixed lane).
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
+    if constexpr (WIDTH == 16) {
+        v += dpp_f32<0x128>(v);  // row_ror:8
+        v += dpp_f32<0x124>(v);  // row_ror:4
+        v += dpp_f32<0x122>(v);  // row_ror:2
+        v += dpp_f32<0x121>(v);  // row_ror:1
+        return v;
+    } else {
 #pragma unroll
-    for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+        for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        return v;
+    }
 }
 
 }  // namespace orth

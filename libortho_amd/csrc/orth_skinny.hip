@@ -16,10 +16,13 @@
 //    The bias is removed per chunk with the activation sums computed while
 //    staging; group scales multiply each chunk's FP32 partial.
 //  * The sparse ortho term of the slice comes from the ortho plan: its
-//    (128-row block, 64-column step) buckets are sorted by row, so each
-//    thread finds its row's entries in each bucket of the slice by binary
-//    search and multiplies them with the staged activations.  Sums are
-//    formed in a fixed order: the result does not depend on scheduling.
+//    (128-row block, 64-column step) buckets are sorted by row.  The slice's
+//    entries are staged in LDS, counted per (bucket, row) with LDS atomics
+//    and turned into row starts by a DPP prefix sum per bucket; four threads
+//    per row then multiply the row's entries with the staged activations,
+//    first the leading entry of every bucket (LDS reads issued in batches),
+//    then the rest.  Sums are formed in a fixed order: the result does not
+//    depend on scheduling.
 //  * When the row blocks alone cannot fill the GPU, K is split over S
 //    workgroups.  Each writes its FP32 partial (ortho term included) to a
 //    workspace and a second kernel adds the S partials in slice order and
@@ -124,18 +127,6 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
     const int64_t my_n = min(wrow0 + nl, a.N - 1);               // clamped weight row
     const int K = a.K;
 
-    // ---- plan words, one vector load per wave issued before the other
-    //      loads (loads return in order, so waiting for it waits for nothing
-    //      else): lanes 0 .. 2 CPS read the slice's bucket offsets, lanes
-    //      32 .. 43 the plan header words 0 .. 11
-    int32_t pword = 0;
-    if (SPARSE) {
-        const int64_t ob = (int64_t)blk * (a.nsteps + 1);
-        const int32_t *src = lane < 32 ? a.poffs + (ob + min(2 * kc0 + min(lane, 2 * nci), a.nsteps))
-                                       : reinterpret_cast<const int32_t *>(a.phdr) + min(lane - 32, 11);
-        pword = *src;
-    }
-
     // ---- activations of the slice: piece p = (m, c, j) covers 8 halves
     u32x4 xreg[XP];
 #pragma unroll
@@ -144,6 +135,19 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
         const int m = min(p / (CPS * 16), a.M - 1);
         const int c = min(kc0 + (p / 16) % CPS, clast);
         xreg[i] = *reinterpret_cast<const u32x4 *>(a.x + (int64_t)m * K + c * 128 + (p & 15) * 8);
+    }
+
+    // ---- plan words, one vector load per wave issued after the activations
+    //      and before the weights (loads complete in order: the staging does
+    //      not wait for it, and it does not wait for the weights): lanes
+    //      0 .. 2 CPS read the slice's bucket offsets, lanes 32 .. 43 the plan
+    //      header words 0 .. 11
+    int32_t pword = 0;
+    if (SPARSE) {
+        const int64_t ob = (int64_t)blk * (a.nsteps + 1);
+        const int32_t *src = lane < 32 ? a.poffs + (ob + min(2 * kc0 + min(lane, 2 * nci), a.nsteps))
+                                       : reinterpret_cast<const int32_t *>(a.phdr) + min(lane - 32, 11);
+        pword = *src;
     }
 
     // ---- scales
@@ -168,7 +172,32 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
     for (int p = 0; p < CPS; p++)
         wv[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(qrow + min(kc0 + p, clast) * 64));
 
-    // ---- bucket offsets of the slice (uniform), checked against the header
+    // ---- stage the activations (interleaved k order) and their bias sums
+#pragma unroll
+    for (int i = 0; i < XP; i++) {
+        const int p = tid + kSkNT * i;
+        const int m = p / (CPS * 16), c = (p / 16) % CPS;
+        u32x4 v = xreg[i];
+        if (m >= a.M) v = u32x4{0, 0, 0, 0};
+        const f16x8 h = __builtin_bit_cast(f16x8, v);
+        // even k weigh 1032, odd k weigh 72 (see int4x8_to_f16_biased)
+        const float e = ((float)h[0] + (float)h[2]) + ((float)h[4] + (float)h[6]);
+        const float o = ((float)h[1] + (float)h[3]) + ((float)h[5] + (float)h[7]);
+        const float b = group_sum<16>(1032.0f * e + 72.0f * o);  // the 16 pieces of (m, c)
+        if (m < MP && c < a.cps) {  // the LDS tile holds the host's cps chunks
+            *reinterpret_cast<u32x4 *>(xs + (m * a.xstride + c * 128 + (p & 15) * 8)) = permute_x8(v);
+            if ((p & 15) == 0) cr[c * MP + m] = b;
+        }
+    }
+    if (SPARSE)
+        for (int i = tid; i < 2 * CPS * 129; i += kSkNT) ridx[i] = 0;
+    __syncthreads();
+
+    // ---- bucket offsets of the slice (uniform), checked against the header.
+    //      Read after the staging and its barrier (kept there by the
+    //      scheduling barrier): the offsets miss the caches more often than
+    //      the activations, and neither need wait for them.
+    __builtin_amdgcn_sched_barrier(0);
     int32_t soff[2 * CPS + 1];
     int32_t e_lo = 0, e_hi = 0;
     if (SPARSE) {
@@ -195,26 +224,6 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
         for (int i = 0; i < kSkESlots; i++) ereg[i] = a.pents[min(e_lo + tid + kSkNT * i, elast)];
     }
 
-    // ---- stage the activations (interleaved k order) and their bias sums
-#pragma unroll
-    for (int i = 0; i < XP; i++) {
-        const int p = tid + kSkNT * i;
-        const int m = p / (CPS * 16), c = (p / 16) % CPS;
-        u32x4 v = xreg[i];
-        if (m >= a.M) v = u32x4{0, 0, 0, 0};
-        const f16x8 h = __builtin_bit_cast(f16x8, v);
-        // even k weigh 1032, odd k weigh 72 (see int4x8_to_f16_biased)
-        const float e = ((float)h[0] + (float)h[2]) + ((float)h[4] + (float)h[6]);
-        const float o = ((float)h[1] + (float)h[3]) + ((float)h[5] + (float)h[7]);
-        const float b = group_sum<16>(1032.0f * e + 72.0f * o);  // the 16 pieces of (m, c)
-        if (m < MP && c < a.cps) {  // the LDS tile holds the host's cps chunks
-            *reinterpret_cast<u32x4 *>(xs + (m * a.xstride + c * 128 + (p & 15) * 8)) = permute_x8(v);
-            if ((p & 15) == 0) cr[c * MP + m] = b;
-        }
-    }
-    if (SPARSE)
-        for (int i = tid; i < 2 * CPS * 129; i += kSkNT) ridx[i] = 0;
-    __syncthreads();
 
     // ---- dense term: wave w, rows 16 w + nl, token tiles tt
     f32x4 acc[NTT];
