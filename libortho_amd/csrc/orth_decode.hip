@@ -62,12 +62,20 @@ struct DecodeArgs {
     int64_t N;
     int cpw;           // chunks per wave, even, <= the CPW template bound
     int xstride;       // LDS row stride of the staged activations, in halves
-    int lds_cr;        // byte offsets of the LDS regions
+    int lds_red;       // byte offsets of the LDS regions
+    int lds_sp;
+    int lds_cr;
     int lds_xs;
     int lds_e;
     float alpha;
     int has_ortho;
 };
+
+// Weights pass through LDS (whole-line loads, transposed on the way) for
+// one or two tokens with staged activations: there the weight stream is all
+// the kernel does, and the LDS holds a wave's weights beside the activations
+// with three workgroups per CU.
+constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 
 // GMODE: 0 per-row scale (G == K); 1 G = 128 with scales readable as
 // aligned 32-bit pairs; 2 any G = 128 * 2^j (one 16-bit load per chunk).
@@ -90,14 +98,29 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     constexpr int XIT = (CPW * 16 + 63) / 64;  // 16-byte activation pieces per lane per token
     constexpr int SW = (CPW + 7) / 8;          // group-128 scale words per lane
     constexpr int ES = kDecodeESlots;
+    // WT: the weights pass through LDS (see decode_wt)
+    constexpr bool WT = decode_wt(MT, XLDS);
+    constexpr int WREG = CPW * 1024;  // WT: LDS bytes of a wave's weight region
 
     extern __shared__ __align__(16) unsigned char smem[];
-    float *red = reinterpret_cast<float *>(smem);              // [W][16][16] split-K partials
-    float *sp = red + W * 256;                                  // [MT][RT] sparse sums
+    // WT: wave w's region holds its weights during the main loop, then its
+    // split-K partials (1 KB), CSR columns (2 KB) and values (1 KB)
+    float *sp = reinterpret_cast<float *>(smem + a.lds_sp);     // [MT][RT] sparse sums
     float *cr = reinterpret_cast<float *>(smem + a.lds_cr);     // [MT][nchunks] bias sums (XLDS)
     f16 *xs = reinterpret_cast<f16 *>(smem + a.lds_xs);         // [MT][xstride] activations
-    int32_t *ec = reinterpret_cast<int32_t *>(smem + a.lds_e);  // staged CSR columns
-    f16 *ev = reinterpret_cast<f16 *>(ec + kDecodeEStaged);     // staged CSR values
+    // split-K partials of wave w: [16 tokens][16 rows]
+    auto red = [&](int w) -> float * {
+        return reinterpret_cast<float *>(smem + (WT ? w * WREG : a.lds_red + w * 1024));
+    };
+    // staged CSR entry li: WT keeps entries [512 w, 512 w + 512) in wave w's region
+    auto ec_at = [&](int32_t li) -> int32_t * {
+        return WT ? reinterpret_cast<int32_t *>(smem + (li >> 9) * WREG + 1024) + (li & 511)
+                  : reinterpret_cast<int32_t *>(smem + a.lds_e) + li;
+    };
+    auto ev_at = [&](int32_t li) -> f16 * {
+        return WT ? reinterpret_cast<f16 *>(smem + (li >> 9) * WREG + 3072) + (li & 511)
+                  : reinterpret_cast<f16 *>(smem + a.lds_e + kDecodeEStaged * 4) + li;
+    };
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -162,13 +185,38 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         for (int p = 0; p < CPW; p++) sh[p] = sbase[min(c_lo + p, clast) >> a.gshift];
     }
 
-    // ---- weights (nontemporal): uniform base + 32-bit lane offset + offset
-    const uint8_t *qrow = a.q + (n0 + my_row) * (int64_t)(K >> 1) + g * 16;
-    u32x4 wv[CPW];
+    // ---- weights (nontemporal).  Direct: lane (row nl, g) loads the 16
+    //      bytes of chunk p it feeds to the MFMA (half a 128-byte line per
+    //      row per instruction).  WT: chunk pair j (128 bytes of each row),
+    //      rows 8h .. 8h + 7 per instruction, so that every instruction reads
+    //      whole lines: lane l takes row 8h + l/8, 16-byte slot l%8 of the
+    //      row's line, which holds logical slot s = (l%8) ^ ((row/2) & 7)
+    //      (the XOR spreads the MFMA-layout reads below over all LDS banks).
+    u32x4 wv[WT ? 1 : CPW];
+    u32x4 wq[WT ? CPW / 2 : 1][2];
+    if (!WT) {
+        const uint8_t *qrow = a.q + (n0 + my_row) * (int64_t)(K >> 1) + g * 16;
 #pragma unroll
-    for (int p = 0; p < CPW; p++)
-        wv[p] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(qrow + min(c_lo + p, clast) * 64));
+        for (int p = 0; p < CPW; p++)
+            wv[p] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4 *>(qrow + min(c_lo + p, clast) * 64));
+    } else {
+        const uint8_t *qh[2];
+        int sh2[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int r = 8 * h + (lane >> 3);
+            const int sl = (lane & 7) ^ ((r >> 1) & 7);
+            qh[h] = a.q + (n0 + min(r, last_row)) * (int64_t)(K >> 1) + (sl & 3) * 16;
+            sh2[h] = sl >> 2;  // which chunk of the pair
+        }
+#pragma unroll
+        for (int j = 0; j < CPW / 2; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                wq[j][h] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4 *>(qh[h] + min(c_lo + 2 * j + sh2[h], clast) * 64));
+    }
 
     // ---- activations from global memory (no LDS staging): 64 bytes per
     //      lane per chunk; A rows beyond M repeat row 0 (outputs unused)
@@ -192,10 +240,14 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     const int32_t wlast4 = min(max((e1 - 1) & ~3, eb), last4);
     u32x4 ecv[ES];
     uint2 evv[ES];
+    // staged slot of thread (wave, lane), group s: entries eb + 4 * slot ..
+    auto e_slot = [&](int s) -> int {
+        return WT ? wave * (kDecodeEStaged / W) + 4 * (lane + 64 * s) : 4 * (tid + NT * s);
+    };
     if (SPARSE == 1) {
 #pragma unroll
         for (int s = 0; s < ES; s++) {
-            const int32_t ic = min(eb + 4 * (tid + NT * s), wlast4);
+            const int32_t ic = min(eb + e_slot(s), wlast4);
             ecv[s] = *reinterpret_cast<const u32x4 *>(a.col + ic);
             evv[s] = *reinterpret_cast<const uint2 *>(a.vals + ic);
         }
@@ -236,10 +288,26 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     const float *cr_lane[MI];
 #pragma unroll
     for (int i = 0; i < MI; i++) cr_lane[i] = cr + ((4 * g + i) & (MT - 1)) * a.nchunks + c_lo;
+    // WT: this wave's weight region as 16-byte slots
+    u32x4 *wl = reinterpret_cast<u32x4 *>(smem + wave * WREG);
 #pragma unroll
     for (int p = 0; p < CPW; p++) {
         if (p < nci) {  // uniform
-            const uint32_t words[4] = {wv[p].x, wv[p].y, wv[p].z, wv[p].w};
+            u32x4 wp;
+            if (WT) {
+                const int j = p >> 1;
+                if ((p & 1) == 0) {  // pair j to LDS, as loaded
+                    wl[(2 * j) * 64 + lane] = wq[j][0];
+                    wl[(2 * j + 1) * 64 + lane] = wq[j][1];
+                    __builtin_amdgcn_wave_barrier();  // (same wave: LDS keeps the order)
+                }
+                // lane (row nl, g) reads logical slot 4 (p & 1) + g of row nl
+                const int phys = (4 * (p & 1) + g) ^ ((nl >> 1) & 7);
+                wp = wl[(2 * j + (nl >> 3)) * 64 + (nl & 7) * 8 + phys];
+            } else {
+                wp = wv[p];
+            }
+            const uint32_t words[4] = {wp.x, wp.y, wp.z, wp.w};
             f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -287,13 +355,13 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 
     // ---- split-K partials and the staged CSR block to LDS
 #pragma unroll
-    for (int i = 0; i < 4; i++) red[(wave * 16 + (4 * g + i)) * 16 + nl] = acc[i];
+    for (int i = 0; i < 4; i++) red(wave)[(4 * g + i) * 16 + nl] = acc[i];
     if (SPARSE == 1) {
 #pragma unroll
         for (int s = 0; s < ES; s++) {
-            const int slot = 4 * (tid + NT * s);
-            *reinterpret_cast<u32x4 *>(ec + slot) = ecv[s];
-            *reinterpret_cast<uint2 *>(ev + slot) = evv[s];
+            const int slot = e_slot(s);
+            *reinterpret_cast<u32x4 *>(ec_at(slot)) = ecv[s];
+            *reinterpret_cast<uint2 *>(ev_at(slot)) = evv[s];
         }
     }
     __syncthreads();  // every wave's activation chunks and the CSR block are in LDS
@@ -317,8 +385,8 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
             for (int u = 0; u < U; u++) {
                 const int32_t j = j0 + 16 * u;
                 const int32_t li = min(j, fast_hi - 1) - eb;  // in [0, kDecodeEStaged)
-                c[u] = ec[li];
-                v[u] = (j < fast_hi) ? (float)ev[li] : 0.f;
+                c[u] = *ec_at(li);
+                v[u] = (j < fast_hi) ? (float)*ev_at(li) : 0.f;
             }
 #pragma unroll
             for (int u = 0; u < U; u++) {
@@ -364,7 +432,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         if (m < a.M && n < a.N) {
             float v = 0.f;
 #pragma unroll
-            for (int w = 0; w < W; w++) v += red[(w * 16 + m) * 16 + r];
+            for (int w = 0; w < W; w++) v += red(w)[m * 16 + r];
             if (!GROUPED) v *= (float)srow;
             if (SPARSE) v += a.alpha * sp[m * RT + r];
             a.y[(int64_t)m * a.N + n] = (f16)v;
@@ -374,41 +442,74 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 
 // ------------------------------------------------------------------ host
 
-template <int MT, int GMODE, bool XLDS, int CPW>
-static hipError_t launch_decode_t(const DecodeArgs &d, int64_t lds_bytes, hipStream_t stream) {
+static const int64_t kDecodeLdsMax = 160 * 1024;
+
+// LDS layout of decode_kernel<MT, *, XLDS, CPW, *>: weight regions (WT) or
+// split-K partials, sparse sums, bias sums, activations, staged CSR block
+// (outside the weight regions when not WT).  Returns the bytes.
+static int64_t decode_lds_layout(DecodeArgs &d, int mt, bool xlds, int cpw_bound) {
+    auto al = [](int64_t v) { return (v + 15) & ~int64_t(15); };
+    const bool wt = decode_wt(mt, xlds);
+    int64_t off = wt ? (int64_t)kDecodeW * cpw_bound * 1024 : (int64_t)kDecodeW * 1024;
+    d.lds_red = 0;
+    d.lds_sp = (int)off;
+    off = al(off + (int64_t)mt * 16 * 4);
+    d.lds_cr = (int)off;
+    if (xlds) off = al(off + (int64_t)mt * d.nchunks * 4);
+    d.lds_xs = (int)off;
+    if (xlds) off = al(off + (int64_t)mt * d.xstride * 2);
+    d.lds_e = (int)off;
+    if (!wt && d.has_ortho && d.csr_vec) off += (int64_t)kDecodeEStaged * (4 + 2);
+    return off;
+}
+
+template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE>
+static hipError_t launch_decode_k(const DecodeArgs &d, int64_t lds, hipStream_t stream) {
+    // more than 64 KB of dynamic LDS must be allowed once per device
+    static int allowed[64] = {0};
+    int dev = 0;
+    if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !allowed[dev]) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<MT, GMODE, XLDS, CPW, SPARSE>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecodeLdsMax);
+        if (e != hipSuccess) return e;
+        allowed[dev] = 1;
+    }
     const unsigned blocks = (unsigned)((d.N + 15) / 16);
-    if (d.has_ortho && d.csr_vec)
-        hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, 1>), dim3(blocks), dim3(kDecodeNT),
-                           (uint32_t)lds_bytes, stream, d);
-    else if (d.has_ortho)
-        hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, 2>), dim3(blocks), dim3(kDecodeNT),
-                           (uint32_t)lds_bytes, stream, d);
-    else
-        hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, 0>), dim3(blocks), dim3(kDecodeNT),
-                           (uint32_t)lds_bytes, stream, d);
+    hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, SPARSE>), dim3(blocks), dim3(kDecodeNT),
+                       (uint32_t)lds, stream, d);
     return hipGetLastError();
+}
+
+template <int MT, int GMODE, bool XLDS, int CPW>
+static hipError_t launch_decode_t(const DecodeArgs &d0, hipStream_t stream) {
+    DecodeArgs d = d0;
+    const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW);
+    if (lds > kDecodeLdsMax) return hipErrorInvalidValue;
+    if (d.has_ortho && d.csr_vec) return launch_decode_k<MT, GMODE, XLDS, CPW, 1>(d, lds, stream);
+    if (d.has_ortho) return launch_decode_k<MT, GMODE, XLDS, CPW, 2>(d, lds, stream);
+    return launch_decode_k<MT, GMODE, XLDS, CPW, 0>(d, lds, stream);
 }
 
 // Chunk-count bounds that can occur: the staged activation block is at most
 // 40 KB (so MT * K is bounded) and the global-memory A path takes CPW <= 8.
 template <int MT, int GMODE, bool XLDS>
-static hipError_t launch_decode_cpw(const DecodeArgs &d, int64_t lds, hipStream_t s) {
+static hipError_t launch_decode_cpw(const DecodeArgs &d, hipStream_t s) {
     constexpr bool c16 = XLDS && MT <= 4;
     constexpr bool c24 = XLDS && MT <= 2;
-    if (d.cpw <= 8) return launch_decode_t<MT, GMODE, XLDS, 8>(d, lds, s);
-    if (d.cpw <= 16 && c16) return launch_decode_t<MT, GMODE, XLDS, (c16 ? 16 : 8)>(d, lds, s);
-    if (c24) return launch_decode_t<MT, GMODE, XLDS, (c24 ? 24 : 8)>(d, lds, s);
+    if (d.cpw <= 8) return launch_decode_t<MT, GMODE, XLDS, 8>(d, s);
+    if (d.cpw <= 16 && c16) return launch_decode_t<MT, GMODE, XLDS, (c16 ? 16 : 8)>(d, s);
+    if (c24) return launch_decode_t<MT, GMODE, XLDS, (c24 ? 24 : 8)>(d, s);
     return hipErrorInvalidValue;  // excluded by decode_supported()
 }
 
 template <int GMODE, bool XLDS>
-static hipError_t launch_decode_mt(int mt, const DecodeArgs &d, int64_t lds, hipStream_t s) {
+static hipError_t launch_decode_mt(int mt, const DecodeArgs &d, hipStream_t s) {
     switch (mt) {
-        case 1: return launch_decode_cpw<1, GMODE, XLDS>(d, lds, s);
-        case 2: return launch_decode_cpw<2, GMODE, XLDS>(d, lds, s);
-        case 4: return launch_decode_cpw<4, GMODE, XLDS>(d, lds, s);
-        case 8: return launch_decode_cpw<8, GMODE, XLDS>(d, lds, s);
-        default: return launch_decode_cpw<16, GMODE, XLDS>(d, lds, s);
+        case 1: return launch_decode_cpw<1, GMODE, XLDS>(d, s);
+        case 2: return launch_decode_cpw<2, GMODE, XLDS>(d, s);
+        case 4: return launch_decode_cpw<4, GMODE, XLDS>(d, s);
+        case 8: return launch_decode_cpw<8, GMODE, XLDS>(d, s);
+        default: return launch_decode_cpw<16, GMODE, XLDS>(d, s);
     }
 }
 
@@ -474,22 +575,10 @@ hipError_t launch_decode(const ForwardArgs &a, hipStream_t stream) {
         while ((128LL << d.gshift) < a.G) d.gshift++;
     d.scale_pairs = (a.ngroups % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.scales) & 3) == 0);
     const bool xlds = decode_xlds(a.M, a.K);
-    int64_t lds = (int64_t)kDecodeW * 256 * 4 + (int64_t)mt * 16 * 4;
-    lds = (lds + 15) & ~int64_t(15);
-    d.lds_cr = (int)lds;
-    if (xlds) lds += (int64_t)mt * d.nchunks * 4;
-    lds = (lds + 15) & ~int64_t(15);
-    d.lds_xs = (int)lds;
-    if (xlds) lds += (int64_t)mt * d.xstride * 2;
-    lds = (lds + 15) & ~int64_t(15);
-    d.lds_e = (int)lds;
-    if (a.has_ortho && d.csr_vec) lds += (int64_t)kDecodeEStaged * (4 + 2);
-    if (lds > 64 * 1024) return hipErrorInvalidValue;
-
     const int gmode = !grouped ? 0 : (d.gshift == 0 && d.scale_pairs ? 1 : 2);
-    if (gmode == 1) return xlds ? launch_decode_mt<1, true>(mt, d, lds, stream) : launch_decode_mt<1, false>(mt, d, lds, stream);
-    if (gmode == 2) return xlds ? launch_decode_mt<2, true>(mt, d, lds, stream) : launch_decode_mt<2, false>(mt, d, lds, stream);
-    return xlds ? launch_decode_mt<0, true>(mt, d, lds, stream) : launch_decode_mt<0, false>(mt, d, lds, stream);
+    if (gmode == 1) return xlds ? launch_decode_mt<1, true>(mt, d, stream) : launch_decode_mt<1, false>(mt, d, stream);
+    if (gmode == 2) return xlds ? launch_decode_mt<2, true>(mt, d, stream) : launch_decode_mt<2, false>(mt, d, stream);
+    return xlds ? launch_decode_mt<0, true>(mt, d, stream) : launch_decode_mt<0, false>(mt, d, stream);
 }
 
 }  // namespace orth
