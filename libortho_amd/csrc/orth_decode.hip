@@ -153,18 +153,16 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     }
 
     // ---- CSR bounds: this thread's epilogue row, and the workgroup block
+    //      (loaded here, used after the staging).  The block bounds come
+    //      from one vector load (lane i: row_ptr[n0 + i]) read with
+    //      readlane: as a scalar load it would be issued late and waited for
+    //      before the CSR block loads.
     const int rl = tid >> 4, sub = tid & 15;
-    int32_t rs = 0, re = 0, e0 = 0, e1 = 0;
+    int32_t r_lo = 0, r_hi = 0, pv = 0;
     if (SPARSE) {
-        const int32_t r_lo = a.row_ptr[n0 + min(rl, last_row)];
-        const int32_t r_hi = a.row_ptr[n0 + min(rl, last_row) + 1];
-        const int32_t b_lo = a.row_ptr[n0];
-        const int32_t b_hi = a.row_ptr[n0 + last_row + 1];
-        rs = min(max(r_lo, 0), a.nnz);
-        re = min(max(r_hi, rs), a.nnz);
-        if (rl > last_row) re = rs;  // rows past N have no entries
-        e0 = min(max(b_lo, 0), a.nnz);
-        e1 = min(max(b_hi, e0), a.nnz);
+        r_lo = a.row_ptr[n0 + min(rl, last_row)];
+        r_hi = a.row_ptr[n0 + min(rl, last_row) + 1];
+        pv = a.row_ptr[n0 + min(lane, last_row + 1)];
     }
 
     // ---- per-row scale of the row this thread combines at the end
@@ -231,28 +229,6 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         }
     }
 
-    // ---- CSR block of the workgroup: 4 entries per thread per slot, from the
-    //      aligned start eb.  Addresses are clamped to the workgroup's last
-    //      aligned group (threads past the block re-read one cached line) and
-    //      to the last aligned group of the arrays (in bounds).
-    const int32_t eb = e0 & ~3;
-    const int32_t last4 = (a.nnz - 4) & ~3;
-    const int32_t wlast4 = min(max((e1 - 1) & ~3, eb), last4);
-    u32x4 ecv[ES];
-    uint2 evv[ES];
-    // staged slot of thread (wave, lane), group s: entries eb + 4 * slot ..
-    auto e_slot = [&](int s) -> int {
-        return WT ? wave * (kDecodeEStaged / W) + 4 * (lane + 64 * s) : 4 * (tid + NT * s);
-    };
-    if (SPARSE == 1) {
-#pragma unroll
-        for (int s = 0; s < ES; s++) {
-            const int32_t ic = min(eb + e_slot(s), wlast4);
-            ecv[s] = *reinterpret_cast<const u32x4 *>(a.col + ic);
-            evv[s] = *reinterpret_cast<const uint2 *>(a.vals + ic);
-        }
-    }
-
     // ---- stage this wave's activations (interleaved k order) and their
     //      per-chunk bias sums; only this wave reads them before the end
     const int wpieces = nci * 16;
@@ -276,6 +252,39 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                     }
                 }
             }
+        }
+    }
+
+    // ---- CSR block of the workgroup: 4 entries per thread per slot, from the
+    //      aligned start eb.  Addresses are clamped to the workgroup's last
+    //      aligned group (threads past the block re-read one cached line) and
+    //      to the last aligned group of the arrays (in bounds).  Issued after
+    //      the staging (held there by the scheduling barrier): the addresses
+    //      wait for the row pointers, and the staging need not.
+    __builtin_amdgcn_sched_barrier(0);
+    int32_t rs = 0, re = 0, e0 = 0, e1 = 0;
+    if (SPARSE) {
+        rs = min(max(r_lo, 0), a.nnz);
+        re = min(max(r_hi, rs), a.nnz);
+        if (rl > last_row) re = rs;  // rows past N have no entries
+        e0 = min(max(__builtin_amdgcn_readlane(pv, 0), 0), a.nnz);
+        e1 = min(max(__builtin_amdgcn_readlane(pv, last_row + 1), e0), a.nnz);
+    }
+    const int32_t eb = e0 & ~3;
+    const int32_t last4 = (a.nnz - 4) & ~3;
+    const int32_t wlast4 = min(max((e1 - 1) & ~3, eb), last4);
+    u32x4 ecv[ES];
+    uint2 evv[ES];
+    // staged slot of thread (wave, lane), group s: entries eb + 4 * slot ..
+    auto e_slot = [&](int s) -> int {
+        return WT ? wave * (kDecodeEStaged / W) + 4 * (lane + 64 * s) : 4 * (tid + NT * s);
+    };
+    if (SPARSE == 1) {
+#pragma unroll
+        for (int s = 0; s < ES; s++) {
+            const int32_t ic = min(eb + e_slot(s), wlast4);
+            ecv[s] = *reinterpret_cast<const u32x4 *>(a.col + ic);
+            evv[s] = *reinterpret_cast<const uint2 *>(a.vals + ic);
         }
     }
 
