@@ -31,9 +31,9 @@
 //  * Sparse ortho term: the CSR entries of the workgroup's 16 rows are
 //    contiguous; they are loaded with 16-byte loads into LDS (bounds first,
 //    then the block), then 16 lanes per row sum v*x with x from LDS, reduce
-//    with lane shuffles and add alpha*sum after the base term, as
-//    /root/reference/src/dual_gemm.cu:212-221 does.  alpha <= 0 skips it on
-//    a uniform branch without touching the CSR arrays.
+//    with DPP moves, and lane 0 of the row adds alpha*sum after the base term
+//    and stores, as /root/reference/src/dual_gemm.cu:212-221 does.  alpha <=
+//    0 takes a kernel without the term, which never touches the CSR arrays.
 #include "orth_common.h"
 
 namespace orth {
@@ -63,7 +63,6 @@ struct DecodeArgs {
     int cpw;           // chunks per wave, even, <= the CPW template bound
     int xstride;       // LDS row stride of the staged activations, in halves
     int lds_red;       // byte offsets of the LDS regions
-    int lds_sp;
     int lds_cr;
     int lds_xs;
     int lds_e;
@@ -105,7 +104,6 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     // WT: wave w's region holds its weights during the main loop, then its
     // split-K partials (1 KB), CSR columns (2 KB) and values (1 KB)
-    float *sp = reinterpret_cast<float *>(smem + a.lds_sp);     // [MT][RT] sparse sums
     float *cr = reinterpret_cast<float *>(smem + a.lds_cr);     // [MT][nchunks] bias sums (XLDS)
     f16 *xs = reinterpret_cast<f16 *>(smem + a.lds_xs);         // [MT][xstride] activations
     // split-K partials of wave w: [16 tokens][16 rows]
@@ -167,7 +165,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 
     // ---- per-row scale of the row this thread combines at the end
     f16 srow = (f16)0.0f;
-    if (!GROUPED) srow = a.scales[n0 + min(tid & 15, last_row)];
+    if (!GROUPED) srow = a.scales[n0 + min(SPARSE ? tid >> 4 : tid & 15, last_row)];
 
     // ---- group scales: lane (row nl, g) holds chunks 8i + 2g, 8i + 2g + 1
     //      (GMODE 1), or one scale per chunk (GMODE 2)
@@ -426,15 +424,26 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 }
             }
         }
+        // lane 0 of each row combines the split-K partials (visible since the
+        // barrier above), scales, adds alpha * sparse and stores
+        const int64_t n = n0 + rl;
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             const float s = group_sum<16>(sacc[m]);
-            if (sub == 0) sp[m * RT + rl] = s;
+            if (sub == 0 && m < a.M && n < a.N) {
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < W; w++) v += red(w)[m * 16 + rl];
+                if (!GROUPED) v *= (float)srow;
+                v += a.alpha * s;
+                a.y[(int64_t)m * a.N + n] = (f16)v;
+            }
         }
+        return;
     }
     __syncthreads();
 
-    // ---- combine split-K partials, scale, add alpha * sparse, store
+    // ---- combine split-K partials, scale, store
     if (tid < MT * RT) {
         const int m = tid >> 4, r = tid & 15;
         const int64_t n = n0 + r;
@@ -443,7 +452,6 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 #pragma unroll
             for (int w = 0; w < W; w++) v += red(w)[m * 16 + r];
             if (!GROUPED) v *= (float)srow;
-            if (SPARSE) v += a.alpha * sp[m * RT + r];
             a.y[(int64_t)m * a.N + n] = (f16)v;
         }
     }
@@ -454,15 +462,13 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 static const int64_t kDecodeLdsMax = 160 * 1024;
 
 // LDS layout of decode_kernel<MT, *, XLDS, CPW, *>: weight regions (WT) or
-// split-K partials, sparse sums, bias sums, activations, staged CSR block
+// split-K partials, bias sums, activations, staged CSR block
 // (outside the weight regions when not WT).  Returns the bytes.
 static int64_t decode_lds_layout(DecodeArgs &d, int mt, bool xlds, int cpw_bound) {
     auto al = [](int64_t v) { return (v + 15) & ~int64_t(15); };
     const bool wt = decode_wt(mt, xlds);
     int64_t off = wt ? (int64_t)kDecodeW * cpw_bound * 1024 : (int64_t)kDecodeW * 1024;
     d.lds_red = 0;
-    d.lds_sp = (int)off;
-    off = al(off + (int64_t)mt * 16 * 4);
     d.lds_cr = (int)off;
     if (xlds) off = al(off + (int64_t)mt * d.nchunks * 4);
     d.lds_xs = (int)off;
