@@ -234,6 +234,8 @@ def summarize_pmc(fetch_csv, write_csv):
         factor = (sum(copies) / len(copies)) * 1024.0 / COPY_BYTES
         kern = {}
         for _, name, v in rows:
+            if name.startswith("_ZN4orth20skinny_reduce_kernel"):  # the trace keeps this name mangled
+                name = "orth::skinny_reduce_kernel"
             if "orth::" in name:
                 kern.setdefault(name, []).append(v)
         per[counter] = (factor, kern)
