@@ -65,6 +65,7 @@ struct SkinnyArgs {
     int nsteps;          // K / 64
     int cps;             // chunks per slice (even)
     int S;               // slices
+    int nblocks;         // 128-row blocks
     int xstride;         // LDS row stride of the staged activations, in halves
     int lds_cr, lds_xs, lds_sp, lds_e, lds_idx;  // byte offsets of the LDS regions
     float alpha;
@@ -118,7 +119,13 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int nl = lane & 15, g = lane >> 4;
-    const int blk = blockIdx.x / a.S, slice = blockIdx.x - blk * a.S;
+    // Workgroup ids are dealt round-robin to the 8 XCDs: all K slices of row
+    // block blk run on XCD blk % 8, as does the reduction workgroup of blk,
+    // so a block's partials are written and read through one L2.  The grid
+    // is padded to 8 * ceil(nblocks / 8) * S.
+    const int q = (int)(blockIdx.x >> 3);
+    const int blk = (int)(blockIdx.x & 7) + 8 * (q / a.S), slice = q - (q / a.S) * a.S;
+    if (blk >= a.nblocks) return;
     const int64_t n0 = (int64_t)blk * kSkRows;
     const int kc0 = slice * a.cps;                               // first chunk of the slice
     const int nci = max(0, min(a.cps, a.nchunks - kc0));         // uniform
@@ -408,44 +415,55 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
 
 // y = sum of the S partials, in slice order.  Thread t takes 4 consecutive
 // outputs of one token (N % 4 == 0) or one output (otherwise).
-__global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f16 *y, int64_t MN, int S,
+__global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f16 *y, int M, int64_t N, int S,
                                                             int vec4) {
-    // the partials were written by other XCDs and miss this L2: all loads of
-    // a group of 8 slices are issued before the first add (addresses clamped
-    // to the last slice, the extra ones not added), sums in slice order
+    // workgroup blk (on XCD blk % 8, like the slices of row block blk) adds
+    // the S partials of rows [128 blk, 128 blk + 128) for every token.  The
+    // loads of a group of 8 slices are issued before the first add (addresses
+    // clamped to the last slice, the extra ones not added); sums in slice order.
     constexpr int U = 8;
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.x * kSkRows;
+    const int64_t MN = (int64_t)M * N;
     if (vec4) {
-        const int64_t o = t * 4;
-        if (o >= MN) return;
-        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < S; s0 += U) {
-            f32x4 w[U];
+        for (int idx = threadIdx.x; idx < M * (kSkRows / 4); idx += 256) {
+            const int m = idx / (kSkRows / 4);
+            const int64_t n = n0 + 4 * (idx - m * (kSkRows / 4));
+            if (n >= N) continue;
+            const int64_t o = (int64_t)m * N + n;
+            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int s0 = 0; s0 < S; s0 += U) {
+                f32x4 w[U];
 #pragma unroll
-            for (int u = 0; u < U; u++)
-                w[u] = *reinterpret_cast<const f32x4 *>(part + (int64_t)min(s0 + u, S - 1) * MN + o);
+                for (int u = 0; u < U; u++)
+                    w[u] = *reinterpret_cast<const f32x4 *>(part + (int64_t)min(s0 + u, S - 1) * MN + o);
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                if (s0 + u == 0) v = w[u];
-                else if (s0 + u < S) v += w[u];
+                for (int u = 0; u < U; u++) {
+                    if (s0 + u == 0) v = w[u];
+                    else if (s0 + u < S) v += w[u];
+                }
             }
+            const f16x2 lo = {(f16)v[0], (f16)v[1]}, hi = {(f16)v[2], (f16)v[3]};
+            *reinterpret_cast<uint2 *>(y + o) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
         }
-        const f16x2 lo = {(f16)v[0], (f16)v[1]}, hi = {(f16)v[2], (f16)v[3]};
-        *reinterpret_cast<uint2 *>(y + o) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
     } else {
-        if (t >= MN) return;
-        float v = 0.f;
-        for (int s0 = 0; s0 < S; s0 += U) {
-            float w[U];
+        for (int idx = threadIdx.x; idx < M * kSkRows; idx += 256) {
+            const int m = idx / kSkRows;
+            const int64_t n = n0 + (idx - m * kSkRows);
+            if (n >= N) continue;
+            const int64_t o = (int64_t)m * N + n;
+            float v = 0.f;
+            for (int s0 = 0; s0 < S; s0 += U) {
+                float w[U];
 #pragma unroll
-            for (int u = 0; u < U; u++) w[u] = part[(int64_t)min(s0 + u, S - 1) * MN + t];
+                for (int u = 0; u < U; u++) w[u] = part[(int64_t)min(s0 + u, S - 1) * MN + o];
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                if (s0 + u == 0) v = w[u];
-                else if (s0 + u < S) v += w[u];
+                for (int u = 0; u < U; u++) {
+                    if (s0 + u == 0) v = w[u];
+                    else if (s0 + u < S) v += w[u];
+                }
             }
+            y[o] = (f16)v;
         }
-        y[t] = (f16)v;
     }
 }
 
@@ -575,6 +593,7 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     d.nchunks = (int)(a.K / 128);
     d.cps = sh.cps;
     d.S = sh.S;
+    d.nblocks = sh.nblocks;
     d.xstride = sh.xstride;
     d.lds_cr = sh.lds_cr;
     d.lds_xs = sh.lds_xs;
@@ -587,7 +606,7 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     // row starts on a pair (even group count, 4-byte aligned scales)
     const bool pairs = (a.ngroups & 1) == 0 && (reinterpret_cast<uintptr_t>(a.scales) & 3) == 0;
     const int gmode = a.ngroups == 1 ? 0 : (d.gshift == 0 && pairs ? 1 : 2);
-    const int blocks = sh.nblocks * sh.S;
+    const int blocks = ((sh.nblocks + 7) / 8) * 8 * sh.S;  // padded: see skinny_kernel
     hipError_t e;
     switch (sh.ntt) {
         case 1: e = skinny_launch_n<1>(d, gmode, sparse, blocks, sh.lds_bytes, stream); break;
@@ -596,11 +615,9 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
         default: e = skinny_launch_n<4>(d, gmode, sparse, blocks, sh.lds_bytes, stream); break;
     }
     if (e != hipSuccess || sh.S == 1) return e;
-    const int64_t MN = a.M * a.N;
     const int vec4 = (a.N % 4 == 0) ? 1 : 0;
-    const int64_t threads = vec4 ? MN / 4 : MN;
-    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, part,
-                       static_cast<f16 *>(a.y), MN, sh.S, vec4);
+    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)sh.nblocks), dim3(256), 0, stream, part,
+                       static_cast<f16 *>(a.y), (int)a.M, a.N, sh.S, vec4);
     return hipGetLastError();
 }
 
