@@ -255,9 +255,10 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
     const int policy = g_policy.load(std::memory_order_relaxed);
     const bool dec_ok = decode_supported(a);
     const bool pre_ok = prefill_supported(a);
-    // the mid-batch kernel needs an ortho plan for the ortho term; without
-    // one, batches the decode kernel takes go there (no plan to build)
-    const bool sk_ok = skinny_supported(a) && (!a.has_ortho || plan_supported(a));
+    // the mid-batch kernel locates each row's ortho entries with the plan's
+    // chunk table; without a plan it filters whole rows, so batches the
+    // decode kernel takes go there instead
+    const bool sk_ok = skinny_supported(a);
     const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok);
     int kernel;
     switch (policy) {
@@ -294,19 +295,8 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
             rc = workspace_for(dev, stream, pbytes, &part);
             if (rc != ORTH_OK) return rc;
         }
-        if (a.has_ortho && !plan) {
-            // stream-ordered temporary plan, as for the prefill kernel
-            const int64_t pb = plan_bytes_for(a.N, a.K, a.nnz);
-            void *tmp = nullptr;
-            e = hipMallocAsync(&tmp, (size_t)pb, stream);
-            if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (temporary ortho plan)");
-            e = launch_plan_build(a, tmp, stream);
-            if (e == hipSuccess) e = launch_skinny(a, tmp, cus, part, stream);
-            hipError_t f = hipFreeAsync(tmp, stream);
-            if (e == hipSuccess) e = f;
-        } else {
-            e = launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
-        }
+        // without a plan the kernel filters each row's CSR by column
+        e = launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
     } else if (kernel == KERNEL_PREFILL) {
         if (a.has_ortho && !plan) {
             // stream-ordered temporary plan: allocated, built, used and freed

@@ -32,14 +32,19 @@ namespace orth {
 //   PlanHeader (64 bytes)
 //   int32 offsets[nblocks][nksteps + 1]   absolute entry index per (block, step)
 //   uint32 entries[nnz]                   (row_in_block << 24) | (col_in_step << 16) | fp16 bits
-// Entries of one (block, step) are ordered by row then by CSR position.
+//   uint16 chunks[N][K/128 + 1]           (K % 128 == 0 only) per row, the number of
+//                                         its CSR entries with column < 128 c
+// Entries of one (block, step) are ordered by row then by CSR position.  The
+// chunk table locates a row's entries of columns [128 c0, 128 c1) in the CSR
+// itself when the row's columns ascend strictly (flag kPlanUnsorted clear).
 
 static const uint32_t kPlanMagic = 0x504f5254u;  // "TROP"
-static const uint32_t kPlanVersion = 1;
+static const uint32_t kPlanVersion = 2;
 static const int kPlanBN = 128;
 static const int kPlanBK = 64;
 static const uint32_t kPlanNonCanonical = 1u;  // duplicate or unsorted columns in a row
 static const uint32_t kPlanMalformed = 2u;     // row_ptr not monotone within [0, nnz]
+static const uint32_t kPlanUnsorted = 4u;      // some row's columns (any value) do not ascend strictly
 
 struct PlanHeader {
     uint32_t magic, version;
@@ -56,9 +61,19 @@ int64_t plan_offsets_bytes(int64_t N, int64_t K) {
     return ((nblocks * (nk + 1) * 4) + 15) & ~int64_t(15);
 }
 
+// Byte offset of the chunk table (16-byte aligned, after the entries) and
+// its size; K % 128 != 0 has none.
+int64_t plan_chunks_at(int64_t N, int64_t K, int64_t nnz) {
+    return (((int64_t)sizeof(PlanHeader) + plan_offsets_bytes(N, K) + 4 * nnz) + 15) & ~int64_t(15);
+}
+
+int64_t plan_chunks_bytes(int64_t N, int64_t K) {
+    return K % 128 == 0 ? ((N * (K / 128 + 1) * 2) + 15) & ~int64_t(15) : 0;
+}
+
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) {
     if (nnz <= 0) return 0;
-    return (int64_t)sizeof(PlanHeader) + plan_offsets_bytes(N, K) + 4 * nnz;
+    return plan_chunks_at(N, K, nnz) + plan_chunks_bytes(N, K);
 }
 
 // Largest K the plan builder's LDS counters take (int32 per (step, row)).
@@ -95,7 +110,7 @@ __device__ __forceinline__ uint32_t value_bits_f16(const void *vals, int dtype, 
 // block's CSR entries by 64-column step, stable in (row, CSR position).
 __global__ void __launch_bounds__(256) plan_build_kernel(ForwardArgs a, PlanHeader *h,
                                                          int32_t *offsets, uint32_t *entries,
-                                                         int nksteps) {
+                                                         uint16_t *chunks, int nksteps) {
     extern __shared__ __align__(16) int32_t cnt[];  // [nksteps][BN], then partials[256]
     int32_t *partials = cnt + nksteps * kPlanBN;
     __shared__ int32_t s_flags;
@@ -115,15 +130,27 @@ __global__ void __launch_bounds__(256) plan_build_kernel(ForwardArgs a, PlanHead
         const int64_t ra = a.row_ptr[n], rb = a.row_ptr[n + 1];
         if (ra < 0 || rb < ra || rb > a.nnz) myflags |= kPlanMalformed;
         csr_row_range(a.row_ptr, n, a.nnz, rs, re);
-        int32_t prev = -1;
+        int32_t prev = -1, praw = INT32_MIN;
+        const int nch = chunks ? (int)(a.K / 128) : 0;
+        uint16_t *crow = chunks ? chunks + n * (int64_t)(nch + 1) : nullptr;
+        int cnext = 0;  // next chunk boundary to record
         for (int32_t j = rs; j < re; j++) {
             const int32_t c = a.col[j];
+            if (c <= praw) myflags |= kPlanUnsorted;
+            praw = c;
+            // boundaries 128 cb <= c end before entry j (meaningful when sorted)
+            if (crow)
+                for (; cnext <= nch && (int64_t)cnext * 128 <= (int64_t)c; cnext++)
+                    crow[cnext] = (uint16_t)min(j - rs, 65535);
             if (c >= 0 && c < a.K) {
                 cnt[(c / kPlanBK) * kPlanBN + r] += 1;
                 if (c <= prev) myflags |= kPlanNonCanonical;
                 prev = c;
             }
         }
+        if (crow)
+            for (; cnext <= nch; cnext++) crow[cnext] = (uint16_t)min(re - rs, 65535);
+        if (re - rs > 65535) myflags |= kPlanUnsorted;  // counts past 16 bits
     }
     if (myflags) atomicOr(&s_flags, (int32_t)myflags);
     __syncthreads();
@@ -194,8 +221,11 @@ hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t strea
     hipLaunchKernelGGL(plan_init_kernel, dim3(1), dim3(64), 0, stream, h, nblocks, nksteps, a.N,
                        a.K, a.nnz);
     const size_t lds = ((size_t)nksteps * kPlanBN + 256) * sizeof(int32_t);
+    uint16_t *chunks = plan_chunks_bytes(a.N, a.K)
+                           ? reinterpret_cast<uint16_t *>(static_cast<char *>(plan) + plan_chunks_at(a.N, a.K, a.nnz))
+                           : nullptr;
     hipLaunchKernelGGL(plan_build_kernel, dim3(nblocks), dim3(256), lds, stream, a, h, offsets,
-                       entries, nksteps);
+                       entries, chunks, nksteps);
     return hipGetLastError();
 }
 

@@ -15,13 +15,18 @@
 //    16-token tile are the A operand, read from LDS (interleaved k order).
 //    The bias is removed per chunk with the activation sums computed while
 //    staging; group scales multiply each chunk's FP32 partial.
-//  * The sparse ortho term of the slice comes from the ortho plan: its
-//    (128-row block, 64-column step) buckets are sorted by row.  The slice's
-//    entries are staged in LDS, counted per (bucket, row) with LDS atomics
-//    and turned into row starts by a DPP prefix sum per bucket; four threads
-//    per row then multiply the row's entries with the staged activations,
-//    first the leading entry of every bucket (LDS reads issued in batches),
-//    then the rest.  Sums are formed in a fixed order: the result does not
+//  * The sparse ortho term reads the CSR itself.  The ortho plan's chunk
+//    table (per row, the count of entries below each 128-column boundary)
+//    gives each row's entries inside the slice as one contiguous CSR range
+//    when the rows' columns ascend; otherwise (or without a plan) each row's
+//    whole range is read and filtered by column, in batches of eight
+//    entries.  Up to 16 tokens, four consecutive lanes share a row: each
+//    loads two of every eight entries, DPP quad broadcasts hand all eight to
+//    the four, each multiplies them with four tokens' staged activations,
+//    and the sums reach the MFMA lanes through LDS.  From 17 tokens (more
+//    registers, and an LDS exchange would cost the second workgroup per CU)
+//    each lane takes the row and tokens of its own MFMA output and reads the
+//    row's entries itself.  Sums are formed in CSR order: the result does not
 //    depend on scheduling.
 //  * When the row blocks alone cannot fill the GPU, K is split over S
 //    workgroups.  Each writes its FP32 partial (ortho term included) to a
@@ -35,13 +40,22 @@
 
 namespace orth {
 
+int64_t plan_chunks_at(int64_t N, int64_t K, int64_t nnz);  // orth_prefill.hip
+int64_t plan_chunks_bytes(int64_t N, int64_t K);
+
 constexpr int kSkNT = 512;            // 8 waves
 constexpr int kSkRows = 128;          // rows per workgroup (= ortho plan block)
 constexpr int kSkMaxCPS = 8;          // chunks per slice (compile-time bound)
-constexpr int kSkESlots = 8;          // plan entries per thread loaded at entry
-constexpr int kSkEStaged = kSkESlots * 512;  // plan entries staged in LDS per workgroup
-constexpr int kSkPlanBK = 64;         // plan column step
+constexpr int kSkEB = 8;              // CSR entries of a row per batch
+
+// x from lane s of each group of four lanes (DPP quad_perm)
+template <int S>
+__device__ __forceinline__ int quad_bcast(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, S | (S << 2) | (S << 4) | (S << 6), 0xf, 0xf, false);
+}
 constexpr uint32_t kSkPlanMagic = 0x504f5254u;
+constexpr uint32_t kSkPlanVersion = 2;
+constexpr uint32_t kSkPlanUnsorted = 4u;  // plan flag: the chunk table does not locate ranges
 
 // Chunks per slice the kernel of ntt token tiles is built for: even (group
 // scales are read in pairs) and with at most 8 activation pieces per thread.
@@ -52,9 +66,11 @@ struct SkinnyArgs {
     const f16 *scales;
     int ngroups;
     int gshift;          // group of chunk c is c >> gshift (G = 128 << gshift)
-    const int32_t *poffs;     // plan offsets [nblocks][nsteps + 1]
-    const uint32_t *pents;    // plan entries
-    const uint32_t *phdr;     // plan header: magic, version, bn, bk, nblocks, nsteps, n, k, nnz
+    const int32_t *row_ptr;   // CSR of the ortho term
+    const int32_t *col;
+    const f16 *vals;
+    const uint16_t *chunks;   // plan chunk table [N][nchunks + 1], or null
+    const uint32_t *phdr;     // plan header (magic, version, bn, bk, nblocks, nsteps, n, k, nnz, flags), or null
     int32_t nnz;
     const f16 *x;
     f16 *y;
@@ -62,58 +78,31 @@ struct SkinnyArgs {
     int K;
     int64_t N;
     int nchunks;         // K / 128
-    int nsteps;          // K / 64
     int cps;             // chunks per slice (even)
     int S;               // slices
     int nblocks;         // 128-row blocks
     int xstride;         // LDS row stride of the staged activations, in halves
-    int lds_cr, lds_xs, lds_sp, lds_e, lds_idx;  // byte offsets of the LDS regions
+    int lds_cr, lds_xs, lds_sp;  // byte offsets of the LDS regions
     float alpha;
     float *part;         // [S][M][N] partials (S > 1)
 };
 
-// v[i] for wave-uniform v and a runtime i in [0, L): a chain of selects, so
-// that v stays in registers (a runtime subscript moves the array to per-lane
-// scratch memory, which is written back through the L2 to HBM).  The
-// readfirstlane keeps the compiler from folding the chain back into a
-// subscripted load.
-template <int L>
-__device__ __forceinline__ int32_t pick(const int32_t (&v)[L], int i) {
-    int32_t r = __builtin_amdgcn_readfirstlane(v[0]);
-#pragma unroll
-    for (int k = 1; k < L; k++) r = i == k ? __builtin_amdgcn_readfirstlane(v[k]) : r;
-    return r;
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave with DPP moves: shifts
-// by 1, 2, 4, 8 within each row of 16 lanes, then row 0's total into row 1
-// and row 2's into row 3 (row_bcast:15), then the total of rows 0-1 into
-// rows 2-3 (row_bcast:31).  Lanes without a source take 0.
-__device__ __forceinline__ int wave_inclusive_sum(int x) {
-    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
-    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
-    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
-    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
-    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
-    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
-    return x;
-}
-
 // GMODE: 0 per-row scale (G == K); 1 G = 128, scales read as aligned pairs;
 // 2 any G = 128 * 2^j.  NTT: 16-token tiles.  CPS: chunk bound per slice.
 template <int NTT, int GMODE, int CPS, bool SPARSE>
-__global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
+__global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT <= 2 ? 4 : 2))) skinny_kernel(SkinnyArgs a) {
     constexpr int MP = NTT * 16;                     // padded tokens
     constexpr int XP = (MP * CPS * 16 + kSkNT - 1) / kSkNT;  // 16-byte pieces per thread
     constexpr int SW = (CPS + 7) / 8;
     constexpr bool GROUPED = GMODE != 0;
+    // QUAD: four consecutive lanes per row in the sparse term (one token tile)
+    constexpr bool QUAD = NTT == 1;
+    constexpr int EL = QUAD ? kSkEB / 4 : kSkEB;  // entries a lane loads per batch
 
     extern __shared__ __align__(16) unsigned char smem[];
     float *cr = reinterpret_cast<float *>(smem + a.lds_cr);     // [cps][MP] bias sums
     f16 *xs = reinterpret_cast<f16 *>(smem + a.lds_xs);         // [MP][xstride] activations
-    float *sp = reinterpret_cast<float *>(smem + a.lds_sp);     // [128][MP] sparse sums
-    uint32_t *es = reinterpret_cast<uint32_t *>(smem + a.lds_e);  // staged plan entries
-    int32_t *ridx = reinterpret_cast<int32_t *>(smem + a.lds_idx);  // [2 cps][129] row starts per bucket
+    float *sp = reinterpret_cast<float *>(smem + a.lds_sp);     // QUAD: [128][MP] sparse sums
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -144,17 +133,27 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
         xreg[i] = *reinterpret_cast<const u32x4 *>(a.x + (int64_t)m * K + c * 128 + (p & 15) * 8);
     }
 
-    // ---- plan words, one vector load per wave issued after the activations
-    //      and before the weights (loads complete in order: the staging does
-    //      not wait for it, and it does not wait for the weights): lanes
-    //      0 .. 2 CPS read the slice's bucket offsets, lanes 32 .. 43 the plan
-    //      header words 0 .. 11
-    int32_t pword = 0;
+    // ---- sparse term inputs of this lane's row, issued after the
+    //      activations and before the weights (loads complete in order: the
+    //      staging does not wait for them, nor they for the weights): the
+    //      row's CSR bounds, its chunk-table counts at the slice's ends, and
+    //      (lanes 0 .. 12) the plan header.  Without a plan the addresses fall
+    //      back to the row pointers (read, not used).
+    // (QUAD: row tid / 4 of the block, tokens tid % 4 + 4 i; else the MFMA
+    //  output's row 16 w + nl)
+    const int sr = QUAD ? tid >> 2 : wave * 16 + nl, tg = tid & 3;
+    const int64_t sn = min(n0 + sr, a.N - 1);
+    int32_t rp0 = 0, rp1 = 0, hw = 0;
+    uint32_t ck0 = 0, ck1 = 0;
     if (SPARSE) {
-        const int64_t ob = (int64_t)blk * (a.nsteps + 1);
-        const int32_t *src = lane < 32 ? a.poffs + (ob + min(2 * kc0 + min(lane, 2 * nci), a.nsteps))
-                                       : reinterpret_cast<const int32_t *>(a.phdr) + min(lane - 32, 11);
-        pword = *src;
+        rp0 = a.row_ptr[sn];
+        rp1 = a.row_ptr[sn + 1];
+        const bool tab = a.chunks != nullptr;
+        const uint16_t *ct = tab ? a.chunks + sn * (int64_t)(a.nchunks + 1) : reinterpret_cast<const uint16_t *>(a.row_ptr);
+        ck0 = ct[tab ? kc0 : 0];
+        ck1 = ct[tab ? kc0 + nci : 0];
+        const uint32_t *hp = a.phdr ? a.phdr : reinterpret_cast<const uint32_t *>(a.row_ptr);
+        hw = (int32_t)hp[a.phdr ? min(lane, 12) : 0];
     }
 
     // ---- scales
@@ -196,41 +195,40 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
             if ((p & 15) == 0) cr[c * MP + m] = b;
         }
     }
-    if (SPARSE)
-        for (int i = tid; i < 2 * CPS * 129; i += kSkNT) ridx[i] = 0;
     __syncthreads();
 
-    // ---- bucket offsets of the slice (uniform), checked against the header.
-    //      Read after the staging and its barrier (kept there by the
-    //      scheduling barrier): the offsets miss the caches more often than
-    //      the activations, and neither need wait for them.
+    // ---- the row's CSR range in the slice.  With a matching plan whose
+    //      rows ascend, the chunk table gives it; otherwise the whole row is
+    //      read and filtered by column.  (Read after the staging and its
+    //      barrier, kept there by the scheduling barrier.)
     __builtin_amdgcn_sched_barrier(0);
-    int32_t soff[2 * CPS + 1];
-    int32_t e_lo = 0, e_hi = 0;
+    int32_t lo = 0, hi = 0;
+    constexpr int EB = kSkEB;
+    int32_t ecol[EL], ecol2[EL];  // the first two batches, loaded before the dense term
+    uint32_t eval[EL], eval2[EL];
+    // entry u of this lane in the batch at j0: j0 + tg + 4 u (QUAD) or j0 + u
+    auto load_batch = [&](int32_t j0, int32_t (&c)[EL], uint32_t (&v)[EL]) {
+        const int32_t jl = min(max(hi - 1, lo), a.nnz - 1);
+#pragma unroll
+        for (int u = 0; u < EL; u++) {
+            const int32_t j = min(j0 + (QUAD ? tg + 4 * u : u), jl);
+            c[u] = a.col[j];
+            v[u] = __builtin_bit_cast(uint16_t, a.vals[j]);
+        }
+    };
     if (SPARSE) {
-        auto word = [&](int l) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane(pword, l); };
+        auto word = [&](int l) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane(hw, l); };
         auto dword = [&](int l) -> int64_t { return (int64_t)(word(l) | ((uint64_t)word(l + 1) << 32)); };
-        const bool plan_ok = (word(32) == kSkPlanMagic) & (word(33) == 1u) & (dword(38) == a.N) &
-                             (dword(40) == (int64_t)K) & (dword(42) == (int64_t)a.nnz);
-#pragma unroll
-        for (int i = 0; i <= 2 * CPS; i++) soff[i] = min(max(__builtin_amdgcn_readlane(pword, i), 0), a.nnz);
-        e_lo = soff[0];
-        e_hi = plan_ok ? max(min(max(__builtin_amdgcn_readlane(pword, 2 * nci), 0), a.nnz), e_lo) : e_lo;
-        // monotone within [e_lo, e_hi] whatever the plan holds
-#pragma unroll
-        for (int i = 0; i <= 2 * CPS; i++) soff[i] = min(max(soff[i], i ? soff[i - 1] : e_lo), e_hi);
+        const bool fast = (a.phdr != nullptr) & (a.chunks != nullptr) & (word(0) == kSkPlanMagic) &
+                          (word(1) == kSkPlanVersion) & (dword(6) == a.N) & (dword(8) == (int64_t)K) &
+                          (dword(10) == (int64_t)a.nnz) & ((word(12) & kSkPlanUnsorted) == 0);
+        const int32_t rs = min(max(rp0, 0), a.nnz), re = min(max(rp1, rs), a.nnz);
+        lo = fast ? rs + min((int32_t)ck0, re - rs) : rs;
+        hi = fast ? rs + min(max((int32_t)ck1, (int32_t)ck0), re - rs) : re;
+        if (n0 + sr >= a.N) hi = lo;  // rows past N
+        load_batch(lo, ecol, eval);
+        load_batch(lo + EB, ecol2, eval2);
     }
-
-    // ---- the slice's plan entries (up to kSkEStaged; more are read from
-    //      memory in the sparse pass).  Addresses past the slice repeat its
-    //      last entry: no bytes beyond the slice's own are fetched.
-    uint32_t ereg[SPARSE ? kSkESlots : 1];
-    if (SPARSE) {
-        const int32_t elast = min(max(e_hi - 1, e_lo), max(a.nnz - 1, 0));
-#pragma unroll
-        for (int i = 0; i < kSkESlots; i++) ereg[i] = a.pents[min(e_lo + tid + kSkNT * i, elast)];
-    }
-
 
     // ---- dense term: wave w, rows 16 w + nl, token tiles tt
     f32x4 acc[NTT];
@@ -281,102 +279,62 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
         }
     }
 
-    // ---- sparse term of the slice.  The slice's buckets are sorted by row,
-    //      so a count per (bucket, row) and a prefix sum per bucket give each
-    //      row's entries; thread (row r, token group tg) then multiplies
-    //      them, in entry order, with the staged activations.
-    constexpr int MQ = MP / 4;  // tokens per thread: tg, tg + 4, ...
+    // ---- sparse term, in batches of eight entries; columns outside the
+    //      slice are skipped.  Token t of the lane: QUAD tg + 4 t, else
+    //      16 (t / 4) + 4 g + t % 4 (the MFMA output's tokens).
+    constexpr int TQ = QUAD ? MP / 4 : NTT * 4;  // tokens per lane
+    float sacc[SPARSE ? TQ : 1];
     if (SPARSE) {
-        constexpr int NB = 2 * CPS;  // buckets (64-column steps) of a slice
-        const int32_t staged_hi = e_lo + min(e_hi - e_lo, kSkEStaged);
-        const uint32_t *pents = a.pents;
-        // Entries below staged_hi are read from LDS, the rest (slices of more
-        // than kSkEStaged entries) from memory, in loops of their own: one
-        // accessor for both would become a flat load, which waits for memory
-        // latency on every entry.
-        // counts: entry i of bucket b (soff[b] <= i < soff[b+1]) adds 1 to
-        // (b, row + 1); the staged entries are counted from registers
-        auto count = [&](int32_t i, uint32_t e) {
-            int b = 0;
 #pragma unroll
-            for (int k = 1; k < NB; k++) b += i >= soff[k] ? 1 : 0;
-            atomicAdd(&ridx[b * 129 + 1 + (int)((e >> 24) & 0x7f)], 1);
-        };
-#pragma unroll
-        for (int i = 0; i < kSkESlots; i++) {
-            es[tid + kSkNT * i] = ereg[i];
-            const int32_t idx = e_lo + tid + kSkNT * i;
-            if (idx < staged_hi) count(idx, ereg[i]);
-        }
-        for (int32_t i = staged_hi + tid; i < e_hi; i += kSkNT) count(i, pents[i]);
-        __syncthreads();
-        // prefix sums: ridx[b][r] = first entry of row r in bucket b
-        for (int b = wave; b < NB; b += kSkNT / 64) {
-            int32_t *t = ridx + b * 129;
-            const int v0 = t[1 + 2 * lane], v1 = t[2 + 2 * lane];
-            const int incl = wave_inclusive_sum(v0 + v1);
-            const int32_t sb = pick(soff, b);
-            const int base = sb + incl - v0 - v1;       // before row 2 lane
-            t[1 + 2 * lane] = base + v0;                // start of row 2 lane + 1
-            t[2 + 2 * lane] = base + v0 + v1;           // start of row 2 lane + 2
-            if (lane == 0) t[0] = sb;
-        }
-        __syncthreads();
-        const int r = tid >> 2, tg = tid & 3;
-        float sacc[MQ];
-#pragma unroll
-        for (int i = 0; i < MQ; i++) sacc[i] = 0.f;
+        for (int t = 0; t < TQ; t++) sacc[t] = 0.f;
+        const int32_t c0 = kc0 * 128, cw = nci * 128;
         const int xstride = a.xstride;
-        auto fma_entry = [&](int cbase, uint32_t e) {
-            const int cl = cbase + (int)((e >> 16) & 0x3f);  // column within the slice
-            const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
-            const int xi = (cl & ~7) | interleaved_pos(cl & 7);
+        auto fma_batch = [&](int32_t j0, const int32_t (&c)[EL], const uint32_t (&v)[EL]) {
 #pragma unroll
-            for (int i2 = 0; i2 < MQ; i2++) sacc[i2] += v * (float)xs[(tg + 4 * i2) * xstride + xi];
+            for (int e = 0; e < kSkEB; e++) {
+                int32_t ce;
+                uint32_t ve;
+                if (QUAD) {  // entry j0 + e sits in lane e % 4 of the quad, slot e / 4
+                    const int slot = e >> 2;
+                    switch (e & 3) {
+                        case 0: ce = quad_bcast<0>(c[slot]); ve = (uint32_t)quad_bcast<0>((int)v[slot]); break;
+                        case 1: ce = quad_bcast<1>(c[slot]); ve = (uint32_t)quad_bcast<1>((int)v[slot]); break;
+                        case 2: ce = quad_bcast<2>(c[slot]); ve = (uint32_t)quad_bcast<2>((int)v[slot]); break;
+                        default: ce = quad_bcast<3>(c[slot]); ve = (uint32_t)quad_bcast<3>((int)v[slot]); break;
+                    }
+                } else {
+                    ce = c[e % EL];
+                    ve = v[e % EL];
+                }
+                const int32_t cl = ce - c0;
+                const bool ok = (j0 + e < hi) & (cl >= 0) & (cl < cw);
+                const int cc = ok ? cl : 0;
+                const float val = (float)__builtin_bit_cast(f16, (uint16_t)(ve & 0xffffu));
+                const int xi = (cc & ~7) | interleaved_pos(cc & 7);
+#pragma unroll
+                for (int t = 0; t < TQ; t++) {
+                    const int m = QUAD ? tg + 4 * t : 16 * (t >> 2) + 4 * g + (t & 3);
+                    const float pr = val * (float)xs[m * xstride + xi];
+                    sacc[t] += ok ? pr : 0.f;
+                }
+            }
         };
-        // First pass: the first entry of every bucket of row r, GB buckets at
-        // a time, so that each round of LDS reads (bounds, entries,
-        // activations) is issued together.  An absent entry reads as value 0
-        // at column 0 of the slice (a column of a bucket past the host's
-        // chunk count would lie outside the staged activations).
-        constexpr int GB = (32 / MQ) < 2 ? 2 : (32 / MQ) > NB ? NB : (32 / MQ);
-        uint32_t more = 0;  // bit st: bucket st has entries the first pass did not take
-#pragma unroll
-        for (int s0 = 0; s0 < NB; s0 += GB) {
-            int32_t lo[GB], hi[GB];
-#pragma unroll
-            for (int u = 0; u < GB; u++) {
-                const int st = min(s0 + u, NB - 1);
-                lo[u] = max(ridx[st * 129 + r], e_lo);
-                hi[u] = min(ridx[st * 129 + r + 1], e_hi);
-            }
-            uint32_t ev[GB];
-            int cb[GB];
-#pragma unroll
-            for (int u = 0; u < GB; u++) {
-                const bool ok = s0 + u < NB && lo[u] < hi[u] && lo[u] < staged_hi;
-                ev[u] = ok ? es[min(lo[u] - e_lo, kSkEStaged - 1)] : 0u;
-                cb[u] = ok ? (s0 + u) * kSkPlanBK : 0;
-                if (s0 + u < NB && hi[u] - lo[u] > (ok ? 1 : 0)) more |= 1u << (s0 + u);
-            }
-#pragma unroll
-            for (int u = 0; u < GB; u++) fma_entry(cb[u], ev[u]);
-            __builtin_amdgcn_sched_barrier(0);
+        fma_batch(lo, ecol, eval);
+        // the lanes of a row take the same branches and trip counts
+        if (lo + kSkEB < hi) fma_batch(lo + kSkEB, ecol2, eval2);
+        // more entries (dense rows, or a whole row without the chunk table)
+        for (int32_t j0 = lo + 2 * kSkEB; j0 < hi; j0 += kSkEB) {
+            int32_t c2[EL];
+            uint32_t v2[EL];
+            load_batch(j0, c2, v2);
+            fma_batch(j0, c2, v2);
         }
-        // Second pass: the remaining entries, bucket by bucket
-        while (more) {
-            const int st = __builtin_ctz(more);
-            more &= more - 1;
-            const int32_t lo = max(ridx[st * 129 + r], e_lo), hi = min(ridx[st * 129 + r + 1], e_hi);
-            const int32_t hs = min(hi, staged_hi);
-            for (int32_t i = lo + 1; i < hs; i++) fma_entry(st * kSkPlanBK, es[i - e_lo]);
-            // past the staged block (the first entry too, when it lay there)
-            for (int32_t i = max(lo, staged_hi); i < hi; i++) fma_entry(st * kSkPlanBK, pents[i]);
-        }
+        if (QUAD) {
 #pragma unroll
-        for (int i2 = 0; i2 < MQ; i2++) sp[r * MP + tg + 4 * i2] = sacc[i2];
+            for (int t = 0; t < TQ; t++) sp[sr * MP + tg + 4 * t] = sacc[t];
+        }
     }
-    __syncthreads();
+    if (SPARSE && QUAD) __syncthreads();  // the sums reach the MFMA lanes
 
     // ---- this slice's values: lane (row nl, tokens tt*16 + 4g + i)
     float val[NTT][4];
@@ -387,7 +345,7 @@ __global__ void __launch_bounds__(kSkNT) skinny_kernel(SkinnyArgs a) {
         for (int i = 0; i < 4; i++) {
             float v = acc[tt][i];
             if (!GROUPED) v = (v - bias_acc[tt][i]) * srow;
-            if (SPARSE) v += a.alpha * sp[(wave * 16 + nl) * MP + tt * 16 + 4 * g + i];
+            if (SPARSE) v += a.alpha * (QUAD ? sp[(wave * 16 + nl) * MP + tt * 16 + 4 * g + i] : sacc[tt * 4 + i]);
             val[tt][i] = v;
         }
     }
@@ -471,7 +429,7 @@ __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f
 
 struct SkinnyShape {
     int ntt, cps, S, nblocks, xstride;
-    int lds_cr, lds_xs, lds_sp, lds_e, lds_idx, lds_bytes;
+    int lds_cr, lds_xs, lds_sp, lds_bytes;
 };
 
 static bool skinny_shape(const ForwardArgs &a, int cus, SkinnyShape &sh) {
@@ -495,11 +453,7 @@ static bool skinny_shape(const ForwardArgs &a, int cus, SkinnyShape &sh) {
     sh.lds_xs = off;
     off += ((mp * sh.xstride * 2) + 15) & ~15;
     sh.lds_sp = off;
-    off += kSkRows * mp * 4;
-    sh.lds_e = off;
-    off += a.has_ortho ? kSkEStaged * 4 : 0;
-    sh.lds_idx = off;
-    off += a.has_ortho ? ((2 * cps_max * 129 * 4 + 15) & ~15) : 0;  // the kernel's 2 CPS buckets
+    off += a.has_ortho && ntt == 1 ? kSkRows * mp * 4 : 0;  // the kernel's QUAD exchange
     sh.lds_bytes = off;
     return off <= 150 * 1024;
 }
@@ -507,6 +461,7 @@ static bool skinny_shape(const ForwardArgs &a, int cus, SkinnyShape &sh) {
 bool skinny_supported(const ForwardArgs &a) {
     if (a.M < 1 || a.M > 64) return false;
     if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
+    if (a.has_ortho && a.val_dtype != ORTH_DT_F16) return false;  // values read from the CSR as FP16
     if (a.K % 128 != 0) return false;
     if (a.ngroups != 1) {
         if (a.G % 128 != 0) return false;
@@ -558,7 +513,8 @@ int64_t skinny_workspace_bytes(const ForwardArgs &a, int cus) {
     return sh.S > 1 ? (int64_t)sh.S * a.M * a.N * 4 : 0;
 }
 
-// plan: the ortho plan (required when has_ortho); part: the workspace.
+// plan: the ortho plan (optional: its chunk table locates the slice's CSR
+// ranges; without it rows are filtered by column); part: the workspace.
 hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float *part, hipStream_t stream) {
     SkinnyShape sh;
     if (!skinny_shape(a, cus, sh)) return hipErrorInvalidValue;
@@ -570,20 +526,14 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     d.gshift = 0;
     if (a.ngroups != 1)
         for (int64_t r = a.G / 128; r > 1; r >>= 1) d.gshift++;
-    const bool sparse = a.has_ortho && plan != nullptr;
-    if (a.has_ortho && !plan) return hipErrorInvalidValue;
-    d.nsteps = (int)(a.K / kSkPlanBK);
-    if (sparse) {
-        const int64_t nb = sh.nblocks;
-        d.phdr = static_cast<const uint32_t *>(plan);
-        d.poffs = reinterpret_cast<const int32_t *>(static_cast<const char *>(plan) + 64);
-        const int64_t ob = ((nb * (d.nsteps + 1) * 4) + 15) & ~int64_t(15);
-        d.pents = reinterpret_cast<const uint32_t *>(static_cast<const char *>(plan) + 64 + ob);
-    } else {
-        d.phdr = nullptr;
-        d.poffs = nullptr;
-        d.pents = nullptr;
-    }
+    const bool sparse = a.has_ortho;
+    d.row_ptr = a.row_ptr;
+    d.col = a.col;
+    d.vals = static_cast<const f16 *>(a.vals);
+    d.phdr = sparse && plan ? static_cast<const uint32_t *>(plan) : nullptr;
+    d.chunks = sparse && plan && plan_chunks_bytes(a.N, a.K)
+                   ? reinterpret_cast<const uint16_t *>(static_cast<const char *>(plan) + plan_chunks_at(a.N, a.K, a.nnz))
+                   : nullptr;
     d.nnz = (int32_t)a.nnz;
     d.x = static_cast<const f16 *>(a.x);
     d.y = static_cast<f16 *>(a.y);
@@ -598,8 +548,6 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     d.lds_cr = sh.lds_cr;
     d.lds_xs = sh.lds_xs;
     d.lds_sp = sh.lds_sp;
-    d.lds_e = sh.lds_e;
-    d.lds_idx = sh.lds_idx;
     d.alpha = a.alpha;
     d.part = part;
     // pairs of group-128 scales are read as aligned 32-bit words when every

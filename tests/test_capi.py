@@ -148,7 +148,11 @@ def test_plan_size(L):
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(nnz=0))) == 0
     n = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4096, N=4096, nnz=100)))
     offsets = ((4096 // 128) * (4096 // 64 + 1) * 4 + 15) // 16 * 16
-    assert n == 64 + offsets + 400
+    chunks = (4096 * (4096 // 128 + 1) * 2 + 15) // 16 * 16  # uint16 [N][K/128 + 1]
+    assert n == (64 + offsets + 400 + 15) // 16 * 16 + chunks
+    # K % 128 != 0: no chunk table
+    n64 = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4160, N=4096, nnz=100)))
+    assert n64 == 64 + ((4096 // 128) * (4160 // 64 + 1) * 4 + 15) // 16 * 16 + 400
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4000, nnz=5))) < 0  # K % 64 != 0
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4095))) == -_lib.ERR_INVALID_ARGUMENT
 

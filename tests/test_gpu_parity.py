@@ -216,6 +216,49 @@ def test_skinny_dense_ortho_past_the_staged_entries(oracle_mod, M):
     assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"skinny dense ortho M={M}")
 
 
+def test_skinny_foreign_plan_falls_back_to_the_csr(oracle_mod):
+    # a plan of another layer (larger, so the size check passes) does not
+    # match the header: each row's CSR range is filtered instead
+    big = W.make_layer(1024, 1024, 128, 0.02, seed=120)
+    lay = W.make_layer(1024, 512, 128, 0.02, seed=121)
+    db, d = W.to_device(big), W.to_device(lay)
+    plan = _C_ops.build_plan(db["q"], db["scales"], db["vals"], db["col"], db["row_ptr"], big.K)
+    for M in (8, 40):
+        x = W.make_x(M, lay.K, 122 + M)
+        xt = torch.from_numpy(x).cuda()
+        y = torch.full((M, lay.N), float("nan"), dtype=torch.float16, device="cuda")
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], xt, y, 1.0, plan)
+        assert _C_ops.last_kernel() == "skinny"
+        torch.cuda.synchronize()
+        assert_close(y.float().cpu().numpy(), oracle_y(oracle_mod, lay, x, 1.0), what=f"foreign plan M={M}")
+
+
+def test_skinny_chunk_table_with_columns_outside_k(oracle_mod):
+    # ascending rows that start below 0 and end past K: the chunk table still
+    # locates each slice's range (the outside columns are skipped)
+    rng = np.random.default_rng(7)
+    K, N = 2048, 384
+    L = W.make_layer(K, N, 128, 0.0, seed=123)
+    rows = []
+    for r in range(N):
+        c = np.sort(rng.choice(K, size=int(rng.integers(0, 40)), replace=False)).astype(np.int32)
+        if r % 3 == 0:
+            c = np.concatenate([[-7, -1], c])
+        if r % 5 == 0:
+            c = np.concatenate([c, [K, K + 9]])
+        rows.append(c.astype(np.int32))
+    rp = np.zeros(N + 1, np.int32)
+    rp[1:] = np.cumsum([len(c) for c in rows])
+    col = np.concatenate(rows).astype(np.int32)
+    vals = rng.normal(0, 0.05, len(col)).astype(np.float16)
+    lay = W.Layer(K, N, L.q, L.scales, rp, col, vals)
+    for M in (6, 33):
+        x = W.make_x(M, K, 124 + M)
+        y, k = run(lay, x, 1.0, plan=True)
+        assert k == "skinny"
+        assert_close(y, oracle_y(oracle_mod, lay, x, 1.0), what=f"outside columns M={M}")
+
+
 def test_skinny_workspace_reuse_and_determinism(oracle_mod, c2):
     # the split-K counters reset themselves; the workspace grows with M
     outs = {}
@@ -245,7 +288,7 @@ def test_ragged_shapes(oracle_mod, M):
 @pytest.mark.parametrize("K,G,M,expect", [
     (64, None, 4, "general"), (64, None, 40, "prefill"), (200, 40, 3, "general"),
     (200, 40, 50, "general"), (512, 64, 2, "general"), (512, 64, 64, "prefill"),
-    (12800, 128, 20, "general"),
+    (12800, 128, 20, "skinny"),   # past the plan's K limit: rows filtered by column
 ])
 def test_shapes_outside_the_fast_paths(oracle_mod, K, G, M, expect):
     L = W.make_layer(K, 96, G, 0.03, seed=K + M)
