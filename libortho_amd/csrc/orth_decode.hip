@@ -34,6 +34,13 @@
 //    with DPP moves, and lane 0 of the row adds alpha*sum after the base term
 //    and stores, as /root/reference/src/dual_gemm.cu:212-221 does.  alpha <=
 //    0 takes a kernel without the term, which never touches the CSR arrays.
+//  * With an ortho plan (up to 4 tokens), the block's entries come from the
+//    plan's record of the block instead: packed column|value words at an
+//    address that needs no row pointer, loaded right after the activations
+//    and summed before the main loop, while the weights are in flight.
+//    Rows reaching past the record read the rest from the CSR at the end.
+#include <type_traits>
+
 #include "orth_common.h"
 
 namespace orth {
@@ -68,7 +75,15 @@ struct DecodeArgs {
     int lds_e;
     float alpha;
     int has_ortho;
+    const uint32_t *phdr;  // plan header (record kernels), checked before the record is used
+    const uint32_t *rec;   // plan records, dcap words per 16-row block
+    int dcap;              // record entries per block (a multiple of 16), 0 without a plan
 };
+
+// plan header words the record kernels check (the plan's layout is defined
+// with its builder in orth_prefill.hip)
+constexpr uint32_t kDecPlanMagic = 0x504f5254u;
+constexpr uint32_t kDecPlanVersion = 3;
 
 // Weights pass through LDS (whole-line loads, transposed on the way) for
 // one or two tokens with staged activations: there the weight stream is all
@@ -81,7 +96,9 @@ constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 // CPW: compile-time bound of the chunks per wave (all issued at entry).
 // SPARSE: 0 no ortho term; 1 ortho term with the workgroup's CSR block
 // staged through LDS (16-byte aligned columns, nnz >= 4); 2 ortho term read
-// entry by entry in the epilogue.
+// entry by entry in the epilogue; 3 / 4 / 5 the plan's record of the block
+// (at most 1024 / 2048 / 4096 entries) staged through LDS and summed before
+// the main loop (XLDS only).
 //
 // Every global load below is unconditional with a clamped, always valid
 // address: a load under a branch makes the compiler's wait-count insertion
@@ -95,11 +112,13 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     constexpr int MI = MT < 4 ? MT : 4;        // live D rows per lane group (tokens 4g + i)
     constexpr bool GROUPED = GMODE != 0;
     constexpr int XIT = (CPW * 16 + 63) / 64;  // 16-byte activation pieces per lane per token
-    constexpr int SW = (CPW + 7) / 8;          // group-128 scale words per lane
     constexpr int ES = kDecodeESlots;
     // WT: the weights pass through LDS (see decode_wt)
     constexpr bool WT = decode_wt(MT, XLDS);
     constexpr int WREG = CPW * 1024;  // WT: LDS bytes of a wave's weight region
+    constexpr bool REC = SPARSE >= 3;
+    constexpr int ER = SPARSE == 5 ? 4 : (SPARSE == 4 ? 2 : 1);  // record: 16-byte loads per thread
+    static_assert(!REC || XLDS, "the record kernels gather staged activations");
 
     extern __shared__ __align__(16) unsigned char smem[];
     // WT: wave w's region holds its weights during the main loop, then its
@@ -150,6 +169,18 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         }
     }
 
+    // ---- the block's plan record (no row pointer needed: issued before the
+    //      weights, it returns with the activations) and the plan header
+    u32x4 rv[ER];
+    int32_t hw = 0;
+    if (REC) {
+        const uint32_t *rb = a.rec + (int64_t)blockIdx.x * a.dcap;
+#pragma unroll
+        for (int r = 0; r < ER; r++)
+            rv[r] = *reinterpret_cast<const u32x4 *>(rb + min(4 * (tid + NT * r), a.dcap - 4));
+        hw = (int32_t)a.phdr[min(lane, 13)];
+    }
+
     // ---- CSR bounds: this thread's epilogue row, and the workgroup block
     //      (loaded here, used after the staging).  The block bounds come
     //      from one vector load (lane i: row_ptr[n0 + i]) read with
@@ -167,15 +198,15 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     f16 srow = (f16)0.0f;
     if (!GROUPED) srow = a.scales[n0 + min(SPARSE ? tid >> 4 : tid & 15, last_row)];
 
-    // ---- group scales: lane (row nl, g) holds chunks 8i + 2g, 8i + 2g + 1
-    //      (GMODE 1), or one scale per chunk (GMODE 2)
+    // ---- group scales of this lane's row nl: chunks c_lo + 2i, + 2i + 1 as
+    //      one 32-bit pair (GMODE 1), or one scale per chunk (GMODE 2)
     const f16 *sbase = a.scales + (n0 + my_row) * (int64_t)a.ngroups;
-    uint32_t sw[SW];
+    uint32_t sw[GMODE == 1 ? CPW / 2 : 1];
     f16 sh[GMODE == 2 ? CPW : 1];
     if (GMODE == 1) {
 #pragma unroll
-        for (int i = 0; i < SW; i++)
-            sw[i] = *reinterpret_cast<const uint32_t *>(sbase + (min(c_lo + 8 * i + 2 * g, clast) & ~1));
+        for (int i = 0; i < CPW / 2; i++)
+            sw[i] = *reinterpret_cast<const uint32_t *>(sbase + (min(c_lo + 2 * i, clast) & ~1));
     } else if (GMODE == 2) {
 #pragma unroll
         for (int p = 0; p < CPW; p++) sh[p] = sbase[min(c_lo + p, clast) >> a.gshift];
@@ -230,6 +261,11 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     // ---- stage this wave's activations (interleaved k order) and their
     //      per-chunk bias sums; only this wave reads them before the end
     const int wpieces = nci * 16;
+    // SGB: the bias sums of token i < MI and chunk p are the same in every
+    // lane (tokens (4 g + i) & (MT - 1) = i): read from the staging registers
+    // into scalar registers instead of LDS
+    constexpr bool SGB = XLDS && MT <= 4 && MT * CPW <= 32;
+    float bsum[SGB ? MT : 1][SGB ? XIT : 1];
     if (XLDS) {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
@@ -244,6 +280,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                     const float e = ((float)h[0] + (float)h[2]) + ((float)h[4] + (float)h[6]);
                     const float o = ((float)h[1] + (float)h[3]) + ((float)h[5] + (float)h[7]);
                     const float b = group_sum<16>(1032.0f * e + 72.0f * o);  // 16 pieces of a chunk
+                    if (SGB) bsum[m][it] = b;
                     if (pc < wpieces) {
                         *reinterpret_cast<u32x4 *>(xs + (m * a.xstride + c_lo * 128 + pc * 8)) = permute_x8(v);
                         if ((pc & 15) == 0) cr[m * a.nchunks + c_lo + (pc >> 4)] = b;
@@ -268,6 +305,49 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         e0 = min(max(__builtin_amdgcn_readlane(pv, 0), 0), a.nnz);
         e1 = min(max(__builtin_amdgcn_readlane(pv, last_row + 1), e0), a.nnz);
     }
+    // ---- REC: stage the record, then the sparse sums of this thread's row
+    //      (16 lanes per row, entries rs + sub + 16 u in order) while the
+    //      weights stream in; a row's entries past the record wait for the end.
+    //      Every path adds entry j as fma(v_j, x_j, sum) in j order (masked
+    //      slots as fma(0, 0, sum)), so planned and unplanned calls agree bit
+    //      for bit.
+    float sacc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; m++) sacc[m] = 0.f;
+    int32_t rec_hi = 0;
+    if (REC) {
+        uint32_t *er = reinterpret_cast<uint32_t *>(smem + a.lds_e);
+#pragma unroll
+        for (int r = 0; r < ER; r++) {
+            const int slot = 4 * (tid + NT * r);
+            if (slot < a.dcap) *reinterpret_cast<u32x4 *>(er + slot) = rv[r];
+        }
+        __syncthreads();  // all activations and the record are in LDS
+        auto word = [&](int l) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane(hw, l); };
+        const bool ok = (word(0) == kDecPlanMagic) & (word(1) == kDecPlanVersion) &
+                        (word(6) == (uint32_t)a.N) & (word(7) == (uint32_t)(a.N >> 32)) &
+                        (word(8) == (uint32_t)K) & (word(9) == 0u) & (word(10) == (uint32_t)a.nnz) &
+                        (word(11) == 0u) & (word(13) == (uint32_t)a.dcap);
+        rec_hi = (ok && rs >= e0) ? min(re, e0 + a.dcap) : rs;
+        constexpr int U = 4;
+        for (int32_t j0 = rs + sub; j0 < rec_hi; j0 += 16 * U) {
+            uint32_t w[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) w[u] = er[min(j0 + 16 * u, rec_hi - 1) - e0];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = (int)(w[u] & 0xffffu);
+                const bool ok_e = (j0 + 16 * u < rec_hi) & (c < K);
+                const int cc = ok_e ? c : 0;
+                const float vv = ok_e ? (float)__builtin_bit_cast(f16, (uint16_t)(w[u] >> 16)) : 0.f;
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    const float xv = (float)xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))];
+                    sacc[m] = __builtin_fmaf(vv, ok_e ? xv : 0.f, sacc[m]);
+                }
+            }
+        }
+    }
     const int32_t eb = e0 & ~3;
     const int32_t last4 = (a.nnz - 4) & ~3;
     const int32_t wlast4 = min(max((e1 - 1) & ~3, eb), last4);
@@ -286,7 +366,9 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         }
     }
 
-    // ---- main loop over this wave's chunks
+    // ---- main loop over this wave's chunks: straight-line code when the
+    //      wave has all CPW chunks (FULL), so that the reads and conversions
+    //      of later chunks overlap the matrix ops of earlier ones
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
     float bias_acc[MI];
 #pragma unroll
@@ -295,66 +377,129 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     const float *cr_lane[MI];
 #pragma unroll
     for (int i = 0; i < MI; i++) cr_lane[i] = cr + ((4 * g + i) & (MT - 1)) * a.nchunks + c_lo;
+    // bias sum of token i, chunk p of this wave
+    auto bias_of = [&](int i, int p) -> float {
+        if constexpr (SGB)
+            return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bsum[i][p >> 2]), 16 * (p & 3)));
+        else
+            return cr_lane[i][p];
+    };
     // WT: this wave's weight region as 16-byte slots
     u32x4 *wl = reinterpret_cast<u32x4 *>(smem + wave * WREG);
+    // one chunk: weights wp (4 words), activations of chunk p; FP32 partial
+    auto chunk_mfma = [&](const u32x4 &wp, int p, f32x4 part) -> f32x4 {
+        const uint32_t words[4] = {wp.x, wp.y, wp.z, wp.w};
 #pragma unroll
-    for (int p = 0; p < CPW; p++) {
-        if (p < nci) {  // uniform
-            u32x4 wp;
-            if (WT) {
-                const int j = p >> 1;
-                if ((p & 1) == 0) {  // pair j to LDS, as loaded
-                    wl[(2 * j) * 64 + lane] = wq[j][0];
-                    wl[(2 * j + 1) * 64 + lane] = wq[j][1];
-                    __builtin_amdgcn_wave_barrier();  // (same wave: LDS keeps the order)
-                }
-                // lane (row nl, g) reads logical slot 4 (p & 1) + g of row nl
-                const int phys = (4 * (p & 1) + g) ^ ((nl >> 1) & 7);
-                wp = wl[(2 * j + (nl >> 3)) * 64 + (nl & 7) * 8 + phys];
+        for (int j = 0; j < 4; j++) {
+            uint32_t b[4];
+            u32x4 av;
+            if (XLDS) {
+                int4x8_to_f16_biased(words[j], b);
+                av = *reinterpret_cast<const u32x4 *>(xs_lane + (p * 128 + 8 * j));
             } else {
-                wp = wv[p];
+                int4x8_to_f16_interleaved(words[j], b);
+                av = permute_x8(ag[p][j]);
             }
-            const uint32_t words[4] = {wp.x, wp.y, wp.z, wp.w};
-            f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+            part = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
+                                                          __builtin_bit_cast(f16x8, u32x4{b[0], b[1], b[2], b[3]}),
+                                                          part, 0, 0, 0);
+        }
+        return part;
+    };
+    // chunk p's partial into acc: scaled (GROUPED) after its bias sum is removed
+    auto chunk_done = [&](const f32x4 &part, int p) {
+        float s;
+        if (GMODE == 1)
+            s = (float)__builtin_bit_cast(f16, (uint16_t)((p & 1) ? (sw[p >> 1] >> 16) : (sw[p >> 1] & 0xffffu)));
+        else
+            s = (float)sh[p];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                uint32_t b[4];
-                u32x4 av;
-                if (XLDS) {
-                    int4x8_to_f16_biased(words[j], b);
-                    av = *reinterpret_cast<const u32x4 *>(xs_lane + (p * 128 + 8 * j));
+        for (int i = 0; i < MI; i++) {
+            float v = part[i];
+            if (XLDS) v -= bias_of(i, p);
+            acc[i] += s * v;
+        }
+    };
+    // WT: pair j (chunks 2j, 2j + 1) to LDS as loaded, then lane (row nl, g)
+    // reads logical slot 4 h + g of row nl for chunk 2j + h
+    auto pair_to_lds = [&](int j) {
+        wl[(2 * j) * 64 + lane] = wq[j][0];
+        wl[(2 * j + 1) * 64 + lane] = wq[j][1];
+        __builtin_amdgcn_wave_barrier();  // (same wave: LDS keeps the order)
+    };
+    auto wt_read = [&](int j, int h) -> u32x4 {
+        const int phys = (4 * h + g) ^ ((nl >> 1) & 7);
+        return wl[(2 * j + (nl >> 3)) * 64 + (nl & 7) * 8 + phys];
+    };
+    auto main_loop = [&](auto full) {
+        constexpr bool FULL = decltype(full)::value;
+        if constexpr (FULL && GROUPED && CPW % 2 == 0) {
+            // chunks in pairs, the two MFMA chains interleaved
+#pragma unroll
+            for (int j = 0; j < CPW / 2; j++) {
+                u32x4 w0, w1;
+                if (WT) {
+                    pair_to_lds(j);
+                    w0 = wt_read(j, 0);
+                    w1 = wt_read(j, 1);
                 } else {
-                    int4x8_to_f16_interleaved(words[j], b);
-                    av = permute_x8(ag[p][j]);
+                    w0 = wv[2 * j];
+                    w1 = wv[2 * j + 1];
                 }
-                const f16x8 afr = __builtin_bit_cast(f16x8, av);
-                const f16x8 bfr = __builtin_bit_cast(f16x8, u32x4{b[0], b[1], b[2], b[3]});
-                if (GROUPED)
-                    part = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr, bfr, part, 0, 0, 0);
-                else
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr, bfr, acc, 0, 0, 0);
+                const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w};
+                const uint32_t u1[4] = {w1.x, w1.y, w1.z, w1.w};
+                f32x4 pa = f32x4{0.f, 0.f, 0.f, 0.f}, pb = pa;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    uint32_t b0[4], b1[4];
+                    u32x4 a0, a1;
+                    if (XLDS) {
+                        int4x8_to_f16_biased(u0[k], b0);
+                        int4x8_to_f16_biased(u1[k], b1);
+                        a0 = *reinterpret_cast<const u32x4 *>(xs_lane + ((2 * j) * 128 + 8 * k));
+                        a1 = *reinterpret_cast<const u32x4 *>(xs_lane + ((2 * j + 1) * 128 + 8 * k));
+                    } else {
+                        int4x8_to_f16_interleaved(u0[k], b0);
+                        int4x8_to_f16_interleaved(u1[k], b1);
+                        a0 = permute_x8(ag[2 * j][k]);
+                        a1 = permute_x8(ag[2 * j + 1][k]);
+                    }
+                    pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0),
+                                                                __builtin_bit_cast(f16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
+                                                                pa, 0, 0, 0);
+                    pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a1),
+                                                                __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
+                                                                pb, 0, 0, 0);
+                }
+                chunk_done(pa, 2 * j);
+                chunk_done(pb, 2 * j + 1);
             }
-            if (GROUPED) {
-                float s;
-                if (GMODE == 1) {
-                    // scales of chunks 8i + 2g', +1 sit in lane 16g' + nl
-                    const uint32_t w2 = (uint32_t)__shfl((int)sw[p >> 3], 16 * ((p & 7) >> 1) + nl, 64);
-                    s = (float)__builtin_bit_cast(f16, (uint16_t)((p & 1) ? (w2 >> 16) : (w2 & 0xffffu)));
-                } else {
-                    s = (float)sh[p];
-                }
+        } else {
 #pragma unroll
-                for (int i = 0; i < MI; i++) {
-                    float v = part[i];
-                    if (XLDS) v -= cr_lane[i][p];
-                    acc[i] += s * v;
-                }
-            } else if (XLDS) {
+            for (int p = 0; p < CPW; p++) {
+                if (FULL || p < nci) {  // uniform
+                    u32x4 wp;
+                    if (WT) {
+                        if ((p & 1) == 0) pair_to_lds(p >> 1);
+                        wp = wt_read(p >> 1, p & 1);
+                    } else {
+                        wp = wv[p];
+                    }
+                    if (GROUPED) {
+                        chunk_done(chunk_mfma(wp, p, f32x4{0.f, 0.f, 0.f, 0.f}), p);
+                    } else {
+                        acc = chunk_mfma(wp, p, acc);
+                        if (XLDS) {
 #pragma unroll
-                for (int i = 0; i < MI; i++) bias_acc[i] += cr_lane[i][p];
+                            for (int i = 0; i < MI; i++) bias_acc[i] += bias_of(i, p);
+                        }
+                    }
+                }
             }
         }
-    }
+    };
+    if (nci == CPW) main_loop(std::true_type{});
+    else main_loop(std::false_type{});
     if (!GROUPED && XLDS) {
 #pragma unroll
         for (int i = 0; i < MI; i++) acc[i] -= bias_acc[i];
@@ -381,11 +526,8 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     if (SPARSE) {
         constexpr int U = 4;
         const int32_t staged_hi = SPARSE == 1 ? min(min(eb + kDecodeEStaged, last4 + 4), e1) : eb;
-        const int32_t fast_hi = min(re, staged_hi);
-        float sacc[MT];
-#pragma unroll
-        for (int m = 0; m < MT; m++) sacc[m] = 0.f;
-        for (int32_t j0 = rs + sub; j0 < fast_hi; j0 += 16 * U) {
+        const int32_t fast_hi = REC ? rec_hi : min(re, staged_hi);
+        for (int32_t j0 = rs + sub; !REC && j0 < fast_hi; j0 += 16 * U) {
             int32_t c[U];
             float v[U];
 #pragma unroll
@@ -393,11 +535,12 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 const int32_t j = j0 + 16 * u;
                 const int32_t li = min(j, fast_hi - 1) - eb;  // in [0, kDecodeEStaged)
                 c[u] = *ec_at(li);
-                v[u] = (j < fast_hi) ? (float)*ev_at(li) : 0.f;
+                v[u] = (float)*ev_at(li);
             }
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const bool ok = c[u] >= 0 && c[u] < K;
+                // entries past the row, or with a column outside [0, K), add nothing
+                const bool ok = (j0 + 16 * u < fast_hi) & (c[u] >= 0) & (c[u] < K);
                 const int cc = ok ? c[u] : 0;
                 const float vv = ok ? v[u] : 0.f;
 #pragma unroll
@@ -405,7 +548,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                     float xv;
                     if (XLDS) xv = (float)xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))];
                     else xv = (float)a.x[(int64_t)min(m, a.M - 1) * K + cc];
-                    sacc[m] += vv * xv;
+                    sacc[m] = __builtin_fmaf(vv, ok ? xv : 0.f, sacc[m]);
                 }
             }
         }
@@ -420,7 +563,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                     float xv;
                     if (XLDS) xv = (float)xs[m * a.xstride + ((c & ~7) | interleaved_pos(c & 7))];
                     else xv = (float)a.x[(int64_t)min(m, a.M - 1) * K + c];
-                    sacc[m] += v * xv;
+                    sacc[m] = __builtin_fmaf(v, xv, sacc[m]);
                 }
             }
         }
@@ -462,9 +605,10 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 static const int64_t kDecodeLdsMax = 160 * 1024;
 
 // LDS layout of decode_kernel<MT, *, XLDS, CPW, *>: weight regions (WT) or
-// split-K partials, bias sums, activations, staged CSR block
-// (outside the weight regions when not WT).  Returns the bytes.
-static int64_t decode_lds_layout(DecodeArgs &d, int mt, bool xlds, int cpw_bound) {
+// split-K partials, bias sums, activations, staged CSR block (outside the
+// weight regions when not WT) or plan record (rec_words > 0).  Returns the
+// bytes.
+static int64_t decode_lds_layout(DecodeArgs &d, int mt, bool xlds, int cpw_bound, int rec_words) {
     auto al = [](int64_t v) { return (v + 15) & ~int64_t(15); };
     const bool wt = decode_wt(mt, xlds);
     int64_t off = wt ? (int64_t)kDecodeW * cpw_bound * 1024 : (int64_t)kDecodeW * 1024;
@@ -474,7 +618,8 @@ static int64_t decode_lds_layout(DecodeArgs &d, int mt, bool xlds, int cpw_bound
     d.lds_xs = (int)off;
     if (xlds) off = al(off + (int64_t)mt * d.xstride * 2);
     d.lds_e = (int)off;
-    if (!wt && d.has_ortho && d.csr_vec) off += (int64_t)kDecodeEStaged * (4 + 2);
+    if (rec_words > 0) off += (int64_t)rec_words * 4;
+    else if (!wt && d.has_ortho && d.csr_vec) off += (int64_t)kDecodeEStaged * (4 + 2);
     return off;
 }
 
@@ -498,7 +643,18 @@ static hipError_t launch_decode_k(const DecodeArgs &d, int64_t lds, hipStream_t 
 template <int MT, int GMODE, bool XLDS, int CPW>
 static hipError_t launch_decode_t(const DecodeArgs &d0, hipStream_t stream) {
     DecodeArgs d = d0;
-    const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW);
+    if constexpr (XLDS && MT <= 4) {
+        // plan records when the LDS takes them (else the CSR block below)
+        if (d.has_ortho && d.dcap > 0 && d.dcap <= 4096) {
+            const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW, d.dcap);
+            if (lds <= kDecodeLdsMax) {
+                if (d.dcap <= 1024) return launch_decode_k<MT, GMODE, XLDS, CPW, 3>(d, lds, stream);
+                if (d.dcap <= 2048) return launch_decode_k<MT, GMODE, XLDS, CPW, 4>(d, lds, stream);
+                return launch_decode_k<MT, GMODE, XLDS, CPW, 5>(d, lds, stream);
+            }
+        }
+    }
+    const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW, 0);
     if (lds > kDecodeLdsMax) return hipErrorInvalidValue;
     if (d.has_ortho && d.csr_vec) return launch_decode_k<MT, GMODE, XLDS, CPW, 1>(d, lds, stream);
     if (d.has_ortho) return launch_decode_k<MT, GMODE, XLDS, CPW, 2>(d, lds, stream);
@@ -560,7 +716,11 @@ bool decode_supported(const ForwardArgs &a) {
     return true;
 }
 
-hipError_t launch_decode(const ForwardArgs &a, hipStream_t stream) {
+int64_t plan_rec_cap(int64_t N, int64_t nnz);           // orth_prefill.hip
+int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz);
+
+// plan: an ortho plan of at least plan_bytes_for(N, K, nnz) bytes, or null.
+hipError_t launch_decode(const ForwardArgs &a, const void *plan, hipStream_t stream) {
     DecodeArgs d;
     d.q = a.q;
     d.scales = static_cast<const f16 *>(a.scales);
@@ -581,6 +741,11 @@ hipError_t launch_decode(const ForwardArgs &a, hipStream_t stream) {
     d.xstride = (int)(a.K + 8);  // +16 bytes: rows start in different LDS banks
     d.alpha = a.alpha;
     d.has_ortho = a.has_ortho;
+    const bool rec = plan && a.has_ortho;
+    d.phdr = rec ? static_cast<const uint32_t *>(plan) : nullptr;
+    d.rec = rec ? reinterpret_cast<const uint32_t *>(static_cast<const char *>(plan) + plan_rec_at(a.N, a.K, a.nnz))
+                : nullptr;
+    d.dcap = rec ? (int)plan_rec_cap(a.N, a.nnz) : 0;
 
     int mt = 1;
     while (mt < a.M) mt <<= 1;

@@ -34,12 +34,20 @@ namespace orth {
 //   uint32 entries[nnz]                   (row_in_block << 24) | (col_in_step << 16) | fp16 bits
 //   uint16 chunks[N][K/128 + 1]           (K % 128 == 0 only) per row, the number of
 //                                         its CSR entries with column < 128 c
+//   uint32 records[ceil(N/16)][dcap]      per 16-row block b, the CSR positions
+//                                         [e0, e0 + dcap), e0 = row_ptr[16 b] clamped
+//                                         to [0, nnz]: column (0xffff when outside
+//                                         [0, K)) | fp16 value bits << 16; 0xffff
+//                                         past nnz.  dcap is in the header's pad[0].
 // Entries of one (block, step) are ordered by row then by CSR position.  The
 // chunk table locates a row's entries of columns [128 c0, 128 c1) in the CSR
 // itself when the row's columns ascend strictly (flag kPlanUnsorted clear).
+// The records give the decode kernel each 16-row block's entries at an
+// address known before any load returns (a CSR block's start is itself a
+// load); rows reaching past their block's record read the rest from the CSR.
 
 static const uint32_t kPlanMagic = 0x504f5254u;  // "TROP"
-static const uint32_t kPlanVersion = 2;
+static const uint32_t kPlanVersion = 3;
 static const int kPlanBN = 128;
 static const int kPlanBK = 64;
 static const uint32_t kPlanNonCanonical = 1u;  // duplicate or unsorted columns in a row
@@ -71,9 +79,27 @@ int64_t plan_chunks_bytes(int64_t N, int64_t K) {
     return K % 128 == 0 ? ((N * (K / 128 + 1) * 2) + 15) & ~int64_t(15) : 0;
 }
 
+// Entries per decode record: the mean count of a 16-row block plus four
+// times its square root (a binomial block count's standard deviation), in
+// whole 16-entry groups, at most kPlanRecMax.
+static const int64_t kPlanRecMax = 4096;
+
+int64_t plan_rec_cap(int64_t N, int64_t nnz) {
+    if (nnz <= 0 || N <= 0) return 0;
+    const int64_t mean = (16 * nnz + N - 1) / N;
+    int64_t s = 0;
+    while ((s + 1) * (s + 1) <= mean) s++;
+    const int64_t cap = (mean + 4 * (s + 1) + 15) & ~int64_t(15);
+    return cap < kPlanRecMax ? cap : kPlanRecMax;
+}
+
+int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz) {
+    return plan_chunks_at(N, K, nnz) + plan_chunks_bytes(N, K);
+}
+
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) {
     if (nnz <= 0) return 0;
-    return plan_chunks_at(N, K, nnz) + plan_chunks_bytes(N, K);
+    return plan_rec_at(N, K, nnz) + ((N + 15) / 16) * plan_rec_cap(N, nnz) * 4;
 }
 
 // Largest K the plan builder's LDS counters take (int32 per (step, row)).
@@ -84,7 +110,7 @@ bool plan_supported(const ForwardArgs &a) {
 }
 
 __global__ void plan_init_kernel(PlanHeader *h, int nblocks, int nksteps, int64_t N, int64_t K,
-                                 int64_t nnz) {
+                                 int64_t nnz, int dcap) {
     if (threadIdx.x == 0) {
         h->magic = kPlanMagic;
         h->version = kPlanVersion;
@@ -96,7 +122,8 @@ __global__ void plan_init_kernel(PlanHeader *h, int nblocks, int nksteps, int64_
         h->k = K;
         h->nnz = nnz;
         h->flags = 0;
-        for (int i = 0; i < 3; i++) h->pad[i] = 0;
+        h->pad[0] = (uint32_t)dcap;
+        h->pad[1] = h->pad[2] = 0;
     }
 }
 
@@ -211,6 +238,23 @@ __global__ void __launch_bounds__(256) plan_build_kernel(ForwardArgs a, PlanHead
     }
 }
 
+// One workgroup per 16-row block: its record, slot s = CSR position e0 + s.
+__global__ void __launch_bounds__(256) plan_rec_kernel(ForwardArgs a, uint32_t *rec, int dcap) {
+    const int64_t b = blockIdx.x;
+    int64_t e0 = a.row_ptr[b * 16];
+    e0 = e0 < 0 ? 0 : (e0 > a.nnz ? a.nnz : e0);
+    uint32_t *r = rec + b * dcap;
+    for (int s = threadIdx.x; s < dcap; s += 256) {
+        const int64_t j = e0 + s;
+        uint32_t w = 0xffffu;
+        if (j < a.nnz) {
+            const int32_t c = a.col[j];
+            w = ((c >= 0 && c < a.K) ? (uint32_t)c : 0xffffu) | (value_bits_f16(a.vals, a.val_dtype, j) << 16);
+        }
+        r[s] = w;
+    }
+}
+
 hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t stream) {
     const int nblocks = (int)((a.N + kPlanBN - 1) / kPlanBN);
     const int nksteps = (int)(a.K / kPlanBK);
@@ -218,14 +262,17 @@ hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t strea
     int32_t *offsets = reinterpret_cast<int32_t *>(static_cast<char *>(plan) + sizeof(PlanHeader));
     uint32_t *entries = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(offsets) +
                                                      plan_offsets_bytes(a.N, a.K));
+    const int dcap = (int)plan_rec_cap(a.N, a.nnz);
     hipLaunchKernelGGL(plan_init_kernel, dim3(1), dim3(64), 0, stream, h, nblocks, nksteps, a.N,
-                       a.K, a.nnz);
+                       a.K, a.nnz, dcap);
     const size_t lds = ((size_t)nksteps * kPlanBN + 256) * sizeof(int32_t);
     uint16_t *chunks = plan_chunks_bytes(a.N, a.K)
                            ? reinterpret_cast<uint16_t *>(static_cast<char *>(plan) + plan_chunks_at(a.N, a.K, a.nnz))
                            : nullptr;
     hipLaunchKernelGGL(plan_build_kernel, dim3(nblocks), dim3(256), lds, stream, a, h, offsets,
                        entries, chunks, nksteps);
+    uint32_t *rec = reinterpret_cast<uint32_t *>(static_cast<char *>(plan) + plan_rec_at(a.N, a.K, a.nnz));
+    hipLaunchKernelGGL(plan_rec_kernel, dim3((unsigned)((a.N + 15) / 16)), dim3(256), 0, stream, a, rec, dcap);
     return hipGetLastError();
 }
 

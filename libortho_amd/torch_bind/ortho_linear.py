@@ -23,10 +23,10 @@ Differences, all deliberate:
   * ``forward`` on a CPU tensor raises instead of returning uninitialised
     memory (the reference's CPU branch is ``pass``, :152-162); there is no
     CPU path in this library.
-  * The ortho plan read by the mid-batch and prefill kernels (a derived
-    layout of the CSR buffers) is built on first use and cached; it is rebuilt whenever one of the three
-    CSR buffers is replaced or modified in place.  It is not a buffer and is
-    not saved in the state_dict.
+  * The ortho plan read by the kernels (a derived layout of the CSR
+    buffers) is built on the first call with alpha > 0 and cached; it is
+    rebuilt whenever one of the three CSR buffers is replaced or modified in
+    place.  It is not a buffer and is not saved in the state_dict.
 """
 from __future__ import annotations
 
@@ -39,10 +39,6 @@ from .. import _C_ops as _C
 from ..tools.sieve import pack_ortho_sparse
 
 HAS_C_OPS = True  # the reference's flag (:15-28); this package has no fallback
-
-# Below this many tokens the decode kernel serves the call and needs no plan;
-# from here on the mid-batch and prefill kernels read the ortho plan.
-_PLAN_MIN_TOKENS = 5
 
 
 class OrthoLinear(nn.Module):
@@ -151,7 +147,7 @@ class OrthoLinear(nn.Module):
             raise RuntimeError("OrthoLinear runs on a ROCm GPU only; move the module and the input "
                                "to a cuda device (the reference's CPU branch returns uninitialised memory)")
         plan = None
-        if self.alpha > 0 and batch_size >= _PLAN_MIN_TOKENS:
+        if self.alpha > 0:
             plan = self._ortho_plan()
         _C.forward_planned(self.base_weight, self.base_scales, self.ortho_values,
                            self.ortho_col_indices, self.ortho_row_ptr, x_flat.contiguous(), output,

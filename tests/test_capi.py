@@ -3,6 +3,7 @@ include/orth_hip.h declares, its structs match the header byte for byte,
 and host-side validation returns the documented status codes (no device
 access is needed for any of these)."""
 import ctypes
+import math
 import os
 import re
 import subprocess
@@ -144,15 +145,28 @@ def test_forward_without_gpu_reports_no_device(L):
         _lib.device_info(0)
 
 
+def rec_cap(N, nnz):
+    # decode records: mean entries of a 16-row block + 4 (isqrt(mean) + 1),
+    # in 16-entry groups, at most 4096
+    mean = -(-16 * nnz // N)
+    return min(4096, (mean + 4 * (math.isqrt(mean) + 1) + 15) // 16 * 16)
+
+
 def test_plan_size(L):
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(nnz=0))) == 0
     n = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4096, N=4096, nnz=100)))
     offsets = ((4096 // 128) * (4096 // 64 + 1) * 4 + 15) // 16 * 16
     chunks = (4096 * (4096 // 128 + 1) * 2 + 15) // 16 * 16  # uint16 [N][K/128 + 1]
-    assert n == (64 + offsets + 400 + 15) // 16 * 16 + chunks
-    # K % 128 != 0: no chunk table
-    n64 = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4160, N=4096, nnz=100)))
-    assert n64 == 64 + ((4096 // 128) * (4160 // 64 + 1) * 4 + 15) // 16 * 16 + 400
+    records = (4096 // 16) * rec_cap(4096, 100) * 4          # uint32 [N/16][dcap]
+    assert rec_cap(4096, 100) == 16
+    assert n == (64 + offsets + 400 + 15) // 16 * 16 + chunks + records
+    # K % 128 != 0: no chunk table; a ragged last row block still has a record
+    n64 = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4160, N=4100, nnz=100)))
+    assert n64 == (64 + ((4100 + 127) // 128) * (4160 // 64 + 1) * 4 + 400 + 15) // 16 * 16 + \
+        ((4100 + 15) // 16) * rec_cap(4100, 100) * 4
+    # c2 (1 % of 4096 x 11008): 656 entries per block on average -> 768
+    assert rec_cap(11008, 450888) == 768
+    assert rec_cap(64, 64 * 4096) == 4096  # capped
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4000, nnz=5))) < 0  # K % 64 != 0
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4095))) == -_lib.ERR_INVALID_ARGUMENT
 

@@ -143,6 +143,64 @@ def test_decode_accuracy_is_tight(oracle_mod, c2):
     assert np.median(rel) < 1e-3
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_decode_plan_records_match_the_csr_path(oracle_mod, c2, M):
+    # with a plan the decode kernel reads each row block's record instead of
+    # the CSR block: the same entries summed in the same order, same bits
+    x = W.make_x(M, c2.K, 3100 + M)
+    y_csr, k0 = run(c2, x, 1.0, plan="auto")
+    y_rec, k1 = run(c2, x, 1.0, plan=True)
+    assert k0 == k1 == "decode"
+    assert np.array_equal(y_rec, y_csr)
+    assert_close(y_rec, oracle_y(oracle_mod, c2, x, 1.0), what=f"c2 planned M={M}")
+
+
+def skewed_rows_layer(K, N, heavy, per_heavy, seed):
+    """~1 % uniform rows plus `heavy` rows of `per_heavy` entries each, so
+    their 16-row blocks hold more entries than the plan's record."""
+    rng = np.random.default_rng(seed)
+    L = W.make_layer(K, N, 128, 0.0, seed=seed)
+    rows = []
+    for r in range(N):
+        n = per_heavy if r in heavy else int(rng.binomial(K, 0.01))
+        rows.append(np.sort(rng.choice(K, size=n, replace=False)).astype(np.int32))
+    rp = np.zeros(N + 1, np.int32)
+    rp[1:] = np.cumsum([len(c) for c in rows])
+    col = np.concatenate(rows).astype(np.int32)
+    vals = rng.normal(0, 0.05, len(col)).astype(np.float16)
+    return W.Layer(K, N, L.q, L.scales, rp, col, vals)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3])
+def test_decode_rows_past_the_record(oracle_mod, M):
+    lay = skewed_rows_layer(2048, 512, {17, 200, 201, 511}, 700, 3200)
+    x = W.make_x(M, lay.K, 3210 + M)
+    y_csr, _ = run(lay, x, 1.0, plan="auto")
+    y_rec, k = run(lay, x, 1.0, plan=True)
+    assert k == "decode"
+    assert np.array_equal(y_rec, y_csr)
+    assert_close(y_rec, oracle_y(oracle_mod, lay, x, 1.0), what=f"rows past the record M={M}")
+
+
+def test_decode_foreign_plan_falls_back_to_the_csr(oracle_mod):
+    # another layer's plan (large enough to pass the size check) fails the
+    # header check: the kernel reads the CSR instead of the records
+    big = W.make_layer(1024, 2048, 128, 0.03, seed=130)
+    lay = W.make_layer(1024, 1024, 128, 0.02, seed=131)
+    db, d = W.to_device(big), W.to_device(lay)
+    plan = _C_ops.build_plan(db["q"], db["scales"], db["vals"], db["col"], db["row_ptr"], big.K)
+    for M in (1, 2, 4):
+        x = W.make_x(M, lay.K, 132 + M)
+        xt = torch.from_numpy(x).cuda()
+        y = torch.full((M, lay.N), float("nan"), dtype=torch.float16, device="cuda")
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], xt, y, 1.0, plan)
+        assert _C_ops.last_kernel() == "decode"
+        torch.cuda.synchronize()
+        y_csr, _ = run(lay, x, 1.0, plan="auto")
+        assert np.array_equal(y.float().cpu().numpy(), y_csr)
+        assert_close(y_csr, oracle_y(oracle_mod, lay, x, 1.0), what=f"foreign plan M={M}")
+
+
 # ------------------------------------------------------- prefill (M > 16)
 
 @pytest.mark.parametrize("alpha", [0.0, 0.5, 1.0])
@@ -252,10 +310,10 @@ def test_skinny_chunk_table_with_columns_outside_k(oracle_mod):
     col = np.concatenate(rows).astype(np.int32)
     vals = rng.normal(0, 0.05, len(col)).astype(np.float16)
     lay = W.Layer(K, N, L.q, L.scales, rp, col, vals)
-    for M in (6, 33):
+    for M in (1, 3, 6, 33):
         x = W.make_x(M, K, 124 + M)
         y, k = run(lay, x, 1.0, plan=True)
-        assert k == "skinny"
+        assert k == ("decode" if M <= 4 else "skinny")
         assert_close(y, oracle_y(oracle_mod, lay, x, 1.0), what=f"outside columns M={M}")
 
 
@@ -338,7 +396,7 @@ def test_non_canonical_csr(oracle_mod):
     col[::23] = -3
     vals = rng.normal(0, 0.05, rp[-1]).astype(np.float16)
     lay = W.Layer(K, N, L.q, L.scales, rp, col, vals)
-    for M, plan in ((1, "auto"), (7, "auto"), (64, True), (64, "auto")):
+    for M, plan in ((1, "auto"), (1, True), (7, "auto"), (64, True), (64, "auto")):
         x = W.make_x(M, K, 98 + M)
         y, _ = run(lay, x, 1.0, plan=plan)
         assert_close(y, oracle_y(oracle_mod, lay, x, 1.0), what=f"non-canonical M={M}")
