@@ -91,9 +91,16 @@ constexpr uint32_t kDecPlanVersion = 3;
 // with three workgroups per CU.
 constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 
-// GMODE: 0 per-row scale (G == K); 1 G = 128 with scales readable as
-// aligned 32-bit pairs; 2 any G = 128 * 2^j (one 16-bit load per chunk).
-// CPW: compile-time bound of the chunks per wave (all issued at entry).
+// GMODE: 0 per-row scale (G == K); 4 the same with every wave taking
+// exactly CPW chunks (K == 512 * CPW); 1 G = 128 with the scales of 8 chunks
+// readable as one aligned 16-byte vector (K % 4096 == 0, so every wave takes
+// exactly CPW chunks); 3 G = 128 with scales readable as aligned 32-bit
+// pairs; 2 any G = 128 * 2^j (one 16-bit load per chunk).
+// CPW: compile-time bound of the chunks per wave.  The weight loads of the
+// first PDP chunk pairs are issued at entry; with all CPW chunks valid the
+// main loop issues pair j + PDP as it takes pair j, so a wave never has more
+// than PDP + 1 pairs in flight and its vector-memory instructions do not
+// queue behind the weight streams of the whole CU before it can compute.
 // SPARSE: 0 no ortho term; 1 ortho term with the workgroup's CSR block
 // staged through LDS (16-byte aligned columns, nnz >= 4); 2 ortho term read
 // entry by entry in the epilogue; 3 / 4 / 5 the plan's record of the block
@@ -110,7 +117,10 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     constexpr int NT = kDecodeNT;
     constexpr int RT = 16;
     constexpr int MI = MT < 4 ? MT : 4;        // live D rows per lane group (tokens 4g + i)
-    constexpr bool GROUPED = GMODE != 0;
+    constexpr bool GROUPED = GMODE != 0 && GMODE != 4;
+    constexpr bool FULL = GMODE == 1 || GMODE == 4;  // every wave has CPW chunks
+    constexpr int PDP = CPW / 2 < 2 ? CPW / 2 : 2;  // weight pairs in flight ahead of the main loop
+    constexpr int PDC = 2 * PDP;                     // the same in chunks (direct loads)
     constexpr int XIT = (CPW * 16 + 63) / 64;  // 16-byte activation pieces per lane per token
     constexpr int ES = kDecodeESlots;
     // WT: the weights pass through LDS (see decode_wt)
@@ -198,12 +208,18 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     f16 srow = (f16)0.0f;
     if (!GROUPED) srow = a.scales[n0 + min(SPARSE ? tid >> 4 : tid & 15, last_row)];
 
-    // ---- group scales of this lane's row nl: chunks c_lo + 2i, + 2i + 1 as
-    //      one 32-bit pair (GMODE 1), or one scale per chunk (GMODE 2)
+    // ---- group scales of this lane's row nl: chunks c_lo + 8i .. + 8i + 7
+    //      as one 16-byte vector (GMODE 1), chunks c_lo + 2i, + 2i + 1 as one
+    //      32-bit pair (GMODE 3), or one scale per chunk (GMODE 2)
     const f16 *sbase = a.scales + (n0 + my_row) * (int64_t)a.ngroups;
-    uint32_t sw[GMODE == 1 ? CPW / 2 : 1];
+    u32x4 sv[GMODE == 1 ? (CPW + 7) / 8 : 1];
+    uint32_t sw[GMODE == 3 ? CPW / 2 : 1];
     f16 sh[GMODE == 2 ? CPW : 1];
     if (GMODE == 1) {
+#pragma unroll
+        for (int i = 0; i < (CPW + 7) / 8; i++)
+            sv[i] = *reinterpret_cast<const u32x4 *>(sbase + min(c_lo + 8 * i, clast & ~7));
+    } else if (GMODE == 3) {
 #pragma unroll
         for (int i = 0; i < CPW / 2; i++)
             sw[i] = *reinterpret_cast<const uint32_t *>(sbase + (min(c_lo + 2 * i, clast) & ~1));
@@ -221,28 +237,31 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     //      (the XOR spreads the MFMA-layout reads below over all LDS banks).
     u32x4 wv[WT ? 1 : CPW];
     u32x4 wq[WT ? CPW / 2 : 1][2];
+    const uint8_t *qrow = a.q + (n0 + my_row) * (int64_t)(K >> 1) + g * 16;
+    const uint8_t *qh[2];
+    int sh2[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int r = 8 * h + (lane >> 3);
+        const int sl = (lane & 7) ^ ((r >> 1) & 7);
+        qh[h] = a.q + (n0 + min(r, last_row)) * (int64_t)(K >> 1) + (sl & 3) * 16;
+        sh2[h] = sl >> 2;  // which chunk of the pair
+    }
+    auto load_chunk = [&](int p) {
+        wv[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(qrow + min(c_lo + p, clast) * 64));
+    };
+    auto load_pair = [&](int j) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            wq[j][h] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4 *>(qh[h] + min(c_lo + 2 * j + sh2[h], clast) * 64));
+    };
     if (!WT) {
-        const uint8_t *qrow = a.q + (n0 + my_row) * (int64_t)(K >> 1) + g * 16;
 #pragma unroll
-        for (int p = 0; p < CPW; p++)
-            wv[p] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4 *>(qrow + min(c_lo + p, clast) * 64));
+        for (int p = 0; p < PDC; p++) load_chunk(p);
     } else {
-        const uint8_t *qh[2];
-        int sh2[2];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int r = 8 * h + (lane >> 3);
-            const int sl = (lane & 7) ^ ((r >> 1) & 7);
-            qh[h] = a.q + (n0 + min(r, last_row)) * (int64_t)(K >> 1) + (sl & 3) * 16;
-            sh2[h] = sl >> 2;  // which chunk of the pair
-        }
-#pragma unroll
-        for (int j = 0; j < CPW / 2; j++)
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-                wq[j][h] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4 *>(qh[h] + min(c_lo + 2 * j + sh2[h], clast) * 64));
+        for (int j = 0; j < PDP; j++) load_pair(j);
     }
 
     // ---- activations from global memory (no LDS staging): 64 bytes per
@@ -409,10 +428,12 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     // chunk p's partial into acc: scaled (GROUPED) after its bias sum is removed
     auto chunk_done = [&](const f32x4 &part, int p) {
         float s;
-        if (GMODE == 1)
-            s = (float)__builtin_bit_cast(f16, (uint16_t)((p & 1) ? (sw[p >> 1] >> 16) : (sw[p >> 1] & 0xffffu)));
-        else
+        if (GMODE == 1 || GMODE == 3) {
+            const uint32_t w2 = GMODE == 1 ? sv[p >> 3][(p >> 1) & 3] : sw[p >> 1];
+            s = (float)__builtin_bit_cast(f16, (uint16_t)((p & 1) ? (w2 >> 16) : (w2 & 0xffffu)));
+        } else {
             s = (float)sh[p];
+        }
 #pragma unroll
         for (int i = 0; i < MI; i++) {
             float v = part[i];
@@ -445,6 +466,8 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 } else {
                     w0 = wv[2 * j];
                     w1 = wv[2 * j + 1];
+                    if (2 * j + PDC < CPW) load_chunk(2 * j + PDC);
+                    if (2 * j + 1 + PDC < CPW) load_chunk(2 * j + 1 + PDC);
                 }
                 const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w};
                 const uint32_t u1[4] = {w1.x, w1.y, w1.z, w1.w};
@@ -471,19 +494,34 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                                                                 __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
                                                                 pb, 0, 0, 0);
                 }
+                if (WT && j + PDP < CPW / 2) load_pair(j + PDP);
                 chunk_done(pa, 2 * j);
                 chunk_done(pb, 2 * j + 1);
             }
         } else {
+            if constexpr (!FULL) {
+                // the rest of the weights at once (addresses clamped, branch-free)
+                if (WT) {
+#pragma unroll
+                    for (int j = PDP; j < CPW / 2; j++) load_pair(j);
+                } else {
+#pragma unroll
+                    for (int p = PDC; p < CPW; p++) load_chunk(p);
+                }
+            }
 #pragma unroll
             for (int p = 0; p < CPW; p++) {
                 if (FULL || p < nci) {  // uniform
                     u32x4 wp;
                     if (WT) {
-                        if ((p & 1) == 0) pair_to_lds(p >> 1);
+                        if ((p & 1) == 0) {
+                            pair_to_lds(p >> 1);
+                            if (FULL && (p >> 1) + PDP < CPW / 2) load_pair((p >> 1) + PDP);
+                        }
                         wp = wt_read(p >> 1, p & 1);
                     } else {
                         wp = wv[p];
+                        if (FULL && p + PDC < CPW) load_chunk(p + PDC);
                     }
                     if (GROUPED) {
                         chunk_done(chunk_mfma(wp, p, f32x4{0.f, 0.f, 0.f, 0.f}), p);
@@ -498,8 +536,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
             }
         }
     };
-    if (nci == CPW) main_loop(std::true_type{});
-    else main_loop(std::false_type{});
+    main_loop(std::integral_constant<bool, FULL>{});
     if (!GROUPED && XLDS) {
 #pragma unroll
         for (int i = 0; i < MI; i++) acc[i] -= bias_acc[i];
@@ -643,6 +680,8 @@ static hipError_t launch_decode_k(const DecodeArgs &d, int64_t lds, hipStream_t 
 template <int MT, int GMODE, bool XLDS, int CPW>
 static hipError_t launch_decode_t(const DecodeArgs &d0, hipStream_t stream) {
     DecodeArgs d = d0;
+    // GMODE 1 and 4 kernels take exactly CPW chunks in every wave
+    if ((GMODE == 1 || GMODE == 4) && !(d.cpw == CPW && d.nchunks == 4 * CPW)) return hipErrorInvalidValue;
     if constexpr (XLDS && MT <= 4) {
         // plan records when the LDS takes them (else the CSR block below)
         if (d.has_ortho && d.dcap > 0 && d.dcap <= 4096) {
@@ -755,8 +794,17 @@ hipError_t launch_decode(const ForwardArgs &a, const void *plan, hipStream_t str
         while ((128LL << d.gshift) < a.G) d.gshift++;
     d.scale_pairs = (a.ngroups % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.scales) & 3) == 0);
     const bool xlds = decode_xlds(a.M, a.K);
-    const int gmode = !grouped ? 0 : (d.gshift == 0 && d.scale_pairs ? 1 : 2);
+    // 16-byte scale vectors: 8 chunks per vector, each wave's chunks start
+    // on a vector boundary
+    const bool scale_vec = d.gshift == 0 && a.ngroups % 8 == 0 && d.cpw % 8 == 0 &&
+                           (reinterpret_cast<uintptr_t>(a.scales) & 15) == 0;
+    // every wave takes exactly the chunk bound (8, 16 or 24 chunks)
+    const bool full = d.nchunks == 4 * d.cpw && (d.cpw == 8 || d.cpw == 16 || d.cpw == 24);
+    const int gmode = !grouped ? (full ? 4 : 0)
+                               : (d.gshift != 0 ? 2 : (scale_vec && full ? 1 : (d.scale_pairs ? 3 : 2)));
     if (gmode == 1) return xlds ? launch_decode_mt<1, true>(mt, d, stream) : launch_decode_mt<1, false>(mt, d, stream);
+    if (gmode == 3) return xlds ? launch_decode_mt<3, true>(mt, d, stream) : launch_decode_mt<3, false>(mt, d, stream);
+    if (gmode == 4) return xlds ? launch_decode_mt<4, true>(mt, d, stream) : launch_decode_mt<4, false>(mt, d, stream);
     if (gmode == 2) return xlds ? launch_decode_mt<2, true>(mt, d, stream) : launch_decode_mt<2, false>(mt, d, stream);
     return xlds ? launch_decode_mt<0, true>(mt, d, stream) : launch_decode_mt<0, false>(mt, d, stream);
 }
