@@ -76,6 +76,21 @@ __device__ __forceinline__ int sext4(uint32_t nib) { return (int)(nib ^ 8u) - 8;
 
 // CSR row range [rs, re), clamped into [0, nnz] so a malformed row_ptr can
 // never address outside the index arrays.
+// Ortho plan decode records (built in orth_prefill.hip, read by the decode
+// kernel): per 16-row block, kRecHdrWords header words then dcap entries.
+// Header: [0] tag, [1] e0 = row_ptr[16 b] clamped to [0, nnz], [2 + r] and
+// [18 + r] the CSR range [rs, re) of row 16 b + r as csr_row_range gives it
+// (empty past N), [34], [35] zero.  Entry s: CSR position e0 + s as column
+// (0xffff outside [0, K)) | fp16 value bits << 16 (0xffff past nnz).
+constexpr int kRecHdrWords = 36;
+
+// Tag of block b's record: ties a record to the layer shape and its place,
+// so that a plan of another layer (or a stale stride) is not read as this one.
+__host__ __device__ inline uint32_t plan_rec_tag(int64_t N, int64_t K, int64_t nnz, int dcap, int64_t b) {
+    return 0x52454331u ^ (uint32_t)nnz ^ ((uint32_t)N * 0x9E3779B1u) ^ ((uint32_t)K << 17) ^
+           ((uint32_t)dcap * 0xC2B2AE3Du) ^ ((uint32_t)b * 0x85EBCA77u);
+}
+
 __device__ __forceinline__ void csr_row_range(const int32_t *row_ptr, int64_t n, int64_t nnz,
                                               int32_t &rs, int32_t &re) {
     int64_t a = row_ptr[n], b = row_ptr[n + 1];

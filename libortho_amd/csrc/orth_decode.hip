@@ -75,15 +75,9 @@ struct DecodeArgs {
     int lds_e;
     float alpha;
     int has_ortho;
-    const uint32_t *phdr;  // plan header (record kernels), checked before the record is used
-    const uint32_t *rec;   // plan records, dcap words per 16-row block
+    const uint32_t *rec;   // plan records, kRecHdrWords + dcap words per 16-row block
     int dcap;              // record entries per block (a multiple of 16), 0 without a plan
 };
-
-// plan header words the record kernels check (the plan's layout is defined
-// with its builder in orth_prefill.hip)
-constexpr uint32_t kDecPlanMagic = 0x504f5254u;
-constexpr uint32_t kDecPlanVersion = 3;
 
 // Weights pass through LDS (whole-line loads, transposed on the way) for
 // one or two tokens with staged activations: there the weight stream is all
@@ -104,7 +98,7 @@ constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 // SPARSE: 0 no ortho term; 1 ortho term with the workgroup's CSR block
 // staged through LDS (16-byte aligned columns, nnz >= 4); 2 ortho term read
 // entry by entry in the epilogue; 3 / 4 / 5 the plan's record of the block
-// (at most 1024 / 2048 / 4096 entries) staged through LDS and summed before
+// (at most 1024 / 2048 / 4096 words) staged through LDS and summed before
 // the main loop (XLDS only).
 //
 // Every global load below is unconditional with a clamped, always valid
@@ -179,16 +173,16 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         }
     }
 
-    // ---- the block's plan record (no row pointer needed: issued before the
-    //      weights, it returns with the activations) and the plan header
+    // ---- the block's plan record: its address needs no row pointer and it
+    //      carries the rows' CSR ranges, so it is issued before the weights
+    //      and returns with the activations
+    const int rwords = kRecHdrWords + a.dcap;
     u32x4 rv[ER];
-    int32_t hw = 0;
     if (REC) {
-        const uint32_t *rb = a.rec + (int64_t)blockIdx.x * a.dcap;
+        const uint32_t *rb = a.rec + (int64_t)blockIdx.x * rwords;
 #pragma unroll
         for (int r = 0; r < ER; r++)
-            rv[r] = *reinterpret_cast<const u32x4 *>(rb + min(4 * (tid + NT * r), a.dcap - 4));
-        hw = (int32_t)a.phdr[min(lane, 13)];
+            rv[r] = *reinterpret_cast<const u32x4 *>(rb + min(4 * (tid + NT * r), rwords - 4));
     }
 
     // ---- CSR bounds: this thread's epilogue row, and the workgroup block
@@ -198,7 +192,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     //      before the CSR block loads.
     const int rl = tid >> 4, sub = tid & 15;
     int32_t r_lo = 0, r_hi = 0, pv = 0;
-    if (SPARSE) {
+    if (SPARSE && !REC) {
         r_lo = a.row_ptr[n0 + min(rl, last_row)];
         r_hi = a.row_ptr[n0 + min(rl, last_row) + 1];
         pv = a.row_ptr[n0 + min(lane, last_row + 1)];
@@ -317,7 +311,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     //      wait for the row pointers, and the staging need not.
     __builtin_amdgcn_sched_barrier(0);
     int32_t rs = 0, re = 0, e0 = 0, e1 = 0;
-    if (SPARSE) {
+    if (SPARSE && !REC) {
         rs = min(max(r_lo, 0), a.nnz);
         re = min(max(r_hi, rs), a.nnz);
         if (rl > last_row) re = rs;  // rows past N have no entries
@@ -334,25 +328,31 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int m = 0; m < MT; m++) sacc[m] = 0.f;
     int32_t rec_hi = 0;
+    bool rec_ok = true;
     if (REC) {
         uint32_t *er = reinterpret_cast<uint32_t *>(smem + a.lds_e);
 #pragma unroll
         for (int r = 0; r < ER; r++) {
             const int slot = 4 * (tid + NT * r);
-            if (slot < a.dcap) *reinterpret_cast<u32x4 *>(er + slot) = rv[r];
+            if (slot < rwords) *reinterpret_cast<u32x4 *>(er + slot) = rv[r];
         }
         __syncthreads();  // all activations and the record are in LDS
-        auto word = [&](int l) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane(hw, l); };
-        const bool ok = (word(0) == kDecPlanMagic) & (word(1) == kDecPlanVersion) &
-                        (word(6) == (uint32_t)a.N) & (word(7) == (uint32_t)(a.N >> 32)) &
-                        (word(8) == (uint32_t)K) & (word(9) == 0u) & (word(10) == (uint32_t)a.nnz) &
-                        (word(11) == 0u) & (word(13) == (uint32_t)a.dcap);
-        rec_hi = (ok && rs >= e0) ? min(re, e0 + a.dcap) : rs;
+        // the record of another layer or block fails the tag: the rows are
+        // then read from the CSR at the end
+        rec_ok = er[0] == plan_rec_tag(a.N, K, a.nnz, a.dcap, blockIdx.x);
+        if (rec_ok) {
+            e0 = min(max((int32_t)er[1], 0), a.nnz);
+            rs = min(max((int32_t)er[2 + rl], 0), a.nnz);
+            re = min(max((int32_t)er[18 + rl], rs), a.nnz);
+            if (rl > last_row) re = rs;
+        }
+        rec_hi = (rec_ok && rs >= e0) ? min(re, e0 + a.dcap) : rs;
+        const uint32_t *ee = er + kRecHdrWords;
         constexpr int U = 4;
         for (int32_t j0 = rs + sub; j0 < rec_hi; j0 += 16 * U) {
             uint32_t w[U];
 #pragma unroll
-            for (int u = 0; u < U; u++) w[u] = er[min(j0 + 16 * u, rec_hi - 1) - e0];
+            for (int u = 0; u < U; u++) w[u] = ee[min(j0 + 16 * u, rec_hi - 1) - e0];
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int c = (int)(w[u] & 0xffffu);
@@ -562,6 +562,11 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     //      staged block (very dense rows) are read from memory one by one.
     if (SPARSE) {
         constexpr int U = 4;
+        if (REC && !rec_ok) {  // (uniform) this row's CSR range, read from memory
+            csr_row_range(a.row_ptr, n0 + min(rl, last_row), a.nnz, rs, re);
+            if (rl > last_row) re = rs;
+            rec_hi = rs;
+        }
         const int32_t staged_hi = SPARSE == 1 ? min(min(eb + kDecodeEStaged, last4 + 4), e1) : eb;
         const int32_t fast_hi = REC ? rec_hi : min(re, staged_hi);
         for (int32_t j0 = rs + sub; !REC && j0 < fast_hi; j0 += 16 * U) {
@@ -684,11 +689,12 @@ static hipError_t launch_decode_t(const DecodeArgs &d0, hipStream_t stream) {
     if ((GMODE == 1 || GMODE == 4) && !(d.cpw == CPW && d.nchunks == 4 * CPW)) return hipErrorInvalidValue;
     if constexpr (XLDS && MT <= 4) {
         // plan records when the LDS takes them (else the CSR block below)
-        if (d.has_ortho && d.dcap > 0 && d.dcap <= 4096) {
-            const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW, d.dcap);
+        const int rwords = kRecHdrWords + d.dcap;
+        if (d.has_ortho && d.dcap > 0 && rwords <= 4096) {
+            const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW, rwords);
             if (lds <= kDecodeLdsMax) {
-                if (d.dcap <= 1024) return launch_decode_k<MT, GMODE, XLDS, CPW, 3>(d, lds, stream);
-                if (d.dcap <= 2048) return launch_decode_k<MT, GMODE, XLDS, CPW, 4>(d, lds, stream);
+                if (rwords <= 1024) return launch_decode_k<MT, GMODE, XLDS, CPW, 3>(d, lds, stream);
+                if (rwords <= 2048) return launch_decode_k<MT, GMODE, XLDS, CPW, 4>(d, lds, stream);
                 return launch_decode_k<MT, GMODE, XLDS, CPW, 5>(d, lds, stream);
             }
         }
@@ -781,7 +787,6 @@ hipError_t launch_decode(const ForwardArgs &a, const void *plan, hipStream_t str
     d.alpha = a.alpha;
     d.has_ortho = a.has_ortho;
     const bool rec = plan && a.has_ortho;
-    d.phdr = rec ? static_cast<const uint32_t *>(plan) : nullptr;
     d.rec = rec ? reinterpret_cast<const uint32_t *>(static_cast<const char *>(plan) + plan_rec_at(a.N, a.K, a.nnz))
                 : nullptr;
     d.dcap = rec ? (int)plan_rec_cap(a.N, a.nnz) : 0;

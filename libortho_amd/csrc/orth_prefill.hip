@@ -34,11 +34,13 @@ namespace orth {
 //   uint32 entries[nnz]                   (row_in_block << 24) | (col_in_step << 16) | fp16 bits
 //   uint16 chunks[N][K/128 + 1]           (K % 128 == 0 only) per row, the number of
 //                                         its CSR entries with column < 128 c
-//   uint32 records[ceil(N/16)][dcap]      per 16-row block b, the CSR positions
-//                                         [e0, e0 + dcap), e0 = row_ptr[16 b] clamped
-//                                         to [0, nnz]: column (0xffff when outside
-//                                         [0, K)) | fp16 value bits << 16; 0xffff
-//                                         past nnz.  dcap is in the header's pad[0].
+//   uint32 records[ceil(N/16)][36 + dcap] per 16-row block b: a header (tag, e0 =
+//                                         row_ptr[16 b] clamped to [0, nnz], the CSR
+//                                         range of each of the 16 rows) and the CSR
+//                                         positions [e0, e0 + dcap) as column (0xffff
+//                                         when outside [0, K)) | fp16 value bits << 16
+//                                         (0xffff past nnz); see orth_common.h.  dcap
+//                                         is in the header's pad[0].
 // Entries of one (block, step) are ordered by row then by CSR position.  The
 // chunk table locates a row's entries of columns [128 c0, 128 c1) in the CSR
 // itself when the row's columns ascend strictly (flag kPlanUnsorted clear).
@@ -81,8 +83,9 @@ int64_t plan_chunks_bytes(int64_t N, int64_t K) {
 
 // Entries per decode record: the mean count of a 16-row block plus four
 // times its square root (a binomial block count's standard deviation), in
-// whole 16-entry groups, at most kPlanRecMax.
-static const int64_t kPlanRecMax = 4096;
+// whole 16-entry groups, at most kPlanRecMax (a record of at most 4096
+// words: four 16-byte loads per thread of the decode kernel).
+static const int64_t kPlanRecMax = 4096 - 48;
 
 int64_t plan_rec_cap(int64_t N, int64_t nnz) {
     if (nnz <= 0 || N <= 0) return 0;
@@ -99,7 +102,7 @@ int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz) {
 
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) {
     if (nnz <= 0) return 0;
-    return plan_rec_at(N, K, nnz) + ((N + 15) / 16) * plan_rec_cap(N, nnz) * 4;
+    return plan_rec_at(N, K, nnz) + ((N + 15) / 16) * (kRecHdrWords + plan_rec_cap(N, nnz)) * 4;
 }
 
 // Largest K the plan builder's LDS counters take (int32 per (step, row)).
@@ -243,8 +246,22 @@ __global__ void __launch_bounds__(256) plan_rec_kernel(ForwardArgs a, uint32_t *
     const int64_t b = blockIdx.x;
     int64_t e0 = a.row_ptr[b * 16];
     e0 = e0 < 0 ? 0 : (e0 > a.nnz ? a.nnz : e0);
-    uint32_t *r = rec + b * dcap;
-    for (int s = threadIdx.x; s < dcap; s += 256) {
+    uint32_t *hdr = rec + b * (kRecHdrWords + dcap);
+    uint32_t *r = hdr + kRecHdrWords;
+    const int t = threadIdx.x;
+    if (t == 0) {
+        hdr[0] = plan_rec_tag(a.N, a.K, a.nnz, dcap, b);
+        hdr[1] = (uint32_t)e0;
+        hdr[34] = hdr[35] = 0u;
+    }
+    if (t < 16) {
+        const int64_t n = b * 16 + t;
+        int32_t rs = 0, re = 0;
+        if (n < a.N) csr_row_range(a.row_ptr, n, a.nnz, rs, re);
+        hdr[2 + t] = (uint32_t)rs;
+        hdr[18 + t] = (uint32_t)re;
+    }
+    for (int s = t; s < dcap; s += 256) {
         const int64_t j = e0 + s;
         uint32_t w = 0xffffu;
         if (j < a.nnz) {

@@ -147,9 +147,9 @@ def test_forward_without_gpu_reports_no_device(L):
 
 def rec_cap(N, nnz):
     # decode records: mean entries of a 16-row block + 4 (isqrt(mean) + 1),
-    # in 16-entry groups, at most 4096
+    # in 16-entry groups, at most 4048 (36 header words + entries <= 4096)
     mean = -(-16 * nnz // N)
-    return min(4096, (mean + 4 * (math.isqrt(mean) + 1) + 15) // 16 * 16)
+    return min(4048, (mean + 4 * (math.isqrt(mean) + 1) + 15) // 16 * 16)
 
 
 def test_plan_size(L):
@@ -157,16 +157,16 @@ def test_plan_size(L):
     n = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4096, N=4096, nnz=100)))
     offsets = ((4096 // 128) * (4096 // 64 + 1) * 4 + 15) // 16 * 16
     chunks = (4096 * (4096 // 128 + 1) * 2 + 15) // 16 * 16  # uint16 [N][K/128 + 1]
-    records = (4096 // 16) * rec_cap(4096, 100) * 4          # uint32 [N/16][dcap]
+    records = (4096 // 16) * (36 + rec_cap(4096, 100)) * 4   # uint32 [N/16][36 + dcap]
     assert rec_cap(4096, 100) == 16
     assert n == (64 + offsets + 400 + 15) // 16 * 16 + chunks + records
     # K % 128 != 0: no chunk table; a ragged last row block still has a record
     n64 = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4160, N=4100, nnz=100)))
     assert n64 == (64 + ((4100 + 127) // 128) * (4160 // 64 + 1) * 4 + 400 + 15) // 16 * 16 + \
-        ((4100 + 15) // 16) * rec_cap(4100, 100) * 4
+        ((4100 + 15) // 16) * (36 + rec_cap(4100, 100)) * 4
     # c2 (1 % of 4096 x 11008): 656 entries per block on average -> 768
     assert rec_cap(11008, 450888) == 768
-    assert rec_cap(64, 64 * 4096) == 4096  # capped
+    assert rec_cap(64, 64 * 4096) == 4048  # capped
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4000, nnz=5))) < 0  # K % 64 != 0
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4095))) == -_lib.ERR_INVALID_ARGUMENT
 
