@@ -22,8 +22,9 @@
 //    whole range is read and filtered by column, in batches of eight
 //    entries.  Up to 16 tokens, four consecutive lanes share a row: each
 //    loads two of every eight entries, DPP quad broadcasts hand all eight to
-//    the four, each multiplies them with four tokens' staged activations,
-//    and the sums reach the MFMA lanes through LDS.  From 17 tokens (more
+//    the four, each multiplies them with four tokens' staged activations
+//    (two up to 8 tokens: tokens past M are padding of the tile), and the
+//    sums reach the MFMA lanes through LDS.  From 17 tokens (more
 //    registers, and an LDS exchange would cost the second workgroup per CU)
 //    each lane takes the row and tokens of its own MFMA output and reads the
 //    row's entries itself.  Sums are formed in CSR order: the result does not
@@ -88,13 +89,23 @@ struct SkinnyArgs {
 };
 
 // GMODE: 0 per-row scale (G == K); 1 G = 128, scales read as aligned pairs;
-// 2 any G = 128 * 2^j.  NTT: 16-token tiles.  CPS: chunk bound per slice.
-template <int NTT, int GMODE, int CPS, bool SPARSE>
+// 2 any G = 128 * 2^j; 3 (one token tile) G = 128 with every slice exactly CPS = 8 chunks
+// (K = 1024 S) and its scales one aligned 16-byte vector per row: the dense
+// term is straight-line code over chunk pairs (two MFMA chains interleaved)
+// and the weight loads run four chunks ahead instead of all at entry.
+// NTT: 16-token tiles.  CPS: chunk bound per slice.  SPK: 0 no ortho term,
+// 1 ortho term, 2 ortho term for at most 8 tokens (one tile: the four lanes
+// of a row gather two tokens each, not four).
+template <int NTT, int GMODE, int CPS, int SPK>
 __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT <= 2 ? 4 : 2))) skinny_kernel(SkinnyArgs a) {
+    constexpr bool SPARSE = SPK != 0;
     constexpr int MP = NTT * 16;                     // padded tokens
     constexpr int XP = (MP * CPS * 16 + kSkNT - 1) / kSkNT;  // 16-byte pieces per thread
     constexpr int SW = (CPS + 7) / 8;
     constexpr bool GROUPED = GMODE != 0;
+    constexpr bool FULL = GMODE == 3;  // every slice holds exactly CPS chunks
+    static_assert(!FULL || CPS == 8, "full slices are one scale vector");
+    constexpr int PDC = FULL ? 4 : CPS;  // weight loads issued at entry
     // QUAD: four consecutive lanes per row in the sparse term (one token tile)
     constexpr bool QUAD = NTT == 1;
     constexpr int EL = QUAD ? kSkEB / 4 : kSkEB;  // entries a lane loads per batch
@@ -160,9 +171,12 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
     const f16 *sbase = a.scales + my_n * (int64_t)a.ngroups;
     uint32_t sw[SW];
     f16 sh[GMODE == 2 ? CPS : 1];
+    u32x4 sv = u32x4{0u, 0u, 0u, 0u};  // GMODE 3: this row's 8 scales of the slice
     float srow = 0.f;  // GMODE 0: the scale of row 16 w + nl (tid & 15 == nl)
     if (GMODE == 0) srow = (float)a.scales[min(wrow0 + (tid & 15), a.N - 1)];
-    if (GMODE == 1) {
+    if (GMODE == 3) {
+        sv = *reinterpret_cast<const u32x4 *>(sbase + kc0);
+    } else if (GMODE == 1) {
 #pragma unroll
         for (int i = 0; i < SW; i++)
             sw[i] = *reinterpret_cast<const uint32_t *>(sbase + (min(kc0 + 8 * i + 2 * g, clast) & ~1));
@@ -174,9 +188,11 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
     // ---- weights (nontemporal), one 16-byte load per chunk
     const uint8_t *qrow = a.q + my_n * (int64_t)(K >> 1) + g * 16;
     u32x4 wv[CPS];
-#pragma unroll
-    for (int p = 0; p < CPS; p++)
+    auto load_chunk = [&](int p) {
         wv[p] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(qrow + min(kc0 + p, clast) * 64));
+    };
+#pragma unroll
+    for (int p = 0; p < PDC; p++) load_chunk(p);
 
     // ---- stage the activations (interleaved k order) and their bias sums
 #pragma unroll
@@ -239,40 +255,83 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
 #pragma unroll
         for (int i = 0; i < 4; i++) bias_acc[tt][i] = 0.f;
     }
+    if constexpr (FULL) {
 #pragma unroll
-    for (int p = 0; p < CPS; p++) {
-        if (p < nci) {  // uniform
-            const uint32_t words[4] = {wv[p].x, wv[p].y, wv[p].z, wv[p].w};
-            uint32_t bq[4][4];
+        for (int p = 0; p < CPS; p += 2) {
+            uint32_t bq0[4][4], bq1[4][4];
+            {
+                const uint32_t w0[4] = {wv[p].x, wv[p].y, wv[p].z, wv[p].w};
+                const uint32_t w1[4] = {wv[p + 1].x, wv[p + 1].y, wv[p + 1].z, wv[p + 1].w};
 #pragma unroll
-            for (int j = 0; j < 4; j++) int4x8_to_f16_biased(words[j], bq[j]);
-            float s = 1.0f;
-            if (GMODE == 1) {
-                // scales of chunks kc0 + 8i + 2g', +1 sit in lane 16g' + nl
-                const uint32_t w2 = (uint32_t)__shfl((int)sw[p >> 3], 16 * ((p & 7) >> 1) + nl, 64);
-                s = (float)__builtin_bit_cast(f16, (uint16_t)((p & 1) ? (w2 >> 16) : (w2 & 0xffffu)));
-            } else if (GMODE == 2) {
-                s = (float)sh[p];
+                for (int j = 0; j < 4; j++) {
+                    int4x8_to_f16_biased(w0[j], bq0[j]);
+                    int4x8_to_f16_biased(w1[j], bq1[j]);
+                }
             }
+            if (p + PDC < CPS) load_chunk(p + PDC);
+            if (p + 1 + PDC < CPS) load_chunk(p + 1 + PDC);
+            const uint32_t s2 = sv[p >> 1];  // the scales of chunks p, p + 1
+            const float s0 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 & 0xffffu));
+            const float s1 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 >> 16));
 #pragma unroll
             for (int tt = 0; tt < NTT; tt++) {
                 const f16 *xl = xs + ((tt * 16 + nl) * a.xstride + p * 128 + g * 32);
-                f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+                f32x4 pa = f32x4{0.f, 0.f, 0.f, 0.f}, pb = pa;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const f16x8 afr = *reinterpret_cast<const f16x8 *>(xl + 8 * j);
-                    const f16x8 bfr = __builtin_bit_cast(f16x8, u32x4{bq[j][0], bq[j][1], bq[j][2], bq[j][3]});
-                    part = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr, bfr, part, 0, 0, 0);
+                    const f16x8 a0 = *reinterpret_cast<const f16x8 *>(xl + 8 * j);
+                    const f16x8 a1 = *reinterpret_cast<const f16x8 *>(xl + 128 + 8 * j);
+                    pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        a0, __builtin_bit_cast(f16x8, u32x4{bq0[j][0], bq0[j][1], bq0[j][2], bq0[j][3]}), pa, 0, 0, 0);
+                    pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        a1, __builtin_bit_cast(f16x8, u32x4{bq1[j][0], bq1[j][1], bq1[j][2], bq1[j][3]}), pb, 0, 0, 0);
                 }
                 // D[token 4g + i][row nl]
-                const f32x4 crv = *reinterpret_cast<const f32x4 *>(cr + p * MP + tt * 16 + 4 * g);
+                const f32x4 cra = *reinterpret_cast<const f32x4 *>(cr + p * MP + tt * 16 + 4 * g);
+                const f32x4 crb = *reinterpret_cast<const f32x4 *>(cr + (p + 1) * MP + tt * 16 + 4 * g);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    if (GROUPED) {
-                        acc[tt][i] += s * (part[i] - crv[i]);
-                    } else {
-                        acc[tt][i] += part[i];
-                        bias_acc[tt][i] += crv[i];
+                    acc[tt][i] += s0 * (pa[i] - cra[i]);
+                    acc[tt][i] += s1 * (pb[i] - crb[i]);
+                }
+            }
+        }
+    } else {
+    #pragma unroll
+        for (int p = 0; p < CPS; p++) {
+            if (p < nci) {  // uniform
+                const uint32_t words[4] = {wv[p].x, wv[p].y, wv[p].z, wv[p].w};
+                uint32_t bq[4][4];
+    #pragma unroll
+                for (int j = 0; j < 4; j++) int4x8_to_f16_biased(words[j], bq[j]);
+                float s = 1.0f;
+                if (GMODE == 1) {
+                    // scales of chunks kc0 + 8i + 2g', +1 sit in lane 16g' + nl
+                    const uint32_t w2 = (uint32_t)__shfl((int)sw[p >> 3], 16 * ((p & 7) >> 1) + nl, 64);
+                    s = (float)__builtin_bit_cast(f16, (uint16_t)((p & 1) ? (w2 >> 16) : (w2 & 0xffffu)));
+                } else if (GMODE == 2) {
+                    s = (float)sh[p];
+                }
+    #pragma unroll
+                for (int tt = 0; tt < NTT; tt++) {
+                    const f16 *xl = xs + ((tt * 16 + nl) * a.xstride + p * 128 + g * 32);
+                    f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const f16x8 afr = *reinterpret_cast<const f16x8 *>(xl + 8 * j);
+                        const f16x8 bfr = __builtin_bit_cast(f16x8, u32x4{bq[j][0], bq[j][1], bq[j][2], bq[j][3]});
+                        part = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr, bfr, part, 0, 0, 0);
+                    }
+                    // D[token 4g + i][row nl]
+                    const f32x4 crv = *reinterpret_cast<const f32x4 *>(cr + p * MP + tt * 16 + 4 * g);
+    #pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        if (GROUPED) {
+                            acc[tt][i] += s * (part[i] - crv[i]);
+                        } else {
+                            acc[tt][i] += part[i];
+                            bias_acc[tt][i] += crv[i];
+                        }
                     }
                 }
             }
@@ -282,7 +341,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
     // ---- sparse term, in batches of eight entries; columns outside the
     //      slice are skipped.  Token t of the lane: QUAD tg + 4 t, else
     //      16 (t / 4) + 4 g + t % 4 (the MFMA output's tokens).
-    constexpr int TQ = QUAD ? MP / 4 : NTT * 4;  // tokens per lane
+    constexpr int TQ = QUAD ? (SPK == 2 ? 2 : MP / 4) : NTT * 4;  // tokens per lane
     float sacc[SPARSE ? TQ : 1];
     if (SPARSE) {
 #pragma unroll
@@ -474,7 +533,7 @@ bool skinny_supported(const ForwardArgs &a) {
     return skinny_shape(a, 256, sh);
 }
 
-template <int NTT, int GMODE, int CPS, bool SPARSE>
+template <int NTT, int GMODE, int CPS, int SPARSE>
 static hipError_t skinny_launch_t(const SkinnyArgs &d, int blocks, int lds, hipStream_t s) {
     // more than 64 KB of dynamic LDS must be allowed once per device
     static int allowed[64] = {0};
@@ -493,8 +552,11 @@ template <int NTT, int GMODE>
 static hipError_t skinny_launch_g(const SkinnyArgs &d, bool sparse, int blocks, int lds, hipStream_t s) {
     constexpr int C = sk_cps_bound(NTT);
     if (d.cps > C) return hipErrorInvalidValue;  // the kernel handles at most C chunks per slice
-    if (sparse) return skinny_launch_t<NTT, GMODE, C, true>(d, blocks, lds, s);
-    return skinny_launch_t<NTT, GMODE, C, false>(d, blocks, lds, s);
+    if (sparse) {
+        if (NTT == 1 && d.M <= 8) return skinny_launch_t<NTT, GMODE, C, (NTT == 1 ? 2 : 1)>(d, blocks, lds, s);
+        return skinny_launch_t<NTT, GMODE, C, 1>(d, blocks, lds, s);
+    }
+    return skinny_launch_t<NTT, GMODE, C, 0>(d, blocks, lds, s);
 }
 
 template <int NTT>
@@ -502,6 +564,9 @@ static hipError_t skinny_launch_n(const SkinnyArgs &d, int gmode, bool sparse, i
     switch (gmode) {
         case 0: return skinny_launch_g<NTT, 0>(d, sparse, blocks, lds, s);
         case 1: return skinny_launch_g<NTT, 1>(d, sparse, blocks, lds, s);
+        case 3:
+            if constexpr (NTT == 1) return skinny_launch_g<NTT, 3>(d, sparse, blocks, lds, s);
+            return hipErrorInvalidValue;
         default: return skinny_launch_g<NTT, 2>(d, sparse, blocks, lds, s);
     }
 }
@@ -553,7 +618,11 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     // pairs of group-128 scales are read as aligned 32-bit words when every
     // row starts on a pair (even group count, 4-byte aligned scales)
     const bool pairs = (a.ngroups & 1) == 0 && (reinterpret_cast<uintptr_t>(a.scales) & 3) == 0;
-    const int gmode = a.ngroups == 1 ? 0 : (d.gshift == 0 && pairs ? 1 : 2);
+    // full slices of 8 chunks with 16-byte scale vectors (GMODE 3)
+    // (one token tile: with two the pair loop would not fit the registers)
+    const bool full = sh.ntt == 1 && sh.cps == 8 && (int64_t)sh.S * 8 == a.K / 128 &&
+                      a.ngroups % 8 == 0 && (reinterpret_cast<uintptr_t>(a.scales) & 15) == 0;
+    const int gmode = a.ngroups == 1 ? 0 : (d.gshift != 0 ? 2 : (full ? 3 : (pairs ? 1 : 2)));
     const int blocks = ((sh.nblocks + 7) / 8) * 8 * sh.S;  // padded: see skinny_kernel
     hipError_t e;
     switch (sh.ntt) {
