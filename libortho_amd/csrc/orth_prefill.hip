@@ -487,8 +487,10 @@ __device__ __forceinline__ void pf_step(const PrefillArgs &a, const PfLane &L, i
     f16 *B_t = Bs0 + J * (PF_B_BYTES / 2), *B_1 = Bs0 + J1 * (PF_B_BYTES / 2), *B_2 = Bs0 + J2 * (PF_B_BYTES / 2);
     pf_store_a(L, ra[J1], As0 + ((t + 1) & 1) * (PF_A_BYTES / 2));
     pf_store_b(rb[J2], B_2);
-    if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_1, trash, canonical);
     pf_mfma(As0 + (t & 1) * (PF_A_BYTES / 2), B_t, wm, wn, acc);
+    // the fold's read-modify-write of stage t+1 waits for the LDS: after the
+    // MFMAs of step t are issued, not before them
+    if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_1, trash, canonical);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
 }
