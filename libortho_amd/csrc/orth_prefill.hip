@@ -466,11 +466,13 @@ __device__ __forceinline__ void pf_mfma(const f16 *As, const f16 *Bs, int wm, in
     }
 }
 
-// One pipeline step t (J = t mod 3, static): issue the loads of steps t+3
-// (activations, plan entries) and t+4 (weights); write step t+1's
-// activations, dequantise step t+2's weights and fold step t+1's plan
-// entries (its weights were written one step ago) while the MFMAs consume
-// step t's stages; one barrier.  Activations use two LDS stages, weights
+// One pipeline step t (J = t mod 3, static): the MFMAs consume step t's
+// stages first; then the loads of steps t+3 (activations, plan entries) and
+// t+4 (weights) are issued, step t+1's activations written, step t+2's
+// weights dequantised and step t+1's plan entries folded (its weights were
+// written one step ago); one barrier.  Issuing the MFMAs first lets them run
+// while the wave waits for the memory queue, older loads and the fold's LDS
+// read-modify-write.  Activations use two LDS stages, weights
 // three, so no write touches a stage being read.
 template <bool FOLD, int J>
 __device__ __forceinline__ void pf_step(const PrefillArgs &a, const PfLane &L, int t, int nk, int wm,
@@ -481,15 +483,13 @@ __device__ __forceinline__ void pf_step(const PrefillArgs &a, const PfLane &L, i
     // keep the scheduler from hoisting a later step's register work (which
     // would wait for younger loads) above this step's barrier
     __builtin_amdgcn_sched_barrier(0);
+    f16 *B_t = Bs0 + J * (PF_B_BYTES / 2), *B_1 = Bs0 + J1 * (PF_B_BYTES / 2), *B_2 = Bs0 + J2 * (PF_B_BYTES / 2);
+    pf_mfma(As0 + (t & 1) * (PF_A_BYTES / 2), B_t, wm, wn, acc);
     pf_load_a(a, L, min(t + 3, nk - 1), ra[J]);
     pf_load_b(a, L, min(t + 4, nk - 1), rb[J1]);
     if (FOLD) pf_load_e(a, offs, min(t + 3, nk - 1), re[J]);
-    f16 *B_t = Bs0 + J * (PF_B_BYTES / 2), *B_1 = Bs0 + J1 * (PF_B_BYTES / 2), *B_2 = Bs0 + J2 * (PF_B_BYTES / 2);
     pf_store_a(L, ra[J1], As0 + ((t + 1) & 1) * (PF_A_BYTES / 2));
     pf_store_b(rb[J2], B_2);
-    pf_mfma(As0 + (t & 1) * (PF_A_BYTES / 2), B_t, wm, wn, acc);
-    // the fold's read-modify-write of stage t+1 waits for the LDS: after the
-    // MFMAs of step t are issued, not before them
     if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_1, trash, canonical);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
