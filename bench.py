@@ -50,7 +50,7 @@ def log(*a):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--steps", type=int, default=2000)  # ~14 ms per replay: start-up < 0.3 %
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget for the CPU baseline sample")
@@ -351,9 +351,11 @@ def main():
                               "GB/s": round(b / (rr["ms_per_step"] * 1e-3) / 1e9, 1),
                               "frac_hbm": round(b / (rr["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
             log(f"  {secondary[-1]}")
-        for name, lay in (("4096->11008", layer), ("4096->4096 (c3)", W.config_layer("c3"))):
+        # 10-20 ms of launches per graph replay: with 20 launches the replay's
+        # start-up (clock ramp, first dispatch) added 10-15 % to the step
+        for name, lay, k in (("4096->11008", layer, 80), ("4096->4096 (c3)", W.config_layer("c3"), 100)):
             for a in (1.0, 0.0):
-                rr = time_workload(torch, lay, 2048, a, 20, 3, plan=True)
+                rr = time_workload(torch, lay, 2048, a, k, 3, plan=True)
                 f = W.algorithmic_flops(lay, 2048, a)
                 tf = f / (rr["ms_per_step"] * 1e-3) / 1e12
                 secondary.append({"workload": f"prefill {name} M=2048 alpha={a}",
