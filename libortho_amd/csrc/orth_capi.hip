@@ -25,7 +25,7 @@ namespace orth {
 hipError_t launch_general(const ForwardArgs &a, hipStream_t stream);
 hipError_t launch_dequant(const ForwardArgs &a, float *out, hipStream_t stream);
 bool decode_supported(const ForwardArgs &a);
-hipError_t launch_decode(const ForwardArgs &a, const void *plan, hipStream_t stream);
+hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream);
 bool prefill_supported(const ForwardArgs &a);
 bool plan_supported(const ForwardArgs &a);
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz);
@@ -286,7 +286,7 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
 
     hipError_t e = hipSuccess;
     if (kernel == KERNEL_DECODE) {
-        e = launch_decode(a, plan, stream);
+        e = launch_decode(a, plan, g_dev[dev].cus, stream);
     } else if (kernel == KERNEL_SKINNY) {
         const int cus = g_dev[dev].cus;
         const int64_t pbytes = skinny_workspace_bytes(a, cus);

@@ -77,6 +77,7 @@ struct DecodeArgs {
     int has_ortho;
     const uint32_t *rec;   // plan records, kRecHdrWords + dcap words per 16-row block
     int dcap;              // record entries per block (a multiple of 16), 0 without a plan
+    int deep;              // (host) fewer than two workgroups per CU: deeper weight prefetch
 };
 
 // Weights pass through LDS (whole-line loads, transposed on the way) for
@@ -91,10 +92,12 @@ constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 // exactly CPW chunks); 3 G = 128 with scales readable as aligned 32-bit
 // pairs; 2 any G = 128 * 2^j (one 16-bit load per chunk).
 // CPW: compile-time bound of the chunks per wave.  The weight loads of the
-// first PDP chunk pairs are issued at entry; with all CPW chunks valid the
-// main loop issues pair j + PDP as it takes pair j, so a wave never has more
-// than PDP + 1 pairs in flight and its vector-memory instructions do not
-// queue behind the weight streams of the whole CU before it can compute.
+// first PDP = min(PD, CPW / 2) chunk pairs are issued at entry; with all CPW
+// chunks valid the main loop issues pair j + PDP as it takes pair j, so a
+// wave never has more than PDP + 1 pairs in flight and its vector-memory
+// instructions do not queue behind the weight streams of the whole CU
+// before it can compute.  PD 1 when a CU holds two or more workgroups (c2:
+// 688 workgroups), 3 when it holds one (4096-row layers), 2 otherwise.
 // SPARSE: 0 no ortho term; 1 ortho term with the workgroup's CSR block
 // staged through LDS (16-byte aligned columns, nnz >= 4); 2 ortho term read
 // entry by entry in the epilogue; 3 / 4 / 5 the plan's record of the block
@@ -105,7 +108,7 @@ constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 // address: a load under a branch makes the compiler's wait-count insertion
 // fall back to waiting for all outstanding loads, which serialises the
 // kernel behind its own weight stream.
-template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE>
+template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, int PD>
 __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     constexpr int W = kDecodeW;
     constexpr int NT = kDecodeNT;
@@ -113,7 +116,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     constexpr int MI = MT < 4 ? MT : 4;        // live D rows per lane group (tokens 4g + i)
     constexpr bool GROUPED = GMODE != 0 && GMODE != 4;
     constexpr bool FULL = GMODE == 1 || GMODE == 4;  // every wave has CPW chunks
-    constexpr int PDP = CPW / 2 < 2 ? CPW / 2 : 2;  // weight pairs in flight ahead of the main loop
+    constexpr int PDP = CPW / 2 < PD ? CPW / 2 : PD;  // weight pairs in flight ahead of the main loop
     constexpr int PDC = 2 * PDP;                     // the same in chunks (direct loads)
     constexpr int XIT = (CPW * 16 + 63) / 64;  // 16-byte activation pieces per lane per token
     constexpr int ES = kDecodeESlots;
@@ -665,21 +668,32 @@ static int64_t decode_lds_layout(DecodeArgs &d, int mt, bool xlds, int cpw_bound
     return off;
 }
 
-template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE>
-static hipError_t launch_decode_k(const DecodeArgs &d, int64_t lds, hipStream_t stream) {
+template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, int PD>
+static hipError_t launch_decode_kp(const DecodeArgs &d, int64_t lds, hipStream_t stream) {
     // more than 64 KB of dynamic LDS must be allowed once per device
     static int allowed[64] = {0};
     int dev = 0;
     if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !allowed[dev]) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<MT, GMODE, XLDS, CPW, SPARSE>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecodeLdsMax);
         if (e != hipSuccess) return e;
         allowed[dev] = 1;
     }
     const unsigned blocks = (unsigned)((d.N + 15) / 16);
-    hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, SPARSE>), dim3(blocks), dim3(kDecodeNT),
+    hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD>), dim3(blocks), dim3(kDecodeNT),
                        (uint32_t)lds, stream, d);
     return hipGetLastError();
+}
+
+// Prefetch depth: full-width kernels (GMODE 1 and 4) by CU occupancy, the
+// others issue everything at entry past the first pairs anyway.
+template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE>
+static hipError_t launch_decode_k(const DecodeArgs &d, int64_t lds, hipStream_t stream) {
+    if constexpr (GMODE == 1 || GMODE == 4)
+        return d.deep ? launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 3>(d, lds, stream)
+                      : launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 1>(d, lds, stream);
+    else
+        return launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 2>(d, lds, stream);
 }
 
 template <int MT, int GMODE, bool XLDS, int CPW>
@@ -764,9 +778,11 @@ bool decode_supported(const ForwardArgs &a) {
 int64_t plan_rec_cap(int64_t N, int64_t nnz);           // orth_prefill.hip
 int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz);
 
-// plan: an ortho plan of at least plan_bytes_for(N, K, nnz) bytes, or null.
-hipError_t launch_decode(const ForwardArgs &a, const void *plan, hipStream_t stream) {
+// plan: an ortho plan of at least plan_bytes_for(N, K, nnz) bytes, or null;
+// cus: the device's compute units.
+hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream) {
     DecodeArgs d;
+    d.deep = (a.N + 15) / 16 < 2 * (int64_t)cus;
     d.q = a.q;
     d.scales = static_cast<const f16 *>(a.scales);
     d.ngroups = (int)a.ngroups;
