@@ -118,6 +118,11 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     constexpr bool FULL = GMODE == 1 || GMODE == 4;  // every wave has CPW chunks
     constexpr int PDP = CPW / 2 < PD ? CPW / 2 : PD;  // weight pairs in flight ahead of the main loop
     constexpr int PDC = 2 * PDP;                     // the same in chunks (direct loads)
+    // record kernels issue PDP more pairs after the record barrier, before
+    // the sparse sums, so the stream does not pause while those are formed;
+    // the main loop then runs PDM pairs ahead
+    constexpr int PDM = (SPARSE >= 3 && FULL) ? (2 * PDP < CPW / 2 ? 2 * PDP : CPW / 2) : PDP;
+    constexpr int PDMC = 2 * PDM;
     constexpr int XIT = (CPW * 16 + 63) / 64;  // 16-byte activation pieces per lane per token
     constexpr int ES = kDecodeESlots;
     // WT: the weights pass through LDS (see decode_wt)
@@ -340,6 +345,15 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
             if (slot < rwords) *reinterpret_cast<u32x4 *>(er + slot) = rv[r];
         }
         __syncthreads();  // all activations and the record are in LDS
+        if (FULL) {
+            if (WT) {
+#pragma unroll
+                for (int j = PDP; j < PDM; j++) load_pair(j);
+            } else {
+#pragma unroll
+                for (int p = PDC; p < PDMC; p++) load_chunk(p);
+            }
+        }
         // the record of another layer or block fails the tag: the rows are
         // then read from the CSR at the end
         rec_ok = er[0] == plan_rec_tag(a.N, K, a.nnz, a.dcap, blockIdx.x);
@@ -469,8 +483,8 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 } else {
                     w0 = wv[2 * j];
                     w1 = wv[2 * j + 1];
-                    if (2 * j + PDC < CPW) load_chunk(2 * j + PDC);
-                    if (2 * j + 1 + PDC < CPW) load_chunk(2 * j + 1 + PDC);
+                    if (2 * j + PDMC < CPW) load_chunk(2 * j + PDMC);
+                    if (2 * j + 1 + PDMC < CPW) load_chunk(2 * j + 1 + PDMC);
                 }
                 const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w};
                 const uint32_t u1[4] = {w1.x, w1.y, w1.z, w1.w};
@@ -497,7 +511,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                                                                 __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
                                                                 pb, 0, 0, 0);
                 }
-                if (WT && j + PDP < CPW / 2) load_pair(j + PDP);
+                if (WT && j + PDM < CPW / 2) load_pair(j + PDM);
                 chunk_done(pa, 2 * j);
                 chunk_done(pb, 2 * j + 1);
             }
@@ -519,12 +533,12 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                     if (WT) {
                         if ((p & 1) == 0) {
                             pair_to_lds(p >> 1);
-                            if (FULL && (p >> 1) + PDP < CPW / 2) load_pair((p >> 1) + PDP);
+                            if (FULL && (p >> 1) + PDM < CPW / 2) load_pair((p >> 1) + PDM);
                         }
                         wp = wt_read(p >> 1, p & 1);
                     } else {
                         wp = wv[p];
-                        if (FULL && p + PDC < CPW) load_chunk(p + PDC);
+                        if (FULL && p + PDMC < CPW) load_chunk(p + PDMC);
                     }
                     if (GROUPED) {
                         chunk_done(chunk_mfma(wp, p, f32x4{0.f, 0.f, 0.f, 0.f}), p);
