@@ -84,6 +84,20 @@ __device__ __forceinline__ int sext4(uint32_t nib) { return (int)(nib ^ 8u) - 8;
 // (0xffff outside [0, K)) | fp16 value bits << 16 (0xffff past nnz).
 constexpr int kRecHdrWords = 36;
 
+// Slice records (read by the mid-batch kernel, K % 1024 == 0): per 16-row
+// group g and 1024-column slice s, kSrecHdrWords header words then entries,
+// kSrecWords(N, K, nnz) words in all (256 or 512).  Header: [0] tag, [1] the
+// number of the cell's entries that did not fit (the kernel then reads the
+// CSR), [2 + r] row 16 g + r's entries as start | end << 16 (entry indices),
+// [18], [19] zero.  Entry: column - 1024 s | fp16 value bits << 16, rows in
+// order, each row's entries in CSR order; unused slots 0xffff.
+constexpr int kSrecHdrWords = 20;
+
+__host__ __device__ inline uint32_t plan_srec_tag(int64_t N, int64_t K, int64_t nnz, int words, int64_t g, int s) {
+    return 0x53524543u ^ (uint32_t)nnz ^ ((uint32_t)N * 0x9E3779B1u) ^ ((uint32_t)K << 13) ^
+           ((uint32_t)words * 0xC2B2AE3Du) ^ ((uint32_t)g * 0x85EBCA77u) ^ ((uint32_t)s * 0x27D4EB2Fu);
+}
+
 // Tag of block b's record: ties a record to the layer shape and its place,
 // so that a plan of another layer (or a stale stride) is not read as this one.
 __host__ __device__ inline uint32_t plan_rec_tag(int64_t N, int64_t K, int64_t nnz, int dcap, int64_t b) {

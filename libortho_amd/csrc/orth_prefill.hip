@@ -41,6 +41,10 @@ namespace orth {
 //                                         when outside [0, K)) | fp16 value bits << 16
 //                                         (0xffff past nnz); see orth_common.h.  dcap
 //                                         is in the header's pad[0].
+//   uint32 srecs[ceil(N/16)][K/1024][W]   (K % 1024 == 0, W = 256 or 512 words) per
+//                                         16-row group and 1024-column slice, the
+//                                         rows' entries of the slice packed: see
+//                                         orth_common.h.  W is in pad[1] (0: none).
 // Entries of one (block, step) are ordered by row then by CSR position.  The
 // chunk table locates a row's entries of columns [128 c0, 128 c1) in the CSR
 // itself when the row's columns ascend strictly (flag kPlanUnsorted clear).
@@ -49,7 +53,7 @@ namespace orth {
 // load); rows reaching past their block's record read the rest from the CSR.
 
 static const uint32_t kPlanMagic = 0x504f5254u;  // "TROP"
-static const uint32_t kPlanVersion = 3;
+static const uint32_t kPlanVersion = 4;
 static const int kPlanBN = 128;
 static const int kPlanBK = 64;
 static const uint32_t kPlanNonCanonical = 1u;  // duplicate or unsorted columns in a row
@@ -100,9 +104,26 @@ int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz) {
     return plan_chunks_at(N, K, nnz) + plan_chunks_bytes(N, K);
 }
 
+// Words per slice record: header plus the mean entry count of a (16-row,
+// 1024-column) cell plus four times (its square root + 1), in 256-word
+// units; 0 (no slice records) when K % 1024 != 0 or more than 512 are needed.
+int plan_srec_words(int64_t N, int64_t K, int64_t nnz) {
+    if (nnz <= 0 || N <= 0 || K % 1024 != 0) return 0;
+    const int64_t mean = (16 * 1024 * nnz + N * K - 1) / (N * K);
+    int64_t s = 0;
+    while ((s + 1) * (s + 1) <= mean) s++;
+    const int64_t need = kSrecHdrWords + mean + 4 * (s + 1);
+    const int64_t w = (need + 255) / 256 * 256;
+    return w <= 512 ? (int)w : 0;
+}
+
+int64_t plan_srec_at(int64_t N, int64_t K, int64_t nnz) {
+    return plan_rec_at(N, K, nnz) + ((N + 15) / 16) * (kRecHdrWords + plan_rec_cap(N, nnz)) * 4;
+}
+
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) {
     if (nnz <= 0) return 0;
-    return plan_rec_at(N, K, nnz) + ((N + 15) / 16) * (kRecHdrWords + plan_rec_cap(N, nnz)) * 4;
+    return plan_srec_at(N, K, nnz) + ((N + 15) / 16) * (K / 1024) * (int64_t)plan_srec_words(N, K, nnz) * 4;
 }
 
 // Largest K the plan builder's LDS counters take (int32 per (step, row)).
@@ -113,7 +134,7 @@ bool plan_supported(const ForwardArgs &a) {
 }
 
 __global__ void plan_init_kernel(PlanHeader *h, int nblocks, int nksteps, int64_t N, int64_t K,
-                                 int64_t nnz, int dcap) {
+                                 int64_t nnz, int dcap, int swords) {
     if (threadIdx.x == 0) {
         h->magic = kPlanMagic;
         h->version = kPlanVersion;
@@ -126,7 +147,8 @@ __global__ void plan_init_kernel(PlanHeader *h, int nblocks, int nksteps, int64_
         h->nnz = nnz;
         h->flags = 0;
         h->pad[0] = (uint32_t)dcap;
-        h->pad[1] = h->pad[2] = 0;
+        h->pad[1] = (uint32_t)swords;
+        h->pad[2] = 0;
     }
 }
 
@@ -272,6 +294,58 @@ __global__ void __launch_bounds__(256) plan_rec_kernel(ForwardArgs a, uint32_t *
     }
 }
 
+// One workgroup of 64 per (16-row group, slice): thread r < 16 counts its
+// row's entries of the slice, thread 0 lays out the rows, then each thread
+// writes its row's entries in CSR order (those past the record are counted
+// in header word 1).
+__global__ void __launch_bounds__(64) plan_srec_kernel(ForwardArgs a, uint32_t *srec, int words, int nslices) {
+    __shared__ int32_t cnt[16], start[17];
+    const int64_t g = blockIdx.x / nslices;
+    const int s = (int)(blockIdx.x - g * nslices);
+    const int t = threadIdx.x;
+    uint32_t *rec = srec + (g * nslices + s) * (int64_t)words;
+    const int cap = words - kSrecHdrWords;
+    const int32_t c0 = s * 1024;
+    int32_t rs = 0, re = 0;
+    const int64_t n = g * 16 + t;
+    if (t < 16) {
+        if (n < a.N) csr_row_range(a.row_ptr, n, a.nnz, rs, re);
+        int32_t k = 0;
+        for (int32_t j = rs; j < re; j++) {
+            const int32_t c = a.col[j];
+            k += (c >= c0 && c < c0 + 1024) ? 1 : 0;
+        }
+        cnt[t] = k;
+    }
+    __syncthreads();
+    if (t == 0) {
+        int32_t run = 0;
+        for (int r = 0; r < 16; r++) {
+            start[r] = run;
+            run += cnt[r];
+        }
+        start[16] = run;
+        rec[0] = plan_srec_tag(a.N, a.K, a.nnz, words, g, s);
+        rec[1] = (uint32_t)(run > cap ? run - cap : 0);
+        rec[18] = rec[19] = 0u;
+    }
+    __syncthreads();
+    for (int i = t; i < cap; i += 64) rec[kSrecHdrWords + i] = 0xffffu;
+    __syncthreads();
+    if (t < 16) {
+        const int32_t b = min(start[t], cap), e = min(start[t + 1], cap);
+        rec[2 + t] = (uint32_t)b | ((uint32_t)e << 16);
+        int32_t w = start[t];
+        for (int32_t j = rs; j < re; j++) {
+            const int32_t c = a.col[j];
+            if (c >= c0 && c < c0 + 1024) {
+                if (w < cap) rec[kSrecHdrWords + w] = (uint32_t)(c - c0) | (value_bits_f16(a.vals, a.val_dtype, j) << 16);
+                w++;
+            }
+        }
+    }
+}
+
 hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t stream) {
     const int nblocks = (int)((a.N + kPlanBN - 1) / kPlanBN);
     const int nksteps = (int)(a.K / kPlanBK);
@@ -280,8 +354,9 @@ hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t strea
     uint32_t *entries = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(offsets) +
                                                      plan_offsets_bytes(a.N, a.K));
     const int dcap = (int)plan_rec_cap(a.N, a.nnz);
+    const int swords = plan_srec_words(a.N, a.K, a.nnz);
     hipLaunchKernelGGL(plan_init_kernel, dim3(1), dim3(64), 0, stream, h, nblocks, nksteps, a.N,
-                       a.K, a.nnz, dcap);
+                       a.K, a.nnz, dcap, swords);
     const size_t lds = ((size_t)nksteps * kPlanBN + 256) * sizeof(int32_t);
     uint16_t *chunks = plan_chunks_bytes(a.N, a.K)
                            ? reinterpret_cast<uint16_t *>(static_cast<char *>(plan) + plan_chunks_at(a.N, a.K, a.nnz))
@@ -290,6 +365,12 @@ hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t strea
                        entries, chunks, nksteps);
     uint32_t *rec = reinterpret_cast<uint32_t *>(static_cast<char *>(plan) + plan_rec_at(a.N, a.K, a.nnz));
     hipLaunchKernelGGL(plan_rec_kernel, dim3((unsigned)((a.N + 15) / 16)), dim3(256), 0, stream, a, rec, dcap);
+    if (swords > 0) {
+        const int nslices = (int)(a.K / 1024);
+        uint32_t *srec = reinterpret_cast<uint32_t *>(static_cast<char *>(plan) + plan_srec_at(a.N, a.K, a.nnz));
+        hipLaunchKernelGGL(plan_srec_kernel, dim3((unsigned)(((a.N + 15) / 16) * nslices)), dim3(64), 0, stream, a,
+                           srec, swords, nslices);
+    }
     return hipGetLastError();
 }
 

@@ -43,6 +43,8 @@ namespace orth {
 
 int64_t plan_chunks_at(int64_t N, int64_t K, int64_t nnz);  // orth_prefill.hip
 int64_t plan_chunks_bytes(int64_t N, int64_t K);
+int plan_srec_words(int64_t N, int64_t K, int64_t nnz);
+int64_t plan_srec_at(int64_t N, int64_t K, int64_t nnz);
 
 constexpr int kSkNT = 512;            // 8 waves
 constexpr int kSkRows = 128;          // rows per workgroup (= ortho plan block)
@@ -55,7 +57,7 @@ __device__ __forceinline__ int quad_bcast(int x) {
     return __builtin_amdgcn_update_dpp(0, x, S | (S << 2) | (S << 4) | (S << 6), 0xf, 0xf, false);
 }
 constexpr uint32_t kSkPlanMagic = 0x504f5254u;
-constexpr uint32_t kSkPlanVersion = 3;
+constexpr uint32_t kSkPlanVersion = 4;
 constexpr uint32_t kSkPlanUnsorted = 4u;  // plan flag: the chunk table does not locate ranges
 
 // Chunks per slice the kernel of ntt token tiles is built for: even (group
@@ -86,6 +88,10 @@ struct SkinnyArgs {
     int lds_cr, lds_xs, lds_sp;  // byte offsets of the LDS regions
     float alpha;
     float *part;         // [S][M][N] partials (S > 1)
+    const uint32_t *srec;  // plan slice records (SPK >= 3), swords words each
+    int swords;
+    int nslices;         // K / 1024
+    int lds_sr;          // SPK >= 3: per-wave record regions
 };
 
 // GMODE: 0 per-row scale (G == K); 1 G = 128, scales read as aligned pairs;
@@ -95,15 +101,21 @@ struct SkinnyArgs {
 // and the weight loads run four chunks ahead instead of all at entry.
 // NTT: 16-token tiles.  CPS: chunk bound per slice.  SPK: 0 no ortho term,
 // 1 ortho term, 2 ortho term for at most 8 tokens (one tile: the four lanes
-// of a row gather two tokens each, not four).
+// of a row gather two tokens each, not four); 3 .. 6 (one tile, GMODE 3) the
+// same from the plan's slice records instead of the CSR: 3 / 4 records of
+// 256 words (4: at most 8 tokens), 5 / 6 of 512 words.
 template <int NTT, int GMODE, int CPS, int SPK>
 __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT <= 2 ? 4 : 2))) skinny_kernel(SkinnyArgs a) {
     constexpr bool SPARSE = SPK != 0;
+    constexpr bool SREC = SPK >= 3;                  // slice records: each wave reads its 16 rows' record
+    constexpr bool HALF = SPK == 2 || SPK == 4 || SPK == 6;
+    constexpr int RQ = SPK >= 5 ? 2 : 1;             // record loads per lane (256 words each per wave)
     constexpr int MP = NTT * 16;                     // padded tokens
     constexpr int XP = (MP * CPS * 16 + kSkNT - 1) / kSkNT;  // 16-byte pieces per thread
     constexpr int SW = (CPS + 7) / 8;
     constexpr bool GROUPED = GMODE != 0;
     constexpr bool FULL = GMODE == 3;  // every slice holds exactly CPS chunks
+    static_assert(!SREC || (FULL && NTT == 1), "slice records: one token tile, 8-chunk slices");
     static_assert(!FULL || CPS == 8, "full slices are one scale vector");
     constexpr int PDC = FULL ? 4 : CPS;  // weight loads issued at entry
     // QUAD: four consecutive lanes per row in the sparse term (one token tile)
@@ -156,7 +168,18 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
     const int64_t sn = min(n0 + sr, a.N - 1);
     int32_t rp0 = 0, rp1 = 0, hw = 0;
     uint32_t ck0 = 0, ck1 = 0;
-    if (SPARSE) {
+    // SREC: this wave's record (rows 16 w .. 16 w + 15 of the block, the
+    // slice's columns), at an address that needs no other load
+    const int64_t g16 = min((int64_t)blk * 8 + wave, (a.N + 15) / 16 - 1);
+    const int sl = kc0 >> 3;
+    u32x4 rq[RQ];
+    if (SREC) {
+        const uint32_t *rb = a.srec + (g16 * a.nslices + sl) * (int64_t)a.swords;
+#pragma unroll
+        for (int i = 0; i < RQ; i++)
+            rq[i] = *reinterpret_cast<const u32x4 *>(rb + min(4 * (lane + 64 * i), a.swords - 4));
+    }
+    if (SPARSE && !SREC) {
         rp0 = a.row_ptr[sn];
         rp1 = a.row_ptr[sn + 1];
         const bool tab = a.chunks != nullptr;
@@ -211,6 +234,14 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
             if ((p & 15) == 0) cr[c * MP + m] = b;
         }
     }
+    if (SREC) {
+        uint32_t *wr = reinterpret_cast<uint32_t *>(smem + a.lds_sr) + wave * a.swords;
+#pragma unroll
+        for (int i = 0; i < RQ; i++) {
+            const int o = 4 * (lane + 64 * i);
+            if (o < a.swords) *reinterpret_cast<u32x4 *>(wr + o) = rq[i];
+        }
+    }
     __syncthreads();
 
     // ---- the row's CSR range in the slice.  With a matching plan whose
@@ -232,7 +263,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
             v[u] = __builtin_bit_cast(uint16_t, a.vals[j]);
         }
     };
-    if (SPARSE) {
+    if (SPARSE && !SREC) {
         auto word = [&](int l) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane(hw, l); };
         auto dword = [&](int l) -> int64_t { return (int64_t)(word(l) | ((uint64_t)word(l + 1) << 32)); };
         const bool fast = (a.phdr != nullptr) & (a.chunks != nullptr) & (word(0) == kSkPlanMagic) &
@@ -341,7 +372,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
     // ---- sparse term, in batches of eight entries; columns outside the
     //      slice are skipped.  Token t of the lane: QUAD tg + 4 t, else
     //      16 (t / 4) + 4 g + t % 4 (the MFMA output's tokens).
-    constexpr int TQ = QUAD ? (SPK == 2 ? 2 : MP / 4) : NTT * 4;  // tokens per lane
+    constexpr int TQ = QUAD ? (HALF ? 2 : MP / 4) : NTT * 4;  // tokens per lane
     float sacc[SPARSE ? TQ : 1];
     if (SPARSE) {
 #pragma unroll
@@ -378,15 +409,51 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
                 }
             }
         };
-        fma_batch(lo, ecol, eval);
-        // the lanes of a row take the same branches and trip counts
-        if (lo + kSkEB < hi) fma_batch(lo + kSkEB, ecol2, eval2);
-        // more entries (dense rows, or a whole row without the chunk table)
-        for (int32_t j0 = lo + 2 * kSkEB; j0 < hi; j0 += kSkEB) {
-            int32_t c2[EL];
-            uint32_t v2[EL];
-            load_batch(j0, c2, v2);
-            fma_batch(j0, c2, v2);
+        if constexpr (SREC) {
+            const uint32_t *wr = reinterpret_cast<const uint32_t *>(smem + a.lds_sr) + wave * a.swords;
+            // (uniform per wave) the record of this group and slice, all its
+            // entries inside: else the row's CSR range, filtered by column
+            const bool ok = (wr[0] == plan_srec_tag(a.N, K, a.nnz, a.swords, g16, sl)) & (wr[1] == 0u);
+            if (ok) {
+                const uint32_t h = wr[2 + ((tid >> 2) & 15)];
+                lo = (int32_t)(h & 0xffffu);
+                hi = (int32_t)(h >> 16);
+                if (n0 + sr >= a.N) hi = lo;
+                const uint32_t *ent = wr + kSrecHdrWords;
+                for (int32_t j0 = lo; j0 < hi; j0 += kSkEB) {
+                    int32_t c2[EL];
+                    uint32_t v2[EL];
+#pragma unroll
+                    for (int u = 0; u < EL; u++) {
+                        const uint32_t w = ent[min(j0 + tg + 4 * u, hi - 1)];
+                        c2[u] = (int32_t)(w & 0xffffu) + c0;
+                        v2[u] = w >> 16;
+                    }
+                    fma_batch(j0, c2, v2);
+                }
+            } else {
+                int32_t rs, re;
+                csr_row_range(a.row_ptr, sn, a.nnz, rs, re);
+                lo = rs;
+                hi = (n0 + sr < a.N) ? re : rs;
+                for (int32_t j0 = lo; j0 < hi; j0 += kSkEB) {
+                    int32_t c2[EL];
+                    uint32_t v2[EL];
+                    load_batch(j0, c2, v2);
+                    fma_batch(j0, c2, v2);
+                }
+            }
+        } else {
+            fma_batch(lo, ecol, eval);
+            // the lanes of a row take the same branches and trip counts
+            if (lo + kSkEB < hi) fma_batch(lo + kSkEB, ecol2, eval2);
+            // more entries (dense rows, or a whole row without the chunk table)
+            for (int32_t j0 = lo + 2 * kSkEB; j0 < hi; j0 += kSkEB) {
+                int32_t c2[EL];
+                uint32_t v2[EL];
+                load_batch(j0, c2, v2);
+                fma_batch(j0, c2, v2);
+            }
         }
         if (QUAD) {
 #pragma unroll
@@ -553,6 +620,15 @@ static hipError_t skinny_launch_g(const SkinnyArgs &d, bool sparse, int blocks, 
     constexpr int C = sk_cps_bound(NTT);
     if (d.cps > C) return hipErrorInvalidValue;  // the kernel handles at most C chunks per slice
     if (sparse) {
+        if constexpr (NTT == 1 && GMODE == 3) {
+            if (d.swords > 0) {  // slice records (launch_skinny checked the shape)
+                const bool half = d.M <= 8;
+                if (d.swords == 256) return half ? skinny_launch_t<NTT, GMODE, C, 4>(d, blocks, lds, s)
+                                                 : skinny_launch_t<NTT, GMODE, C, 3>(d, blocks, lds, s);
+                return half ? skinny_launch_t<NTT, GMODE, C, 6>(d, blocks, lds, s)
+                            : skinny_launch_t<NTT, GMODE, C, 5>(d, blocks, lds, s);
+            }
+        }
         if (NTT == 1 && d.M <= 8) return skinny_launch_t<NTT, GMODE, C, (NTT == 1 ? 2 : 1)>(d, blocks, lds, s);
         return skinny_launch_t<NTT, GMODE, C, 1>(d, blocks, lds, s);
     }
@@ -623,13 +699,26 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     const bool full = sh.ntt == 1 && sh.cps == 8 && (int64_t)sh.S * 8 == a.K / 128 &&
                       a.ngroups % 8 == 0 && (reinterpret_cast<uintptr_t>(a.scales) & 15) == 0;
     const int gmode = a.ngroups == 1 ? 0 : (d.gshift != 0 ? 2 : (full ? 3 : (pairs ? 1 : 2)));
+    // the plan's slice records (one token tile, full 8-chunk slices): each
+    // wave stages its record in its own LDS region
+    d.srec = nullptr;
+    d.swords = 0;
+    d.nslices = (int)(a.K / 1024);
+    d.lds_sr = sh.lds_bytes;
+    int lds = sh.lds_bytes;
+    const int sw = plan ? plan_srec_words(a.N, a.K, a.nnz) : 0;
+    if (sparse && gmode == 3 && sh.ntt == 1 && sh.cps == 8 && sw > 0 && lds + 8 * sw * 4 <= 150 * 1024) {
+        d.srec = reinterpret_cast<const uint32_t *>(static_cast<const char *>(plan) + plan_srec_at(a.N, a.K, a.nnz));
+        d.swords = sw;
+        lds += 8 * sw * 4;
+    }
     const int blocks = ((sh.nblocks + 7) / 8) * 8 * sh.S;  // padded: see skinny_kernel
     hipError_t e;
     switch (sh.ntt) {
-        case 1: e = skinny_launch_n<1>(d, gmode, sparse, blocks, sh.lds_bytes, stream); break;
-        case 2: e = skinny_launch_n<2>(d, gmode, sparse, blocks, sh.lds_bytes, stream); break;
-        case 3: e = skinny_launch_n<3>(d, gmode, sparse, blocks, sh.lds_bytes, stream); break;
-        default: e = skinny_launch_n<4>(d, gmode, sparse, blocks, sh.lds_bytes, stream); break;
+        case 1: e = skinny_launch_n<1>(d, gmode, sparse, blocks, lds, stream); break;
+        case 2: e = skinny_launch_n<2>(d, gmode, sparse, blocks, lds, stream); break;
+        case 3: e = skinny_launch_n<3>(d, gmode, sparse, blocks, lds, stream); break;
+        default: e = skinny_launch_n<4>(d, gmode, sparse, blocks, lds, stream); break;
     }
     if (e != hipSuccess || sh.S == 1) return e;
     const int vec4 = (a.N % 4 == 0) ? 1 : 0;

@@ -152,6 +152,16 @@ def rec_cap(N, nnz):
     return min(4048, (mean + 4 * (math.isqrt(mean) + 1) + 15) // 16 * 16)
 
 
+def srec_words(N, K, nnz):
+    # mid-batch slice records: header + mean entries of a (16-row, 1024-col)
+    # cell + 4 (isqrt(mean) + 1), in 256-word units, at most 512 (else none)
+    if K % 1024:
+        return 0
+    mean = -(-16 * 1024 * nnz // (N * K))
+    w = -(-(20 + mean + 4 * (math.isqrt(mean) + 1)) // 256) * 256
+    return w if w <= 512 else 0
+
+
 def test_plan_size(L):
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(nnz=0))) == 0
     n = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4096, N=4096, nnz=100)))
@@ -159,7 +169,9 @@ def test_plan_size(L):
     chunks = (4096 * (4096 // 128 + 1) * 2 + 15) // 16 * 16  # uint16 [N][K/128 + 1]
     records = (4096 // 16) * (36 + rec_cap(4096, 100)) * 4   # uint32 [N/16][36 + dcap]
     assert rec_cap(4096, 100) == 16
-    assert n == (64 + offsets + 400 + 15) // 16 * 16 + chunks + records
+    srecs = (4096 // 16) * (4096 // 1024) * srec_words(4096, 4096, 100) * 4
+    assert srec_words(4096, 4096, 100) == 256
+    assert n == (64 + offsets + 400 + 15) // 16 * 16 + chunks + records + srecs
     # K % 128 != 0: no chunk table; a ragged last row block still has a record
     n64 = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4160, N=4100, nnz=100)))
     assert n64 == (64 + ((4100 + 127) // 128) * (4160 // 64 + 1) * 4 + 400 + 15) // 16 * 16 + \
@@ -167,6 +179,10 @@ def test_plan_size(L):
     # c2 (1 % of 4096 x 11008): 656 entries per block on average -> 768
     assert rec_cap(11008, 450888) == 768
     assert rec_cap(64, 64 * 4096) == 4048  # capped
+    # c2: 164 entries per (16-row, 1024-column) cell -> 256 words; 2 % -> 512
+    assert srec_words(11008, 4096, 450888) == 256
+    assert srec_words(4096, 4096, 335544) == 512
+    assert srec_words(4096, 4096, 4096 * 4096 // 10) == 0  # 10 %: the CSR path
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4000, nnz=5))) < 0  # K % 64 != 0
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4095))) == -_lib.ERR_INVALID_ARGUMENT
 

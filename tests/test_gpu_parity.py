@@ -317,6 +317,36 @@ def test_skinny_chunk_table_with_columns_outside_k(oracle_mod):
         assert_close(y, oracle_y(oracle_mod, lay, x, 1.0), what=f"outside columns M={M}")
 
 
+@pytest.mark.parametrize("M", [6, 16])
+def test_skinny_slice_records_match_the_csr_path(oracle_mod, M):
+    # K % 1024 == 0, one token tile: the planned call reads the plan's slice
+    # records; rows 5 and 77 hold more entries than a record cell, so their
+    # cells fall back to the CSR.  The same entries are summed in the same
+    # order as the unplanned mid-batch call (which filters each row's CSR).
+    lay = skewed_rows_layer(2048, 384, {5, 77}, 900, 3300)
+    x = W.make_x(M, lay.K, 3310 + M)
+    y_rec, k1 = run(lay, x, 1.0, plan=True)
+    y_csr, k2 = run(lay, x, 1.0, policy="skinny", plan="auto")
+    assert k1 == k2 == "skinny"
+    assert np.array_equal(y_rec, y_csr)
+    assert_close(y_rec, oracle_y(oracle_mod, lay, x, 1.0), what=f"slice records M={M}")
+
+
+def test_skinny_slice_records_of_another_layer(oracle_mod):
+    big = W.make_layer(2048, 2048, 128, 0.03, seed=140)
+    lay = W.make_layer(2048, 1024, 128, 0.01, seed=141)
+    db, d = W.to_device(big), W.to_device(lay)
+    plan = _C_ops.build_plan(db["q"], db["scales"], db["vals"], db["col"], db["row_ptr"], big.K)
+    for M in (8, 12):
+        x = W.make_x(M, lay.K, 142 + M)
+        xt = torch.from_numpy(x).cuda()
+        y = torch.full((M, lay.N), float("nan"), dtype=torch.float16, device="cuda")
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], xt, y, 1.0, plan)
+        assert _C_ops.last_kernel() == "skinny"
+        torch.cuda.synchronize()
+        assert_close(y.float().cpu().numpy(), oracle_y(oracle_mod, lay, x, 1.0), what=f"foreign slice records M={M}")
+
+
 def test_skinny_workspace_reuse_and_determinism(oracle_mod, c2):
     # the split-K counters reset themselves; the workspace grows with M
     outs = {}
