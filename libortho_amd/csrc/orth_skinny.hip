@@ -29,6 +29,11 @@
 //    each lane takes the row and tokens of its own MFMA output and reads the
 //    row's entries itself.  Sums are formed in CSR order: the result does not
 //    depend on scheduling.
+//  * With the plan's slice records (one token tile, 8-chunk slices,
+//    K % 1024 == 0) each wave instead loads its 16 rows' record of the slice
+//    at entry (packed column | value words at an address that needs no other
+//    load), stages it in its own LDS region, and forms the sums before the
+//    dense term, after issuing the rest of its weight loads.
 //  * When the row blocks alone cannot fill the GPU, K is split over S
 //    workgroups.  Each writes its FP32 partial (ortho term included) to a
 //    workspace and a second kernel adds the S partials in slice order and
@@ -277,6 +282,88 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
         load_batch(lo + EB, ecol2, eval2);
     }
 
+    // ---- SREC: the sparse sums from the record, before the dense term:
+    //      the remaining weight loads are issued first, so the stream does
+    //      not pause while the sums are formed
+    constexpr int TQ = QUAD ? (HALF ? 2 : MP / 4) : NTT * 4;  // tokens per lane
+    float sacc_e[SREC ? TQ : 1];
+    if constexpr (SREC) {
+#pragma unroll
+        for (int p = PDC; p < CPS; p++) load_chunk(p);
+    }
+    if constexpr (SREC) {
+#pragma unroll
+        for (int t = 0; t < TQ; t++) sacc_e[t] = 0.f;
+        const int32_t c0 = kc0 * 128, cw = nci * 128;
+        const int xstride = a.xstride;
+        auto fma_batch = [&](int32_t j0, const int32_t (&c)[EL], const uint32_t (&v)[EL]) {
+#pragma unroll
+            for (int e = 0; e < kSkEB; e++) {
+                int32_t ce;
+                uint32_t ve;
+                if (QUAD) {  // entry j0 + e sits in lane e % 4 of the quad, slot e / 4
+                    const int slot = e >> 2;
+                    switch (e & 3) {
+                        case 0: ce = quad_bcast<0>(c[slot]); ve = (uint32_t)quad_bcast<0>((int)v[slot]); break;
+                        case 1: ce = quad_bcast<1>(c[slot]); ve = (uint32_t)quad_bcast<1>((int)v[slot]); break;
+                        case 2: ce = quad_bcast<2>(c[slot]); ve = (uint32_t)quad_bcast<2>((int)v[slot]); break;
+                        default: ce = quad_bcast<3>(c[slot]); ve = (uint32_t)quad_bcast<3>((int)v[slot]); break;
+                    }
+                } else {
+                    ce = c[e % EL];
+                    ve = v[e % EL];
+                }
+                const int32_t cl = ce - c0;
+                const bool ok = (j0 + e < hi) & (cl >= 0) & (cl < cw);
+                const int cc = ok ? cl : 0;
+                const float val = (float)__builtin_bit_cast(f16, (uint16_t)(ve & 0xffffu));
+                const int xi = (cc & ~7) | interleaved_pos(cc & 7);
+#pragma unroll
+                for (int t = 0; t < TQ; t++) {
+                    const int m = QUAD ? tg + 4 * t : 16 * (t >> 2) + 4 * g + (t & 3);
+                    const float pr = val * (float)xs[m * xstride + xi];
+                    sacc_e[t] += ok ? pr : 0.f;
+                }
+            }
+        };
+        const uint32_t *wr = reinterpret_cast<const uint32_t *>(smem + a.lds_sr) + wave * a.swords;
+        // (uniform per wave) the record of this group and slice, all its
+        // entries inside: else the row's CSR range, filtered by column
+        const bool ok = (wr[0] == plan_srec_tag(a.N, K, a.nnz, a.swords, g16, sl)) & (wr[1] == 0u);
+        if (ok) {
+            const uint32_t h = wr[2 + ((tid >> 2) & 15)];
+            lo = (int32_t)(h & 0xffffu);
+            hi = (int32_t)(h >> 16);
+            if (n0 + sr >= a.N) hi = lo;
+            const uint32_t *ent = wr + kSrecHdrWords;
+            for (int32_t j0 = lo; j0 < hi; j0 += kSkEB) {
+                int32_t c2[EL];
+                uint32_t v2[EL];
+#pragma unroll
+                for (int u = 0; u < EL; u++) {
+                    const uint32_t w = ent[min(j0 + tg + 4 * u, hi - 1)];
+                    c2[u] = (int32_t)(w & 0xffffu) + c0;
+                    v2[u] = w >> 16;
+                }
+                fma_batch(j0, c2, v2);
+            }
+        } else {
+            int32_t rs, re;
+            csr_row_range(a.row_ptr, sn, a.nnz, rs, re);
+            lo = rs;
+            hi = (n0 + sr < a.N) ? re : rs;
+            for (int32_t j0 = lo; j0 < hi; j0 += kSkEB) {
+                int32_t c2[EL];
+                uint32_t v2[EL];
+                load_batch(j0, c2, v2);
+                fma_batch(j0, c2, v2);
+            }
+        }
+        if (QUAD) {
+#pragma unroll
+            for (int t = 0; t < TQ; t++) sp[sr * MP + tg + 4 * t] = sacc_e[t];
+        }
+    }
     // ---- dense term: wave w, rows 16 w + nl, token tiles tt
     f32x4 acc[NTT];
     float bias_acc[NTT][4];
@@ -299,8 +386,8 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
                     int4x8_to_f16_biased(w1[j], bq1[j]);
                 }
             }
-            if (p + PDC < CPS) load_chunk(p + PDC);
-            if (p + 1 + PDC < CPS) load_chunk(p + 1 + PDC);
+            if (!SREC && p + PDC < CPS) load_chunk(p + PDC);
+            if (!SREC && p + 1 + PDC < CPS) load_chunk(p + 1 + PDC);
             const uint32_t s2 = sv[p >> 1];  // the scales of chunks p, p + 1
             const float s0 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 & 0xffffu));
             const float s1 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 >> 16));
@@ -372,9 +459,8 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
     // ---- sparse term, in batches of eight entries; columns outside the
     //      slice are skipped.  Token t of the lane: QUAD tg + 4 t, else
     //      16 (t / 4) + 4 g + t % 4 (the MFMA output's tokens).
-    constexpr int TQ = QUAD ? (HALF ? 2 : MP / 4) : NTT * 4;  // tokens per lane
-    float sacc[SPARSE ? TQ : 1];
-    if (SPARSE) {
+    float sacc[SPARSE && !SREC ? TQ : 1];
+    if constexpr (SPARSE && !SREC) {
 #pragma unroll
         for (int t = 0; t < TQ; t++) sacc[t] = 0.f;
         const int32_t c0 = kc0 * 128, cw = nci * 128;
@@ -409,51 +495,15 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
                 }
             }
         };
-        if constexpr (SREC) {
-            const uint32_t *wr = reinterpret_cast<const uint32_t *>(smem + a.lds_sr) + wave * a.swords;
-            // (uniform per wave) the record of this group and slice, all its
-            // entries inside: else the row's CSR range, filtered by column
-            const bool ok = (wr[0] == plan_srec_tag(a.N, K, a.nnz, a.swords, g16, sl)) & (wr[1] == 0u);
-            if (ok) {
-                const uint32_t h = wr[2 + ((tid >> 2) & 15)];
-                lo = (int32_t)(h & 0xffffu);
-                hi = (int32_t)(h >> 16);
-                if (n0 + sr >= a.N) hi = lo;
-                const uint32_t *ent = wr + kSrecHdrWords;
-                for (int32_t j0 = lo; j0 < hi; j0 += kSkEB) {
-                    int32_t c2[EL];
-                    uint32_t v2[EL];
-#pragma unroll
-                    for (int u = 0; u < EL; u++) {
-                        const uint32_t w = ent[min(j0 + tg + 4 * u, hi - 1)];
-                        c2[u] = (int32_t)(w & 0xffffu) + c0;
-                        v2[u] = w >> 16;
-                    }
-                    fma_batch(j0, c2, v2);
-                }
-            } else {
-                int32_t rs, re;
-                csr_row_range(a.row_ptr, sn, a.nnz, rs, re);
-                lo = rs;
-                hi = (n0 + sr < a.N) ? re : rs;
-                for (int32_t j0 = lo; j0 < hi; j0 += kSkEB) {
-                    int32_t c2[EL];
-                    uint32_t v2[EL];
-                    load_batch(j0, c2, v2);
-                    fma_batch(j0, c2, v2);
-                }
-            }
-        } else {
-            fma_batch(lo, ecol, eval);
-            // the lanes of a row take the same branches and trip counts
-            if (lo + kSkEB < hi) fma_batch(lo + kSkEB, ecol2, eval2);
-            // more entries (dense rows, or a whole row without the chunk table)
-            for (int32_t j0 = lo + 2 * kSkEB; j0 < hi; j0 += kSkEB) {
-                int32_t c2[EL];
-                uint32_t v2[EL];
-                load_batch(j0, c2, v2);
-                fma_batch(j0, c2, v2);
-            }
+        fma_batch(lo, ecol, eval);
+        // the lanes of a row take the same branches and trip counts
+        if (lo + kSkEB < hi) fma_batch(lo + kSkEB, ecol2, eval2);
+        // more entries (dense rows, or a whole row without the chunk table)
+        for (int32_t j0 = lo + 2 * kSkEB; j0 < hi; j0 += kSkEB) {
+            int32_t c2[EL];
+            uint32_t v2[EL];
+            load_batch(j0, c2, v2);
+            fma_batch(j0, c2, v2);
         }
         if (QUAD) {
 #pragma unroll
