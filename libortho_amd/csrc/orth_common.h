@@ -74,37 +74,36 @@ __device__ __forceinline__ void store_from_f32(void *p, int dtype, int64_t i, fl
 // Sign-extend a 4-bit two's complement nibble.
 __device__ __forceinline__ int sext4(uint32_t nib) { return (int)(nib ^ 8u) - 8; }
 
+// Ortho plan cell records (built in orth_prefill.hip): for a 16-row group g
+// and a column cell c (the decode kernel's K quarters, the mid-batch
+// kernel's 1024-column slices), `words` words at an address that needs no
+// other load.  Header: [0] tag, [1] the number of the cell's entries that
+// did not fit (the kernel then reads the CSR), [2 + r] row 16 g + r's
+// entries as start | end << 16 (entry indices), [18], [19] zero.  Entries
+// from word 20: column - the cell's first column | fp16 value bits << 16,
+// rows in order, each row's entries in CSR order; unused slots 0xffff.
+constexpr int kCellHdrWords = 20;
+constexpr uint32_t kCellQuarter = 0x51524543u;  // decode K quarters
+constexpr uint32_t kCellSlice = 0x53524543u;    // mid-batch 1024-column slices
+
+// Tag of a cell record: ties it to its kind, the layer shape, the record
+// size and its place, so that a plan of another layer is not read as this one.
+__host__ __device__ inline uint32_t plan_cell_tag(uint32_t kind, int64_t N, int64_t K, int64_t nnz, int words,
+                                                  int64_t g, int c) {
+    return kind ^ (uint32_t)nnz ^ ((uint32_t)N * 0x9E3779B1u) ^ ((uint32_t)K << 13) ^
+           ((uint32_t)words * 0xC2B2AE3Du) ^ ((uint32_t)g * 0x85EBCA77u) ^ ((uint32_t)c * 0x27D4EB2Fu);
+}
+
+// Chunks (128 columns) per wave of the decode kernel: the K quarter of wave
+// w is chunks [w c, min((w + 1) c, K / 128)), c even.
+__host__ __device__ inline int decode_chunks_per_wave(int64_t K) {
+    const int64_t nchunks = K / 128;
+    const int64_t c = (nchunks + 3) / 4;
+    return (int)((c + 1) & ~int64_t(1));
+}
+
 // CSR row range [rs, re), clamped into [0, nnz] so a malformed row_ptr can
 // never address outside the index arrays.
-// Ortho plan decode records (built in orth_prefill.hip, read by the decode
-// kernel): per 16-row block, kRecHdrWords header words then dcap entries.
-// Header: [0] tag, [1] e0 = row_ptr[16 b] clamped to [0, nnz], [2 + r] and
-// [18 + r] the CSR range [rs, re) of row 16 b + r as csr_row_range gives it
-// (empty past N), [34], [35] zero.  Entry s: CSR position e0 + s as column
-// (0xffff outside [0, K)) | fp16 value bits << 16 (0xffff past nnz).
-constexpr int kRecHdrWords = 36;
-
-// Slice records (read by the mid-batch kernel, K % 1024 == 0): per 16-row
-// group g and 1024-column slice s, kSrecHdrWords header words then entries,
-// kSrecWords(N, K, nnz) words in all (256 or 512).  Header: [0] tag, [1] the
-// number of the cell's entries that did not fit (the kernel then reads the
-// CSR), [2 + r] row 16 g + r's entries as start | end << 16 (entry indices),
-// [18], [19] zero.  Entry: column - 1024 s | fp16 value bits << 16, rows in
-// order, each row's entries in CSR order; unused slots 0xffff.
-constexpr int kSrecHdrWords = 20;
-
-__host__ __device__ inline uint32_t plan_srec_tag(int64_t N, int64_t K, int64_t nnz, int words, int64_t g, int s) {
-    return 0x53524543u ^ (uint32_t)nnz ^ ((uint32_t)N * 0x9E3779B1u) ^ ((uint32_t)K << 13) ^
-           ((uint32_t)words * 0xC2B2AE3Du) ^ ((uint32_t)g * 0x85EBCA77u) ^ ((uint32_t)s * 0x27D4EB2Fu);
-}
-
-// Tag of block b's record: ties a record to the layer shape and its place,
-// so that a plan of another layer (or a stale stride) is not read as this one.
-__host__ __device__ inline uint32_t plan_rec_tag(int64_t N, int64_t K, int64_t nnz, int dcap, int64_t b) {
-    return 0x52454331u ^ (uint32_t)nnz ^ ((uint32_t)N * 0x9E3779B1u) ^ ((uint32_t)K << 17) ^
-           ((uint32_t)dcap * 0xC2B2AE3Du) ^ ((uint32_t)b * 0x85EBCA77u);
-}
-
 __device__ __forceinline__ void csr_row_range(const int32_t *row_ptr, int64_t n, int64_t nnz,
                                               int32_t &rs, int32_t &re) {
     int64_t a = row_ptr[n], b = row_ptr[n + 1];

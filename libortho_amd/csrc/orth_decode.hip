@@ -34,11 +34,13 @@
 //    with DPP moves, and lane 0 of the row adds alpha*sum after the base term
 //    and stores, as /root/reference/src/dual_gemm.cu:212-221 does.  alpha <=
 //    0 takes a kernel without the term, which never touches the CSR arrays.
-//  * With an ortho plan (up to 4 tokens), the block's entries come from the
-//    plan's record of the block instead: packed column|value words at an
-//    address that needs no row pointer, loaded right after the activations
-//    and summed before the main loop, while the weights are in flight.
-//    Rows reaching past the record read the rest from the CSR at the end.
+//  * With an ortho plan, each wave reads the entries of its K quarter from
+//    the plan's record of (block, quarter) instead: packed column|value words
+//    at an address that needs no row pointer, loaded with the activations and
+//    summed (4 lanes per row) before the main loop, while the weights are in
+//    flight; no workgroup barrier is needed since a wave's entries use only
+//    the activations it staged.  A quarter whose entries did not fit its
+//    record reads the rows' CSR, filtered to the quarter's columns.
 #include <type_traits>
 
 #include "orth_common.h"
@@ -75,8 +77,8 @@ struct DecodeArgs {
     int lds_e;
     float alpha;
     int has_ortho;
-    const uint32_t *rec;   // plan records, kRecHdrWords + dcap words per 16-row block
-    int dcap;              // record entries per block (a multiple of 16), 0 without a plan
+    const uint32_t *rec;   // plan quarter records: qwords words per (16-row block, wave)
+    int qwords;            // a multiple of 256, at most 2048; 0 without a plan
     int deep;              // (host) fewer than two workgroups per CU: deeper weight prefetch
 };
 
@@ -100,9 +102,9 @@ constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 // 688 workgroups), 3 when it holds one (4096-row layers), 2 otherwise.
 // SPARSE: 0 no ortho term; 1 ortho term with the workgroup's CSR block
 // staged through LDS (16-byte aligned columns, nnz >= 4); 2 ortho term read
-// entry by entry in the epilogue; 3 / 4 / 5 the plan's record of the block
-// (at most 1024 / 2048 / 4096 words) staged through LDS and summed before
-// the main loop (XLDS only).
+// entry by entry in the epilogue; 3 / 4 / 5 / 6 the plan's records of the
+// block's four K quarters (256 / 512 / <= 1024 / <= 2048 words), one per
+// wave, staged through LDS and summed before the main loop (XLDS only).
 //
 // Every global load below is unconditional with a clamped, always valid
 // address: a load under a branch makes the compiler's wait-count insertion
@@ -129,7 +131,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     constexpr bool WT = decode_wt(MT, XLDS);
     constexpr int WREG = CPW * 1024;  // WT: LDS bytes of a wave's weight region
     constexpr bool REC = SPARSE >= 3;
-    constexpr int ER = SPARSE == 5 ? 4 : (SPARSE == 4 ? 2 : 1);  // record: 16-byte loads per thread
+    constexpr int ER = 1 << (SPARSE >= 3 ? SPARSE - 3 : 0);  // record: 16-byte loads per lane
     static_assert(!REC || XLDS, "the record kernels gather staged activations");
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -181,16 +183,15 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         }
     }
 
-    // ---- the block's plan record: its address needs no row pointer and it
-    //      carries the rows' CSR ranges, so it is issued before the weights
-    //      and returns with the activations
-    const int rwords = kRecHdrWords + a.dcap;
+    // ---- REC: this wave's plan record (the block's 16 rows, the wave's K
+    //      quarter): its address needs no other load, so it is issued before
+    //      the weights and returns with the activations
     u32x4 rv[ER];
     if (REC) {
-        const uint32_t *rb = a.rec + (int64_t)blockIdx.x * rwords;
+        const uint32_t *rb = a.rec + ((int64_t)blockIdx.x * 4 + wave) * a.qwords;
 #pragma unroll
         for (int r = 0; r < ER; r++)
-            rv[r] = *reinterpret_cast<const u32x4 *>(rb + min(4 * (tid + NT * r), rwords - 4));
+            rv[r] = *reinterpret_cast<const u32x4 *>(rb + min(4 * (lane + 64 * r), a.qwords - 4));
     }
 
     // ---- CSR bounds: this thread's epilogue row, and the workgroup block
@@ -208,7 +209,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 
     // ---- per-row scale of the row this thread combines at the end
     f16 srow = (f16)0.0f;
-    if (!GROUPED) srow = a.scales[n0 + min(SPARSE ? tid >> 4 : tid & 15, last_row)];
+    if (!GROUPED) srow = a.scales[n0 + min((SPARSE && !REC) ? tid >> 4 : tid & 15, last_row)];
 
     // ---- group scales of this lane's row nl: chunks c_lo + 8i .. + 8i + 7
     //      as one 16-byte vector (GMODE 1), chunks c_lo + 2i, + 2i + 1 as one
@@ -326,25 +327,26 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         e0 = min(max(__builtin_amdgcn_readlane(pv, 0), 0), a.nnz);
         e1 = min(max(__builtin_amdgcn_readlane(pv, last_row + 1), e0), a.nnz);
     }
-    // ---- REC: stage the record, then the sparse sums of this thread's row
-    //      (16 lanes per row, entries rs + sub + 16 u in order) while the
-    //      weights stream in; a row's entries past the record wait for the end.
-    //      Every path adds entry j as fma(v_j, x_j, sum) in j order (masked
-    //      slots as fma(0, 0, sum)), so planned and unplanned calls agree bit
-    //      for bit.
+    // ---- REC: the wave stages its record in its own LDS region and sums
+    //      v * x over the entries of its quarter, 4 lanes per row (entries
+    //      start + tg + 4 u, in order), reduced over the quad; the sums wait in
+    //      the region (over the record) for the epilogue, which adds
+    //      alpha * (sum over the 4 quarters) after the dense term.  No
+    //      workgroup barrier: the wave reads only activations it staged.
+    //      The remaining weight pairs are issued first.  Without a matching
+    //      record (another layer's plan, or entries that did not fit) the
+    //      rows are read from the CSR, filtered to the quarter's columns.
     float sacc[MT];
 #pragma unroll
     for (int m = 0; m < MT; m++) sacc[m] = 0.f;
-    int32_t rec_hi = 0;
-    bool rec_ok = true;
     if (REC) {
-        uint32_t *er = reinterpret_cast<uint32_t *>(smem + a.lds_e);
+        uint32_t *er = reinterpret_cast<uint32_t *>(smem + a.lds_e) + wave * a.qwords;
 #pragma unroll
         for (int r = 0; r < ER; r++) {
-            const int slot = 4 * (tid + NT * r);
-            if (slot < rwords) *reinterpret_cast<u32x4 *>(er + slot) = rv[r];
+            const int o = 4 * (lane + 64 * r);
+            if (o < a.qwords) *reinterpret_cast<u32x4 *>(er + o) = rv[r];
         }
-        __syncthreads();  // all activations and the record are in LDS
+        __builtin_amdgcn_wave_barrier();  // (same wave: LDS keeps the order)
         if (FULL) {
             if (WT) {
 #pragma unroll
@@ -354,34 +356,54 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 for (int p = PDC; p < PDMC; p++) load_chunk(p);
             }
         }
-        // the record of another layer or block fails the tag: the rows are
-        // then read from the CSR at the end
-        rec_ok = er[0] == plan_rec_tag(a.N, K, a.nnz, a.dcap, blockIdx.x);
-        if (rec_ok) {
-            e0 = min(max((int32_t)er[1], 0), a.nnz);
-            rs = min(max((int32_t)er[2 + rl], 0), a.nnz);
-            re = min(max((int32_t)er[18 + rl], rs), a.nnz);
-            if (rl > last_row) re = rs;
-        }
-        rec_hi = (rec_ok && rs >= e0) ? min(re, e0 + a.dcap) : rs;
-        const uint32_t *ee = er + kRecHdrWords;
-        constexpr int U = 4;
-        for (int32_t j0 = rs + sub; j0 < rec_hi; j0 += 16 * U) {
-            uint32_t w[U];
+        const int qr = lane >> 2, tg = lane & 3;  // row of the block, lane of its quad
+        const int32_t col0 = c_lo * 128, col1 = (c_lo + nci) * 128;
+        auto add_entry = [&](bool ok_e, int c, float vv) {
+            const int cc = ok_e ? c : 0;
 #pragma unroll
-            for (int u = 0; u < U; u++) w[u] = ee[min(j0 + 16 * u, rec_hi - 1) - e0];
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int c = (int)(w[u] & 0xffffu);
-                const bool ok_e = (j0 + 16 * u < rec_hi) & (c < K);
-                const int cc = ok_e ? c : 0;
-                const float vv = ok_e ? (float)__builtin_bit_cast(f16, (uint16_t)(w[u] >> 16)) : 0.f;
-#pragma unroll
-                for (int m = 0; m < MT; m++) {
-                    const float xv = (float)xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))];
-                    sacc[m] = __builtin_fmaf(vv, ok_e ? xv : 0.f, sacc[m]);
-                }
+            for (int m = 0; m < MT; m++) {
+                const float xv = (float)xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))];
+                sacc[m] = __builtin_fmaf(ok_e ? vv : 0.f, ok_e ? xv : 0.f, sacc[m]);
             }
+        };
+        const bool ok = (er[0] == plan_cell_tag(kCellQuarter, a.N, K, a.nnz, a.qwords, blockIdx.x, wave)) &
+                        (er[1] == 0u);  // (uniform)
+        if (ok) {
+            const uint32_t h = er[2 + qr];
+            const int32_t lo = (int32_t)(h & 0xffffu);
+            const int32_t hi = qr <= last_row ? (int32_t)(h >> 16) : lo;
+            const uint32_t *ee = er + kCellHdrWords;
+            constexpr int U = 4;
+            for (int32_t j0 = lo + tg; j0 < hi; j0 += 4 * U) {
+                uint32_t w[U];
+#pragma unroll
+                for (int u = 0; u < U; u++) w[u] = ee[min(j0 + 4 * u, hi - 1)];
+#pragma unroll
+                for (int u = 0; u < U; u++)
+                    add_entry(j0 + 4 * u < hi, (int)(w[u] & 0xffffu) + col0,
+                              (float)__builtin_bit_cast(f16, (uint16_t)(w[u] >> 16)));
+            }
+        } else {
+            int32_t fs = 0, fe = 0;
+            csr_row_range(a.row_ptr, n0 + min(qr, last_row), a.nnz, fs, fe);
+            if (qr > last_row) fe = fs;
+            for (int32_t j = fs + tg; j < fe; j += 4) {
+                const int32_t c = a.col[j];
+                add_entry(c >= col0 && c < col1, c, (float)a.vals[j]);
+            }
+        }
+        // quad sums (fixed order), kept for the epilogue in the record region
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            float v = sacc[m];
+            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
+            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
+            sacc[m] = v;
+        }
+        __builtin_amdgcn_wave_barrier();  // every lane has read the record
+        if (tg == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) reinterpret_cast<float *>(er)[m * 16 + qr] = sacc[m];
         }
     }
     const int32_t eb = e0 & ~3;
@@ -577,16 +599,11 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     //      then their activation reads, are issued together (one LDS or L2
     //      round trip each instead of one per entry); entries past the
     //      staged block (very dense rows) are read from memory one by one.
-    if (SPARSE) {
+    if (SPARSE && !REC) {
         constexpr int U = 4;
-        if (REC && !rec_ok) {  // (uniform) this row's CSR range, read from memory
-            csr_row_range(a.row_ptr, n0 + min(rl, last_row), a.nnz, rs, re);
-            if (rl > last_row) re = rs;
-            rec_hi = rs;
-        }
         const int32_t staged_hi = SPARSE == 1 ? min(min(eb + kDecodeEStaged, last4 + 4), e1) : eb;
-        const int32_t fast_hi = REC ? rec_hi : min(re, staged_hi);
-        for (int32_t j0 = rs + sub; !REC && j0 < fast_hi; j0 += 16 * U) {
+        const int32_t fast_hi = min(re, staged_hi);
+        for (int32_t j0 = rs + sub; j0 < fast_hi; j0 += 16 * U) {
             int32_t c[U];
             float v[U];
 #pragma unroll
@@ -643,9 +660,9 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
         }
         return;
     }
-    __syncthreads();
 
-    // ---- combine split-K partials, scale, store
+    // ---- combine split-K partials (visible since the barrier above), scale,
+    //      add alpha * (the quarters' sparse sums, REC), store
     if (tid < MT * RT) {
         const int m = tid >> 4, r = tid & 15;
         const int64_t n = n0 + r;
@@ -654,6 +671,12 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 #pragma unroll
             for (int w = 0; w < W; w++) v += red(w)[m * 16 + r];
             if (!GROUPED) v *= (float)srow;
+            if (REC) {
+                float sp = 0.f;
+#pragma unroll
+                for (int w = 0; w < W; w++) sp += (reinterpret_cast<const float *>(smem + a.lds_e) + w * a.qwords)[m * 16 + r];
+                v += a.alpha * sp;
+            }
             a.y[(int64_t)m * a.N + n] = (f16)v;
         }
     }
@@ -717,13 +740,13 @@ static hipError_t launch_decode_t(const DecodeArgs &d0, hipStream_t stream) {
     if ((GMODE == 1 || GMODE == 4) && !(d.cpw == CPW && d.nchunks == 4 * CPW)) return hipErrorInvalidValue;
     if constexpr (XLDS && MT <= 4) {
         // plan records when the LDS takes them (else the CSR block below)
-        const int rwords = kRecHdrWords + d.dcap;
-        if (d.has_ortho && d.dcap > 0 && rwords <= 4096) {
-            const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW, rwords);
+        if (d.has_ortho && d.qwords > 0) {
+            const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW, kDecodeW * d.qwords);
             if (lds <= kDecodeLdsMax) {
-                if (rwords <= 1024) return launch_decode_k<MT, GMODE, XLDS, CPW, 3>(d, lds, stream);
-                if (rwords <= 2048) return launch_decode_k<MT, GMODE, XLDS, CPW, 4>(d, lds, stream);
-                return launch_decode_k<MT, GMODE, XLDS, CPW, 5>(d, lds, stream);
+                if (d.qwords == 256) return launch_decode_k<MT, GMODE, XLDS, CPW, 3>(d, lds, stream);
+                if (d.qwords == 512) return launch_decode_k<MT, GMODE, XLDS, CPW, 4>(d, lds, stream);
+                if (d.qwords <= 1024) return launch_decode_k<MT, GMODE, XLDS, CPW, 5>(d, lds, stream);
+                return launch_decode_k<MT, GMODE, XLDS, CPW, 6>(d, lds, stream);
             }
         }
     }
@@ -763,11 +786,8 @@ static const int64_t kDecodeXLdsMax = 40 * 1024;
 static const int kDecodeMaxCPW = 24;
 
 // Chunks per wave: an even count (group-128 scales come in pairs).
-static int decode_cpw(int64_t K) {
-    const int64_t nchunks = K / 128;
-    const int64_t c = (nchunks + kDecodeW - 1) / kDecodeW;
-    return (int)((c + 1) & ~int64_t(1));
-}
+// chunks per wave; the plan's decode records cover the same K quarters
+static int decode_cpw(int64_t K) { return decode_chunks_per_wave(K); }
 
 static bool decode_xlds(int64_t M, int64_t K) {
     int64_t mt = 1;
@@ -789,7 +809,7 @@ bool decode_supported(const ForwardArgs &a) {
     return true;
 }
 
-int64_t plan_rec_cap(int64_t N, int64_t nnz);           // orth_prefill.hip
+int plan_qrec_words(int64_t N, int64_t K, int64_t nnz);  // orth_prefill.hip
 int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz);
 
 // plan: an ortho plan of at least plan_bytes_for(N, K, nnz) bytes, or null;
@@ -819,7 +839,7 @@ hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStr
     const bool rec = plan && a.has_ortho;
     d.rec = rec ? reinterpret_cast<const uint32_t *>(static_cast<const char *>(plan) + plan_rec_at(a.N, a.K, a.nnz))
                 : nullptr;
-    d.dcap = rec ? (int)plan_rec_cap(a.N, a.nnz) : 0;
+    d.qwords = rec ? plan_qrec_words(a.N, a.K, a.nnz) : 0;
 
     int mt = 1;
     while (mt < a.M) mt <<= 1;

@@ -34,23 +34,19 @@ namespace orth {
 //   uint32 entries[nnz]                   (row_in_block << 24) | (col_in_step << 16) | fp16 bits
 //   uint16 chunks[N][K/128 + 1]           (K % 128 == 0 only) per row, the number of
 //                                         its CSR entries with column < 128 c
-//   uint32 records[ceil(N/16)][36 + dcap] per 16-row block b: a header (tag, e0 =
-//                                         row_ptr[16 b] clamped to [0, nnz], the CSR
-//                                         range of each of the 16 rows) and the CSR
-//                                         positions [e0, e0 + dcap) as column (0xffff
-//                                         when outside [0, K)) | fp16 value bits << 16
-//                                         (0xffff past nnz); see orth_common.h.  dcap
-//                                         is in the header's pad[0].
-//   uint32 srecs[ceil(N/16)][K/1024][W]   (K % 1024 == 0, W = 256 or 512 words) per
-//                                         16-row group and 1024-column slice, the
-//                                         rows' entries of the slice packed: see
-//                                         orth_common.h.  W is in pad[1] (0: none).
+//   uint32 qrecs[ceil(N/16)][4][Wq]      per 16-row group and decode K quarter (the
+//                                         columns of decode wave w), the rows' entries
+//                                         packed (cell records, see orth_common.h);
+//                                         Wq = 256 .. 2048 words, in pad[0]
+//   uint32 srecs[ceil(N/16)][K/1024][W]   (K % 1024 == 0) the same per 1024-column
+//                                         slice for the mid-batch kernel; W = 256 or
+//                                         512 words, in pad[1] (0: none)
 // Entries of one (block, step) are ordered by row then by CSR position.  The
 // chunk table locates a row's entries of columns [128 c0, 128 c1) in the CSR
 // itself when the row's columns ascend strictly (flag kPlanUnsorted clear).
-// The records give the decode kernel each 16-row block's entries at an
-// address known before any load returns (a CSR block's start is itself a
-// load); rows reaching past their block's record read the rest from the CSR.
+// The cell records give the decode and mid-batch kernels each wave's
+// entries at an address known before any load returns (a CSR range's start
+// is itself a load); a cell whose entries do not fit is read from the CSR.
 
 static const uint32_t kPlanMagic = 0x504f5254u;  // "TROP"
 static const uint32_t kPlanVersion = 4;
@@ -85,40 +81,37 @@ int64_t plan_chunks_bytes(int64_t N, int64_t K) {
     return K % 128 == 0 ? ((N * (K / 128 + 1) * 2) + 15) & ~int64_t(15) : 0;
 }
 
-// Entries per decode record: the mean count of a 16-row block plus four
-// times its square root (a binomial block count's standard deviation), in
-// whole 16-entry groups, at most kPlanRecMax (a record of at most 4096
-// words: four 16-byte loads per thread of the decode kernel).
-static const int64_t kPlanRecMax = 4096 - 48;
-
-int64_t plan_rec_cap(int64_t N, int64_t nnz) {
-    if (nnz <= 0 || N <= 0) return 0;
-    const int64_t mean = (16 * nnz + N - 1) / N;
+// Words of a cell record of `cols` columns: the header plus the mean entry
+// count of a 16-row cell plus four times (its square root + 1), in 256-word
+// units; 0 (no records) past max_words.
+static int cell_words(int64_t N, int64_t K, int64_t nnz, int64_t cols, int max_words) {
+    if (nnz <= 0 || N <= 0 || K <= 0) return 0;
+    const int64_t mean = (16 * cols * nnz + N * K - 1) / (N * K);
     int64_t s = 0;
     while ((s + 1) * (s + 1) <= mean) s++;
-    const int64_t cap = (mean + 4 * (s + 1) + 15) & ~int64_t(15);
-    return cap < kPlanRecMax ? cap : kPlanRecMax;
+    const int64_t need = kCellHdrWords + mean + 4 * (s + 1);
+    const int64_t w = (need + 255) / 256 * 256;
+    return w <= max_words ? (int)w : 0;
+}
+
+// decode K quarters (K % 128 == 0): a multiple of 256 words, at most 2048
+int plan_qrec_words(int64_t N, int64_t K, int64_t nnz) {
+    if (K % 128 != 0) return 0;
+    return cell_words(N, K, nnz, (int64_t)decode_chunks_per_wave(K) * 128, 2048);
+}
+
+// mid-batch slices (K % 1024 == 0): 256 or 512 words
+int plan_srec_words(int64_t N, int64_t K, int64_t nnz) {
+    if (K % 1024 != 0) return 0;
+    return cell_words(N, K, nnz, 1024, 512);
 }
 
 int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz) {
     return plan_chunks_at(N, K, nnz) + plan_chunks_bytes(N, K);
 }
 
-// Words per slice record: header plus the mean entry count of a (16-row,
-// 1024-column) cell plus four times (its square root + 1), in 256-word
-// units; 0 (no slice records) when K % 1024 != 0 or more than 512 are needed.
-int plan_srec_words(int64_t N, int64_t K, int64_t nnz) {
-    if (nnz <= 0 || N <= 0 || K % 1024 != 0) return 0;
-    const int64_t mean = (16 * 1024 * nnz + N * K - 1) / (N * K);
-    int64_t s = 0;
-    while ((s + 1) * (s + 1) <= mean) s++;
-    const int64_t need = kSrecHdrWords + mean + 4 * (s + 1);
-    const int64_t w = (need + 255) / 256 * 256;
-    return w <= 512 ? (int)w : 0;
-}
-
 int64_t plan_srec_at(int64_t N, int64_t K, int64_t nnz) {
-    return plan_rec_at(N, K, nnz) + ((N + 15) / 16) * (kRecHdrWords + plan_rec_cap(N, nnz)) * 4;
+    return plan_rec_at(N, K, nnz) + ((N + 15) / 16) * 4 * (int64_t)plan_qrec_words(N, K, nnz) * 4;
 }
 
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) {
@@ -134,7 +127,7 @@ bool plan_supported(const ForwardArgs &a) {
 }
 
 __global__ void plan_init_kernel(PlanHeader *h, int nblocks, int nksteps, int64_t N, int64_t K,
-                                 int64_t nnz, int dcap, int swords) {
+                                 int64_t nnz, int qwords, int swords) {
     if (threadIdx.x == 0) {
         h->magic = kPlanMagic;
         h->version = kPlanVersion;
@@ -146,7 +139,7 @@ __global__ void plan_init_kernel(PlanHeader *h, int nblocks, int nksteps, int64_
         h->k = K;
         h->nnz = nnz;
         h->flags = 0;
-        h->pad[0] = (uint32_t)dcap;
+        h->pad[0] = (uint32_t)qwords;
         h->pad[1] = (uint32_t)swords;
         h->pad[2] = 0;
     }
@@ -263,57 +256,27 @@ __global__ void __launch_bounds__(256) plan_build_kernel(ForwardArgs a, PlanHead
     }
 }
 
-// One workgroup per 16-row block: its record, slot s = CSR position e0 + s.
-__global__ void __launch_bounds__(256) plan_rec_kernel(ForwardArgs a, uint32_t *rec, int dcap) {
-    const int64_t b = blockIdx.x;
-    int64_t e0 = a.row_ptr[b * 16];
-    e0 = e0 < 0 ? 0 : (e0 > a.nnz ? a.nnz : e0);
-    uint32_t *hdr = rec + b * (kRecHdrWords + dcap);
-    uint32_t *r = hdr + kRecHdrWords;
-    const int t = threadIdx.x;
-    if (t == 0) {
-        hdr[0] = plan_rec_tag(a.N, a.K, a.nnz, dcap, b);
-        hdr[1] = (uint32_t)e0;
-        hdr[34] = hdr[35] = 0u;
-    }
-    if (t < 16) {
-        const int64_t n = b * 16 + t;
-        int32_t rs = 0, re = 0;
-        if (n < a.N) csr_row_range(a.row_ptr, n, a.nnz, rs, re);
-        hdr[2 + t] = (uint32_t)rs;
-        hdr[18 + t] = (uint32_t)re;
-    }
-    for (int s = t; s < dcap; s += 256) {
-        const int64_t j = e0 + s;
-        uint32_t w = 0xffffu;
-        if (j < a.nnz) {
-            const int32_t c = a.col[j];
-            w = ((c >= 0 && c < a.K) ? (uint32_t)c : 0xffffu) | (value_bits_f16(a.vals, a.val_dtype, j) << 16);
-        }
-        r[s] = w;
-    }
-}
-
-// One workgroup of 64 per (16-row group, slice): thread r < 16 counts its
-// row's entries of the slice, thread 0 lays out the rows, then each thread
-// writes its row's entries in CSR order (those past the record are counted
-// in header word 1).
-__global__ void __launch_bounds__(64) plan_srec_kernel(ForwardArgs a, uint32_t *srec, int words, int nslices) {
+// One workgroup of 64 per (16-row group, cell) of `ncells` cells of
+// `cols` columns: thread r < 16 counts its row's entries of the cell, thread
+// 0 lays out the rows, then each thread writes its row's entries in CSR
+// order (those past the record are counted in header word 1).
+__global__ void __launch_bounds__(64) plan_cell_kernel(ForwardArgs a, uint32_t *out, int words, int ncells,
+                                                       int cols, uint32_t kind) {
     __shared__ int32_t cnt[16], start[17];
-    const int64_t g = blockIdx.x / nslices;
-    const int s = (int)(blockIdx.x - g * nslices);
+    const int64_t g = blockIdx.x / ncells;
+    const int c = (int)(blockIdx.x - g * ncells);
     const int t = threadIdx.x;
-    uint32_t *rec = srec + (g * nslices + s) * (int64_t)words;
-    const int cap = words - kSrecHdrWords;
-    const int32_t c0 = s * 1024;
+    uint32_t *rec = out + (g * ncells + c) * (int64_t)words;
+    const int cap = words - kCellHdrWords;
+    const int64_t c0 = (int64_t)c * cols, c1 = min(c0 + cols, a.K);
     int32_t rs = 0, re = 0;
     const int64_t n = g * 16 + t;
     if (t < 16) {
         if (n < a.N) csr_row_range(a.row_ptr, n, a.nnz, rs, re);
         int32_t k = 0;
         for (int32_t j = rs; j < re; j++) {
-            const int32_t c = a.col[j];
-            k += (c >= c0 && c < c0 + 1024) ? 1 : 0;
+            const int32_t cc = a.col[j];
+            k += (cc >= c0 && cc < c1) ? 1 : 0;
         }
         cnt[t] = k;
     }
@@ -325,21 +288,21 @@ __global__ void __launch_bounds__(64) plan_srec_kernel(ForwardArgs a, uint32_t *
             run += cnt[r];
         }
         start[16] = run;
-        rec[0] = plan_srec_tag(a.N, a.K, a.nnz, words, g, s);
+        rec[0] = plan_cell_tag(kind, a.N, a.K, a.nnz, words, g, c);
         rec[1] = (uint32_t)(run > cap ? run - cap : 0);
         rec[18] = rec[19] = 0u;
     }
     __syncthreads();
-    for (int i = t; i < cap; i += 64) rec[kSrecHdrWords + i] = 0xffffu;
+    for (int i = t; i < cap; i += 64) rec[kCellHdrWords + i] = 0xffffu;
     __syncthreads();
     if (t < 16) {
         const int32_t b = min(start[t], cap), e = min(start[t + 1], cap);
         rec[2 + t] = (uint32_t)b | ((uint32_t)e << 16);
         int32_t w = start[t];
         for (int32_t j = rs; j < re; j++) {
-            const int32_t c = a.col[j];
-            if (c >= c0 && c < c0 + 1024) {
-                if (w < cap) rec[kSrecHdrWords + w] = (uint32_t)(c - c0) | (value_bits_f16(a.vals, a.val_dtype, j) << 16);
+            const int32_t cc = a.col[j];
+            if (cc >= c0 && cc < c1) {
+                if (w < cap) rec[kCellHdrWords + w] = (uint32_t)(cc - c0) | (value_bits_f16(a.vals, a.val_dtype, j) << 16);
                 w++;
             }
         }
@@ -353,23 +316,27 @@ hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t strea
     int32_t *offsets = reinterpret_cast<int32_t *>(static_cast<char *>(plan) + sizeof(PlanHeader));
     uint32_t *entries = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(offsets) +
                                                      plan_offsets_bytes(a.N, a.K));
-    const int dcap = (int)plan_rec_cap(a.N, a.nnz);
+    const int qwords = plan_qrec_words(a.N, a.K, a.nnz);
     const int swords = plan_srec_words(a.N, a.K, a.nnz);
     hipLaunchKernelGGL(plan_init_kernel, dim3(1), dim3(64), 0, stream, h, nblocks, nksteps, a.N,
-                       a.K, a.nnz, dcap, swords);
+                       a.K, a.nnz, qwords, swords);
     const size_t lds = ((size_t)nksteps * kPlanBN + 256) * sizeof(int32_t);
     uint16_t *chunks = plan_chunks_bytes(a.N, a.K)
                            ? reinterpret_cast<uint16_t *>(static_cast<char *>(plan) + plan_chunks_at(a.N, a.K, a.nnz))
                            : nullptr;
     hipLaunchKernelGGL(plan_build_kernel, dim3(nblocks), dim3(256), lds, stream, a, h, offsets,
                        entries, chunks, nksteps);
-    uint32_t *rec = reinterpret_cast<uint32_t *>(static_cast<char *>(plan) + plan_rec_at(a.N, a.K, a.nnz));
-    hipLaunchKernelGGL(plan_rec_kernel, dim3((unsigned)((a.N + 15) / 16)), dim3(256), 0, stream, a, rec, dcap);
+    const unsigned ngroups = (unsigned)((a.N + 15) / 16);
+    if (qwords > 0) {
+        uint32_t *qrec = reinterpret_cast<uint32_t *>(static_cast<char *>(plan) + plan_rec_at(a.N, a.K, a.nnz));
+        hipLaunchKernelGGL(plan_cell_kernel, dim3(ngroups * 4), dim3(64), 0, stream, a, qrec, qwords, 4,
+                           decode_chunks_per_wave(a.K) * 128, kCellQuarter);
+    }
     if (swords > 0) {
         const int nslices = (int)(a.K / 1024);
         uint32_t *srec = reinterpret_cast<uint32_t *>(static_cast<char *>(plan) + plan_srec_at(a.N, a.K, a.nnz));
-        hipLaunchKernelGGL(plan_srec_kernel, dim3((unsigned)(((a.N + 15) / 16) * nslices)), dim3(64), 0, stream, a,
-                           srec, swords, nslices);
+        hipLaunchKernelGGL(plan_cell_kernel, dim3(ngroups * (unsigned)nslices), dim3(64), 0, stream, a, srec,
+                           swords, nslices, 1024, kCellSlice);
     }
     return hipGetLastError();
 }

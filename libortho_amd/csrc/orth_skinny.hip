@@ -329,13 +329,13 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
         const uint32_t *wr = reinterpret_cast<const uint32_t *>(smem + a.lds_sr) + wave * a.swords;
         // (uniform per wave) the record of this group and slice, all its
         // entries inside: else the row's CSR range, filtered by column
-        const bool ok = (wr[0] == plan_srec_tag(a.N, K, a.nnz, a.swords, g16, sl)) & (wr[1] == 0u);
+        const bool ok = (wr[0] == plan_cell_tag(kCellSlice, a.N, K, a.nnz, a.swords, g16, sl)) & (wr[1] == 0u);
         if (ok) {
             const uint32_t h = wr[2 + ((tid >> 2) & 15)];
             lo = (int32_t)(h & 0xffffu);
             hi = (int32_t)(h >> 16);
             if (n0 + sr >= a.N) hi = lo;
-            const uint32_t *ent = wr + kSrecHdrWords;
+            const uint32_t *ent = wr + kCellHdrWords;
             for (int32_t j0 = lo; j0 < hi; j0 += kSkEB) {
                 int32_t c2[EL];
                 uint32_t v2[EL];

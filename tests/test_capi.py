@@ -145,21 +145,26 @@ def test_forward_without_gpu_reports_no_device(L):
         _lib.device_info(0)
 
 
-def rec_cap(N, nnz):
-    # decode records: mean entries of a 16-row block + 4 (isqrt(mean) + 1),
-    # in 16-entry groups, at most 4048 (36 header words + entries <= 4096)
-    mean = -(-16 * nnz // N)
-    return min(4048, (mean + 4 * (math.isqrt(mean) + 1) + 15) // 16 * 16)
+def cell_words(N, K, nnz, cols, max_words):
+    # plan records of (16-row block, cols-column cell): 20 header words + the
+    # mean entries of a cell + 4 (isqrt(mean) + 1), in 256-word units; 0 (no
+    # records) above max_words
+    mean = -(-16 * cols * nnz // (N * K))
+    w = -(-(20 + mean + 4 * (math.isqrt(mean) + 1)) // 256) * 256
+    return w if w <= max_words else 0
+
+
+def qrec_words(N, K, nnz):
+    # decode records: one per (16-row block, K quarter of cpw chunks)
+    if K % 128:
+        return 0
+    c = (K // 128 + 3) // 4
+    return cell_words(N, K, nnz, ((c + 1) & ~1) * 128, 2048)
 
 
 def srec_words(N, K, nnz):
-    # mid-batch slice records: header + mean entries of a (16-row, 1024-col)
-    # cell + 4 (isqrt(mean) + 1), in 256-word units, at most 512 (else none)
-    if K % 1024:
-        return 0
-    mean = -(-16 * 1024 * nnz // (N * K))
-    w = -(-(20 + mean + 4 * (math.isqrt(mean) + 1)) // 256) * 256
-    return w if w <= 512 else 0
+    # mid-batch records: one per (16-row block, 1024-column slice)
+    return 0 if K % 1024 else cell_words(N, K, nnz, 1024, 512)
 
 
 def test_plan_size(L):
@@ -167,22 +172,25 @@ def test_plan_size(L):
     n = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4096, N=4096, nnz=100)))
     offsets = ((4096 // 128) * (4096 // 64 + 1) * 4 + 15) // 16 * 16
     chunks = (4096 * (4096 // 128 + 1) * 2 + 15) // 16 * 16  # uint16 [N][K/128 + 1]
-    records = (4096 // 16) * (36 + rec_cap(4096, 100)) * 4   # uint32 [N/16][36 + dcap]
-    assert rec_cap(4096, 100) == 16
+    qrecs = (4096 // 16) * 4 * qrec_words(4096, 4096, 100) * 4  # uint32 [N/16][4][Wq]
+    assert qrec_words(4096, 4096, 100) == 256
     srecs = (4096 // 16) * (4096 // 1024) * srec_words(4096, 4096, 100) * 4
     assert srec_words(4096, 4096, 100) == 256
-    assert n == (64 + offsets + 400 + 15) // 16 * 16 + chunks + records + srecs
-    # K % 128 != 0: no chunk table; a ragged last row block still has a record
+    assert n == (64 + offsets + 400 + 15) // 16 * 16 + chunks + qrecs + srecs
+    # K % 128 != 0: no chunk table and no records
     n64 = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4160, N=4100, nnz=100)))
-    assert n64 == (64 + ((4100 + 127) // 128) * (4160 // 64 + 1) * 4 + 400 + 15) // 16 * 16 + \
-        ((4100 + 15) // 16) * (36 + rec_cap(4100, 100)) * 4
-    # c2 (1 % of 4096 x 11008): 656 entries per block on average -> 768
-    assert rec_cap(11008, 450888) == 768
-    assert rec_cap(64, 64 * 4096) == 4048  # capped
-    # c2: 164 entries per (16-row, 1024-column) cell -> 256 words; 2 % -> 512
+    assert n64 == (64 + ((4100 + 127) // 128) * (4160 // 64 + 1) * 4 + 400 + 15) // 16 * 16
+    # c2 (1 % of 4096 x 11008): 164 entries per (16-row, 1024-column) cell ->
+    # 256 words; 2 % -> 512; 10 %: no records (the CSR paths)
+    assert qrec_words(11008, 4096, 450888) == 256
     assert srec_words(11008, 4096, 450888) == 256
     assert srec_words(4096, 4096, 335544) == 512
-    assert srec_words(4096, 4096, 4096 * 4096 // 10) == 0  # 10 %: the CSR path
+    assert srec_words(4096, 4096, 4096 * 4096 // 10) == 0
+    # down_proj shape (K = 11008: quarters of 22 chunks, 2816 columns) at 1 %
+    assert qrec_words(4096, 11008, 450888) == 768
+    assert qrec_words(4096, 11008, 2 * 450888) == 1280   # down_proj at 2 %
+    assert qrec_words(4096, 4096, 4096 * 4096 // 10) == 2048
+    assert qrec_words(4096, 4096, 4096 * 4096 // 5) == 0  # 20 %: the CSR path
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4000, nnz=5))) < 0  # K % 64 != 0
     assert L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=4095))) == -_lib.ERR_INVALID_ARGUMENT
 
