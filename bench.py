@@ -246,8 +246,10 @@ def summarize_pmc(fetch_csv, write_csv):
     w_fac, w_k = per["WRITE_SIZE"]
     for name in f_k:
         if name.startswith("void orth::decode_kernel"):
-            # template arg SPARSE (last) is 0 for the alpha = 0 launches
-            alpha = 0.0 if name.rstrip(")").endswith("0>(orth::DecodeArgs") else 1.0
+            # template args <MT, GMODE, XLDS, CPW, SPARSE, PD>: SPARSE is 0
+            # for the alpha = 0 launches
+            targs = name[name.index("<") + 1:name.index(">")].split(",")
+            alpha = 0.0 if targs[4].strip() == "0" else 1.0
             key, algo = f"c2_m1_alpha{int(alpha)}", W.algorithmic_bytes(c2, 1, alpha)
         elif "orth::prefill_kernel" in name:
             key, algo = "c3_m2048_alpha1", W.algorithmic_bytes(c3, 2048, 1.0)
