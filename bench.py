@@ -21,7 +21,10 @@ Printed: one JSON line with the contract fields plus
   cpu_baseline  the reference CPU forward restated (oracle/cpu_baseline.c,
                 reference flags, 1 pinned core) on a bounded sample
   secondary     the rest of the metric: M in {2,4,8,16} GB/s, and the
-                prefill TFLOP/s at M=2048 (4096->11008 and 4096->4096)
+                prefill TFLOP/s at M=2048 (4096->11008 and 4096->4096);
+                then the packing kernels (load time) on the c2 layer from
+                dense FP32 weights: GB/s of algorithmic bytes (W read once,
+                q / scales / CSR written once)
 """
 from __future__ import annotations
 
@@ -158,6 +161,88 @@ def time_workload(torch, layer, M, alpha, steps, warmup, plan=False):
     ms = t0.elapsed_time(t1) / steps
     del g
     return dict(ms_per_step=ms, kernel=kernel, copies=rot.n)
+
+
+def graph_time(torch, fn, steps):
+    """Average duration of fn(i) for i < steps: HIP events around one replay
+    of a graph holding the steps launches (as time_workload)."""
+    fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    del g
+    return t0.elapsed_time(t1) / steps
+
+
+def time_pack(torch, steps=30):
+    """The packing kernels on the c2 layer (4096 -> 11008) from dense FP32
+    weights rotated over 3 copies (3 x 180 MB, past the Infinity Cache):
+    INT4 base packing with group-128 and per-row scales, and the CSR of a
+    1 % matrix (row counts + scan, then the fill).  Returns secondary
+    entries; algorithmic bytes read W once and write each output once."""
+    import ctypes
+    from libortho_amd import _lib
+    L = _lib.lib()
+    N, K, nnz, copies = 11008, 4096, 450888, 3
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    S = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    out = []
+
+    wb = [torch.randn(N, K, device="cuda", generator=gen) * 0.05 for _ in range(copies)]
+    q = torch.empty(N, K // 2, dtype=torch.uint8, device="cuda")
+    for G, label in ((128, "group-128"), (K, "per-row")):
+        s16 = torch.empty(N * (K // G), dtype=torch.float16, device="cuda")
+        ms = graph_time(torch, lambda i: _lib.check(L.orth_pack_base_hip(
+            P(wb[i % copies]), _lib.DT_F32, N, K, G, None, 0, P(q), P(s16), S())), steps)
+        b = N * K * 4 + N * K // 2 + 2 * N * (K // G)
+        out.append({"workload": f"pack base c2 fp32 {label}", "kernel": "pack_group" if G == 128 else "pack_row",
+                    "us_per_step": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        log(f"  {out[-1]}")
+    del wb
+
+    wo = []
+    for _ in range(copies):
+        w = torch.zeros(N * K, device="cuda")
+        idx = torch.randperm(N * K, device="cuda", generator=gen)[:nnz]
+        w[idx] = torch.randn(nnz, device="cuda", generator=gen) + 3.0
+        wo.append(w.view(N, K))
+    rps = [torch.empty(N + 1, dtype=torch.int32, device="cuda") for _ in range(copies)]
+    for i in range(copies):
+        _lib.check(L.orth_pack_csr_rows_hip(P(wo[i]), _lib.DT_F32, N, K, P(rps[i]), S()))
+    torch.cuda.synchronize()
+    assert all(int(r[N]) == nnz for r in rps)
+    col = torch.empty(nnz, dtype=torch.int32, device="cuda")
+    vals = torch.empty(nnz, dtype=torch.float32, device="cuda")
+    ms_rows = graph_time(torch, lambda i: _lib.check(L.orth_pack_csr_rows_hip(
+        P(wo[i % copies]), _lib.DT_F32, N, K, P(rps[i % copies]), S())), steps)
+    ms_fill = graph_time(torch, lambda i: _lib.check(L.orth_pack_csr_fill_hip(
+        P(wo[i % copies]), _lib.DT_F32, N, K, P(rps[i % copies]), P(col), P(vals), _lib.DT_F32, S())), steps)
+    b = N * K * 4 + 4 * (N + 1) + 8 * nnz
+    ms = ms_rows + ms_fill
+    out.append({"workload": "pack csr c2 fp32 1 %", "kernel": "csr_count+csr_scan, csr_fill",
+                "us_per_step": round(ms * 1e3, 2), "us_rows": round(ms_rows * 1e3, 2),
+                "us_fill": round(ms_fill * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    log(f"  {out[-1]}")
+    return out
 
 
 COPY_BYTES = 512 << 20  # calibration copy: reads and writes exactly this many bytes
@@ -366,6 +451,7 @@ def main():
                                   "TFLOP/s": round(tf, 1),
                                   "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
                 log(f"  {secondary[-1]}")
+        secondary.extend(time_pack(torch))
 
     workload = "c2_m1_alpha1"
     out = {

@@ -138,6 +138,47 @@ int orth_ortho_plan_build(const orth_hip_layer_t *layer, void *plan, int64_t pla
  * and unpack_int4 of /root/reference/src/dual_gemm.cu:30-40. */
 int orth_base_dequant_hip(const orth_hip_layer_t *layer, float *out, void *stream);
 
+/* Packing on the device (load time).  All pointers are device memory; the
+ * calls are asynchronous on `stream`.
+ *
+ * orth_pack_base_hip quantises dense weights w [out_features, in_features]
+ * (F16, BF16 or F32, row-major) to the packed INT4 layout of
+ * orth_hip_base_t: q_out uint8 [out_features, in_features / 2] (low nibble =
+ * even index) and scales_out FP16 [out_features, in_features / group_size]
+ * (group_size <= 0: one scale per row).  Without scales_in the scales are
+ * max|w| / 7 per row or group, clamped at 1e-6; with scales_in (dtype
+ * scales_in_dtype, same shape) those are used.  q = clamp(round(w / s), -8,
+ * 7) with s as computed or given, not its FP16 copy.  Replaces the torch
+ * ops of load_from_weights, /root/reference/torch_bind/ortho_linear.py:89-120,
+ * with their results on a GPU tensor (see orth_pack.hip for the arithmetic).
+ * group_size must be even and divide in_features (even). */
+int orth_pack_base_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                       int64_t group_size, const void *scales_in, int32_t scales_in_dtype, void *q_out,
+                       void *scales_out, void *stream);
+
+/* Which kernel orth_pack_base_hip takes for these arguments: 1 one wave per
+ * (row, group) for group sizes 128, 256, 512, 1024 and 2048 (16-byte
+ * aligned w and q_out), 2 one workgroup per row for one scale per row up to
+ * 16384 columns, 3 the per-group fallback.  No counterpart in the
+ * reference (testing and measurement). */
+int orth_pack_base_path(const void *w, int32_t w_dtype, int64_t in_features, int64_t group_size,
+                        const void *q_out);
+
+/* CSR of the nonzeros (w != 0: -0 dropped, NaN kept) of dense w
+ * [out_features, in_features], in two steps as
+ * pack_ortho_sparse(w, "csr"), /root/reference/tools/sieve.py:119-152:
+ * orth_pack_csr_rows_hip writes row_ptr int32 [out_features + 1] (0, then
+ * the running counts; -1 from the first row where the count passes
+ * 2^31 - 1); the caller reads nnz = row_ptr[out_features] and allocates;
+ * orth_pack_csr_fill_hip writes col_out int32 [nnz] (ascending within a
+ * row) and values_out [nnz] in value_dtype (bit copies when it is w's dtype,
+ * else rounded to nearest even). */
+int orth_pack_csr_rows_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                           int32_t *row_ptr, void *stream);
+int orth_pack_csr_fill_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                           const int32_t *row_ptr, int32_t *col_out, void *values_out, int32_t value_dtype,
+                           void *stream);
+
 /* Device facts.  Replaces check_tensor_core_support,
  * /root/reference/src/dual_gemm_tensor_core.cu:342-350. */
 typedef struct {

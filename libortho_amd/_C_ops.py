@@ -183,6 +183,68 @@ def dequant(q_weight, q_scales, in_features: int) -> torch.Tensor:
     return out
 
 
+def pack_base(base_weight: torch.Tensor, group_size=None, base_scales=None):
+    """INT4 quantisation and nibble packing of dense ``base_weight`` [N, K]
+    on the GPU: (q uint8 [N, K/2], scales float16 [N] or [N, K/G]), the
+    results of load_from_weights' torch ops on a GPU tensor
+    (/root/reference/torch_bind/ortho_linear.py:89-120)."""
+    dev = base_weight.device
+    _req(dev.type == "cuda", "pack_base needs the weights on a ROCm GPU")
+    _req(base_weight.dim() == 2 and base_weight.dtype in _DT,
+         "base_weight must be a 2-D float16, bfloat16 or float32 tensor")
+    w = base_weight.contiguous()
+    N, K = int(w.shape[0]), int(w.shape[1])
+    G = K if group_size is None else int(group_size)
+    _req(K % 2 == 0 and G > 0 and G % 2 == 0 and K % G == 0,
+         f"in_features ({K}) must be even and group_size ({G}) even and dividing it")
+    s_in = None
+    if base_scales is not None:
+        _req(base_scales.dtype in _DT and base_scales.device == dev and base_scales.numel() == N * (K // G),
+             "base_scales must be float16/bfloat16/float32 on the weights' device with N * K/G elements")
+        s_in = base_scales.contiguous()
+    q = torch.empty((N, K // 2), dtype=torch.uint8, device=dev)
+    scales = torch.empty((N,) if G == K else (N, K // G), dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().orth_pack_base_hip(
+            _ptr(w), _DT[w.dtype], N, K, G, _ptr(s_in) if s_in is not None else None,
+            _DT[s_in.dtype] if s_in is not None else 0, _ptr(q), _ptr(scales), _stream(dev)))
+    return q, scales
+
+
+def pack_base_path(base_weight: torch.Tensor, group_size, q: torch.Tensor) -> int:
+    """Kernel pack_base takes: 1 per-group waves, 2 per-row workgroups, 3 fallback."""
+    K = int(base_weight.shape[1])
+    return _lib.lib().orth_pack_base_path(_ptr(base_weight), _DT[base_weight.dtype], K,
+                                          K if group_size is None else int(group_size), _ptr(q))
+
+
+def pack_csr(ortho_weight: torch.Tensor, values_dtype=None):
+    """CSR of the nonzeros of dense ``ortho_weight`` [N, K] built on the GPU:
+    (row_ptr int32 [N+1], col int32 [nnz], values [nnz] in ``values_dtype``,
+    default the weight's dtype), as pack_ortho_sparse(W, "csr")
+    (/root/reference/tools/sieve.py:119-152).  Reads nnz back to the host."""
+    dev = ortho_weight.device
+    _req(dev.type == "cuda", "pack_csr needs the weights on a ROCm GPU")
+    _req(ortho_weight.dim() == 2 and ortho_weight.dtype in _DT,
+         "ortho_weight must be a 2-D float16, bfloat16 or float32 tensor")
+    w = ortho_weight.contiguous()
+    N, K = int(w.shape[0]), int(w.shape[1])
+    vdt = w.dtype if values_dtype is None else values_dtype
+    _req(vdt in _DT, f"values dtype {vdt} is not float16, bfloat16 or float32")
+    row_ptr = torch.empty(N + 1, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        L = _lib.lib()
+        _lib.check(L.orth_pack_csr_rows_hip(_ptr(w), _DT[w.dtype], N, K, _ptr(row_ptr), _stream(dev)))
+        nnz = int(row_ptr[N].item())  # synchronises the stream
+        _req(nnz >= 0, "more than 2^31 - 1 nonzeros")
+        col = torch.empty(nnz, dtype=torch.int32, device=dev)
+        vals = torch.empty(nnz, dtype=vdt, device=dev)
+        if nnz > 0:
+            _lib.check(L.orth_pack_csr_fill_hip(_ptr(w), _DT[w.dtype], N, K, _ptr(row_ptr), _ptr(col),
+                                                _ptr(vals), _DT[vdt], _stream(dev)))
+    return row_ptr, col, vals
+
+
 def last_kernel() -> str:
     """Kernel used by this thread's last forward: decode, skinny (5..64
     tokens), prefill or general."""

@@ -24,6 +24,12 @@
 namespace orth {
 hipError_t launch_general(const ForwardArgs &a, hipStream_t stream);
 hipError_t launch_dequant(const ForwardArgs &a, float *out, hipStream_t stream);
+hipError_t launch_pack_base(const void *w, int wdt, int64_t N, int64_t K, int64_t G, const void *s_in,
+                            int sdt, uint8_t *q, void *s_out, hipStream_t stream);
+int pack_base_path(const void *w, int wdt, int64_t K, int64_t G, const void *q);
+hipError_t launch_csr_rows(const void *w, int wdt, int64_t N, int64_t K, int32_t *row_ptr, hipStream_t stream);
+hipError_t launch_csr_fill(const void *w, int wdt, int64_t N, int64_t K, const int32_t *row_ptr, int32_t *col,
+                           void *vals, int vdt, hipStream_t stream);
 bool decode_supported(const ForwardArgs &a);
 hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream);
 bool prefill_supported(const ForwardArgs &a);
@@ -394,6 +400,72 @@ int orth_base_dequant_hip(const orth_hip_layer_t *layer, float *out, void *strea
     return ORTH_OK;
 }
 
+namespace {
+int check_pack_dims(const void *w, int32_t w_dtype, int64_t N, int64_t K) {
+    if (!w) return fail(ORTH_ERR_INVALID_ARGUMENT, "weights pointer is NULL");
+    if (!valid_dtype(w_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "weight dtype %d is not F16, BF16 or F32", w_dtype);
+    if (N <= 0 || K <= 0) return fail(ORTH_ERR_INVALID_ARGUMENT, "out_features and in_features must be positive");
+    if (K > ((int64_t)1 << 40) / N) return fail(ORTH_ERR_INVALID_ARGUMENT, "in_features * out_features is too large");
+    return ORTH_OK;
+}
+}  // namespace
+
+int orth_pack_base_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                       int64_t group_size, const void *scales_in, int32_t scales_in_dtype, void *q_out,
+                       void *scales_out, void *stream) {
+    int rc = check_pack_dims(w, w_dtype, out_features, in_features);
+    if (rc != ORTH_OK) return rc;
+    const int64_t K = in_features;
+    if (K & 1) return fail(ORTH_ERR_INVALID_ARGUMENT, "in_features must be even (got %lld)", (long long)K);
+    const int64_t G = group_size <= 0 ? K : group_size;
+    if ((G & 1) || K % G != 0)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "group_size (%lld) must be even and divide in_features (%lld)",
+                    (long long)G, (long long)K);
+    if (!q_out || !scales_out) return fail(ORTH_ERR_INVALID_ARGUMENT, "q_out or scales_out is NULL");
+    if (scales_in && !valid_dtype(scales_in_dtype))
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "scales_in dtype %d is not F16, BF16 or F32", scales_in_dtype);
+    rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipError_t e = launch_pack_base(w, w_dtype, out_features, K, G, scales_in, scales_in_dtype,
+                                    static_cast<uint8_t *>(q_out), scales_out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "base packing launch");
+    return ORTH_OK;
+}
+
+int orth_pack_base_path(const void *w, int32_t w_dtype, int64_t in_features, int64_t group_size,
+                        const void *q_out) {
+    const int64_t G = group_size <= 0 ? in_features : group_size;
+    return pack_base_path(w, w_dtype, in_features, G, q_out);
+}
+
+int orth_pack_csr_rows_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                           int32_t *row_ptr, void *stream) {
+    int rc = check_pack_dims(w, w_dtype, out_features, in_features);
+    if (rc != ORTH_OK) return rc;
+    if (!row_ptr) return fail(ORTH_ERR_INVALID_ARGUMENT, "row_ptr is NULL");
+    rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipError_t e = launch_csr_rows(w, w_dtype, out_features, in_features, row_ptr, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "CSR row count launch");
+    return ORTH_OK;
+}
+
+int orth_pack_csr_fill_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                           const int32_t *row_ptr, int32_t *col_out, void *values_out, int32_t value_dtype,
+                           void *stream) {
+    int rc = check_pack_dims(w, w_dtype, out_features, in_features);
+    if (rc != ORTH_OK) return rc;
+    if (!row_ptr) return fail(ORTH_ERR_INVALID_ARGUMENT, "row_ptr is NULL");
+    if (!valid_dtype(value_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "value dtype %d is not F16, BF16 or F32", value_dtype);
+    if (!col_out || !values_out) return fail(ORTH_ERR_INVALID_ARGUMENT, "col_out or values_out is NULL");
+    rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipError_t e = launch_csr_fill(w, w_dtype, out_features, in_features, row_ptr, col_out, values_out,
+                                   value_dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "CSR fill launch");
+    return ORTH_OK;
+}
+
 int orth_hip_device_info(int device, orth_hip_device_info_t *info) {
     if (!info) return fail(ORTH_ERR_INVALID_ARGUMENT, "info is NULL");
     std::memset(info, 0, sizeof(*info));
@@ -430,6 +502,6 @@ int orth_hip_last_kernel(void) { return t_last_kernel; }
 
 const char *orth_hip_last_error(void) { return t_error.c_str(); }
 
-int orth_hip_abi_version(void) { return 100; }
+int orth_hip_abi_version(void) { return 101; }
 
 }  // extern "C"

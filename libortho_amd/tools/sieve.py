@@ -11,8 +11,10 @@
       so it only addresses matrices of at most 65536 elements.
   anything else -> ValueError.
 
-It runs on whatever device ``w_ortho`` is on.  ``torch.nonzero`` already
-lists coordinates in row-major order, so no sort is needed.
+On a ROCm GPU the CSR is built by the library's packing kernels
+(``_C_ops.pack_csr``, same result bit for bit); elsewhere by torch ops
+(``torch.nonzero`` already lists coordinates in row-major order, so no sort
+is needed).
 """
 from __future__ import annotations
 
@@ -25,6 +27,14 @@ def pack_ortho_sparse(w_ortho: torch.Tensor, format: str = "csr"
                       ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     if w_ortho.dim() != 2:
         raise ValueError(f"w_ortho must be 2-D [out_features, in_features], got {tuple(w_ortho.shape)}")
+    if format == "csr" and w_ortho.is_cuda and w_ortho.dtype in (torch.float16, torch.bfloat16, torch.float32):
+        from .. import _C_ops
+        return _C_ops.pack_csr(w_ortho)
+    return pack_ortho_sparse_torch(w_ortho, format)
+
+
+def pack_ortho_sparse_torch(w_ortho: torch.Tensor, format: str = "csr"):
+    """The torch-op form of ``pack_ortho_sparse`` on any device."""
     out_features, in_features = w_ortho.shape
     mask = w_ortho != 0
     coords = torch.nonzero(mask, as_tuple=False)  # row-major order

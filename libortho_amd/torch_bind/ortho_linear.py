@@ -41,6 +41,28 @@ from ..tools.sieve import pack_ortho_sparse
 HAS_C_OPS = True  # the reference's flag (:15-28); this package has no fallback
 
 
+def pack_base_torch(base_weight: torch.Tensor, group_size: Optional[int] = None,
+                    base_scales: Optional[torch.Tensor] = None):
+    """The torch-op form of the Base packing of load_from_weights
+    (/root/reference/torch_bind/ortho_linear.py:89-120, plus group scales):
+    (q uint8 [N, K/2], scales float16 [N] or [N, K/G]) on base_weight's device."""
+    N, K = base_weight.shape
+    G = K if group_size is None else group_size
+    if base_scales is None:
+        grouped = base_weight.reshape(N, K // G, G)
+        scales = (grouped.abs().amax(dim=2) / 7.0).clamp(min=1e-6)
+        if group_size is None:
+            scales = scales.reshape(N)
+    else:
+        scales = base_scales
+    s_full = scales.reshape(N, -1).to(base_weight.device)
+    s_full = s_full.repeat_interleave(K // s_full.shape[1], dim=1)
+    w_int = (base_weight / s_full).round().clamp(-8, 7).to(torch.int8)
+    w_flat = w_int.flatten()
+    packed = (w_flat[0::2] & 0x0F) | ((w_flat[1::2] & 0x0F) << 4)
+    return packed.to(torch.uint8).view(N, -1), scales.to(dtype=torch.float16)
+
+
 class OrthoLinear(nn.Module):
     """Y = X @ W_base^T + alpha * (X @ W_ortho^T) (+ bias)."""
 
@@ -93,21 +115,14 @@ class OrthoLinear(nn.Module):
         N, K = self.out_features, self.in_features
         if tuple(base_weight.shape) != (N, K) or tuple(ortho_weight.shape) != (N, K):
             raise ValueError(f"weights must be [{N}, {K}]")
-        G = K if self.group_size is None else self.group_size
-        if base_scales is None:
-            grouped = base_weight.reshape(N, K // G, G)
-            scales = (grouped.abs().amax(dim=2) / 7.0).clamp(min=1e-6)
-            if self.group_size is None:
-                scales = scales.reshape(N)
+        if base_weight.is_cuda and base_weight.dtype in (torch.float16, torch.bfloat16, torch.float32) and \
+                (base_scales is None or base_scales.device == base_weight.device):
+            # the library's packing kernels: the same bits as the torch ops below
+            q, scales16 = _C.pack_base(base_weight, self.group_size, base_scales)
         else:
-            scales = base_scales
-        self.base_scales.data = scales.to(dtype=torch.float16, device=device)
-        s_full = scales.reshape(N, -1).to(base_weight.device)
-        s_full = s_full.repeat_interleave(K // s_full.shape[1], dim=1)
-        w_int = (base_weight / s_full).round().clamp(-8, 7).to(torch.int8)
-        w_flat = w_int.flatten()
-        packed = (w_flat[0::2] & 0x0F) | ((w_flat[1::2] & 0x0F) << 4)
-        self.base_weight.data = packed.to(torch.uint8).view(N, -1).to(device)
+            q, scales16 = pack_base_torch(base_weight, self.group_size, base_scales)
+        self.base_scales.data = scales16.to(device)
+        self.base_weight.data = q.to(device)
 
         row_ptr, col_indices, values = pack_ortho_sparse(ortho_weight, format="csr")
         self.ortho_row_ptr = row_ptr.to(device=device, dtype=torch.int32)
