@@ -119,6 +119,15 @@ int orth_layer_forward_hip_planned(const orth_hip_layer_t *layer, const void *pl
                                    int64_t plan_bytes, const void *input, void *output,
                                    int64_t batch_size, int32_t io_dtype, void *stream);
 
+/* Same, with the bias of OrthoLinear.forward fused into the output store:
+ * bias [out_features] (F16, BF16 or F32; NULL for none) is added as
+ * `output += bias` does after the kernel, /root/reference/torch_bind/
+ * ortho_linear.py:165-166: y = round(float(round(acc)) + bias[n]) in the
+ * output dtype, so the result has the same bits as the unfused add. */
+int orth_layer_forward_hip_ex(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
+                              const void *bias, int32_t bias_dtype, const void *input, void *output,
+                              int64_t batch_size, int32_t io_dtype, void *stream);
+
 /* Size in bytes of the ortho plan for this layer (0 when count == 0), or a
  * negative orth_status_t on invalid arguments. */
 int64_t orth_ortho_plan_bytes(const orth_hip_layer_t *layer);

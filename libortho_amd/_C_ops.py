@@ -128,17 +128,28 @@ def forward(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, 
 
 
 def forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input,
-                    output, alpha, plan) -> None:
-    """``forward`` with an ortho plan from :func:`build_plan` (or None)."""
+                    output, alpha, plan, bias=None) -> None:
+    """``forward`` with an ortho plan from :func:`build_plan` (or None) and,
+    optionally, the bias [N] fused into the store (the bits of ``output +=
+    bias`` after the kernel)."""
     _check_io(input, output)
     K, N = int(input.shape[1]), int(output.shape[1])
     dev = input.device
     layer = make_layer(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, K, N,
                        float(alpha), dev)
     L = _lib.lib()
+    has_plan = plan is not None and plan.numel() > 0
+    if has_plan:
+        _req(plan.device == dev and plan.dtype == torch.uint8, "plan must be a uint8 tensor on input's device")
     with torch.cuda.device(dev):
-        if plan is not None and plan.numel() > 0:
-            _req(plan.device == dev and plan.dtype == torch.uint8, "plan must be a uint8 tensor on input's device")
+        if bias is not None:
+            _req(bias.device == dev and bias.dtype in _DT and bias.numel() == N and bias.is_contiguous(),
+                 f"bias must be a contiguous float tensor of {N} elements on input's device")
+            rc = L.orth_layer_forward_hip_ex(ctypes.byref(layer), _ptr(plan) if has_plan else None,
+                                             plan.numel() if has_plan else 0, _ptr(bias), _DT[bias.dtype],
+                                             _ptr(input), _ptr(output), int(input.shape[0]),
+                                             _DT[input.dtype], _stream(dev))
+        elif has_plan:
             rc = L.orth_layer_forward_hip_planned(ctypes.byref(layer), _ptr(plan), plan.numel(),
                                                   _ptr(input), _ptr(output), int(input.shape[0]),
                                                   _DT[input.dtype], _stream(dev))

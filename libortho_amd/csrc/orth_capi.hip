@@ -242,10 +242,15 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part)
 }
 
 int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
-                 const void *input, void *output, int64_t batch, int32_t io_dtype, void *stream_v) {
+                 const void *input, void *output, int64_t batch, int32_t io_dtype, void *stream_v,
+                 const void *bias = nullptr, int32_t bias_dtype = ORTH_DT_F32) {
     ForwardArgs a;
     int rc = resolve(layer, input, output, batch, io_dtype, true, a);
     if (rc != ORTH_OK) return rc;
+    if (bias && !valid_dtype(bias_dtype))
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "bias dtype %d is not F16, BF16 or F32", bias_dtype);
+    a.bias = bias;
+    a.bias_dtype = bias_dtype;
     if (plan && plan_bytes < plan_bytes_for(a.N, a.K, a.nnz))
         return fail(ORTH_ERR_INVALID_ARGUMENT, "plan_bytes %lld is smaller than the plan size %lld",
                     (long long)plan_bytes, (long long)plan_bytes_for(a.N, a.K, a.nnz));
@@ -349,6 +354,13 @@ int orth_layer_forward_hip_planned(const orth_hip_layer_t *layer, const void *pl
                                    int64_t plan_bytes, const void *input, void *output,
                                    int64_t batch_size, int32_t io_dtype, void *stream) {
     return forward_impl(layer, plan, plan_bytes, input, output, batch_size, io_dtype, stream);
+}
+
+int orth_layer_forward_hip_ex(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
+                              const void *bias, int32_t bias_dtype, const void *input, void *output,
+                              int64_t batch_size, int32_t io_dtype, void *stream) {
+    return forward_impl(layer, plan, plan_bytes, input, output, batch_size, io_dtype, stream, bias,
+                        bias_dtype);
 }
 
 int64_t orth_ortho_plan_bytes(const orth_hip_layer_t *layer) {

@@ -42,6 +42,8 @@ struct ForwardArgs {
     int64_t M, K, N;
     float alpha;
     int has_ortho;           // alpha > 0 && nnz > 0 (/root/reference/src/ortho.c:343)
+    const void *bias = nullptr;  // [N] added to y after rounding, or null
+    int bias_dtype = 0;
 };
 
 // ---------------------------------------------------------------- scalars
@@ -69,6 +71,23 @@ __device__ __forceinline__ void store_from_f32(void *p, int dtype, int64_t i, fl
     if (dtype == ORTH_DT_F16) ((f16 *)p)[i] = (f16)v;
     else if (dtype == ORTH_DT_BF16) ((uint16_t *)p)[i] = f32_to_bf16_bits(v);
     else ((float *)p)[i] = v;
+}
+
+// v rounded to the precision of an orth_dtype_t (nearest even), as float.
+__device__ __forceinline__ float round_as(int dtype, float v) {
+    if (dtype == ORTH_DT_F16) return (float)(f16)v;
+    if (dtype == ORTH_DT_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+    return v;
+}
+
+// An FP16 output with the optional bias: y = fp16(float(fp16(v)) + bias[n]),
+// the bits of the kernel's FP16 output followed by `y += bias` in torch
+// (/root/reference/torch_bind/ortho_linear.py:165-166: the sum in FP32,
+// rounded to y's dtype).
+__device__ __forceinline__ f16 out_f16(float v, const void *bias, int bias_dtype, int64_t n) {
+    f16 r = (f16)v;
+    if (bias) r = (f16)((float)r + load_as_f32(bias, bias_dtype, n));
+    return r;
 }
 
 // Sign-extend a 4-bit two's complement nibble.

@@ -80,6 +80,8 @@ struct DecodeArgs {
     const uint32_t *rec;   // plan quarter records: qwords words per (16-row block, wave)
     int qwords;            // a multiple of 256, at most 2048; 0 without a plan
     int deep;              // (host) fewer than two workgroups per CU: deeper weight prefetch
+    const void *bias;      // [N] added after rounding (out_f16), or null
+    int bias_dtype;
 };
 
 // Weights pass through LDS (whole-line loads, transposed on the way) for
@@ -655,7 +657,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 for (int w = 0; w < W; w++) v += red(w)[m * 16 + rl];
                 if (!GROUPED) v *= (float)srow;
                 v += a.alpha * s;
-                a.y[(int64_t)m * a.N + n] = (f16)v;
+                a.y[(int64_t)m * a.N + n] = out_f16(v, a.bias, a.bias_dtype, n);
             }
         }
         return;
@@ -677,7 +679,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 for (int w = 0; w < W; w++) sp += (reinterpret_cast<const float *>(smem + a.lds_e) + w * a.qwords)[m * 16 + r];
                 v += a.alpha * sp;
             }
-            a.y[(int64_t)m * a.N + n] = (f16)v;
+            a.y[(int64_t)m * a.N + n] = out_f16(v, a.bias, a.bias_dtype, n);
         }
     }
 }
@@ -828,6 +830,8 @@ hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStr
                 ((reinterpret_cast<uintptr_t>(a.vals) & 7) == 0);
     d.x = static_cast<const f16 *>(a.x);
     d.y = static_cast<f16 *>(a.y);
+    d.bias = a.bias;
+    d.bias_dtype = a.bias_dtype;
     d.M = (int)a.M;
     d.nchunks = (int)(a.K / 128);
     d.K = (int)a.K;

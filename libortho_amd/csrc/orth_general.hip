@@ -49,6 +49,8 @@ __global__ void __launch_bounds__(256) general_kernel(ForwardArgs a) {
         sp = wave_sum(sp);
         if (lane == 0) {
             if (a.has_ortho) acc += a.alpha * sp;
+            // with a bias: y rounded, then y + bias in FP32 rounded (as out_f16)
+            if (a.bias) acc = round_as(a.io_dtype, acc) + load_as_f32(a.bias, a.bias_dtype, n);
             store_from_f32(a.y, a.io_dtype, m * a.N + n, acc);
         }
     }

@@ -32,11 +32,7 @@ namespace {
 
 constexpr int kPackNT = 256;  // threads per workgroup (4 waves)
 
-__device__ __forceinline__ float round_to(int dt, float v) {
-    if (dt == ORTH_DT_F16) return (float)(f16)v;
-    if (dt == ORTH_DT_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
-    return v;
-}
+__device__ __forceinline__ float round_to(int dt, float v) { return round_as(dt, v); }
 
 // |v| as bits: for non-negative floats the integer order is the float order,
 // and NaN patterns sort above +inf, so a max over these bits propagates NaN

@@ -368,6 +368,8 @@ struct PrefillArgs {
     const int32_t *offsets;   // [nblocks][nksteps+1]
     const uint32_t *entries;
     int nbm, nbn;             // tile grid
+    const void *bias;  // [N] added after rounding (out_f16), or null
+    int bias_dtype;
 };
 
 constexpr int PF_BM = 256, PF_BN = 128, PF_BK = 64;
@@ -651,7 +653,7 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int64_t m = m0 + wm * 64 + bm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                if (m < a.M && n < a.N) a.y[m * a.N + n] = (f16)acc[bm][bn][i];
+                if (m < a.M && n < a.N) a.y[m * a.N + n] = out_f16(acc[bm][bn][i], a.bias, a.bias_dtype, n);
             }
         }
     }
@@ -679,6 +681,8 @@ hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t st
     p.G = a.G;
     p.x = static_cast<const f16 *>(a.x);
     p.y = static_cast<f16 *>(a.y);
+    p.bias = a.bias;
+    p.bias_dtype = a.bias_dtype;
     p.M = a.M;
     p.K = a.K;
     p.N = a.N;

@@ -97,6 +97,8 @@ struct SkinnyArgs {
     int swords;
     int nslices;         // K / 1024
     int lds_sr;          // SPK >= 3: per-wave record regions
+    const void *bias;  // [N] added after rounding (out_f16), or null
+    int bias_dtype;
 };
 
 // GMODE: 0 per-row scale (G == K); 1 G = 128, scales read as aligned pairs;
@@ -531,7 +533,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = tt * 16 + 4 * g + i;
-                if (m < a.M && n < a.N) a.y[(int64_t)m * a.N + n] = (f16)val[tt][i];
+                if (m < a.M && n < a.N) a.y[(int64_t)m * a.N + n] = out_f16(val[tt][i], a.bias, a.bias_dtype, n);
             }
         return;
     }
@@ -550,7 +552,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
 // y = sum of the S partials, in slice order.  Thread t takes 4 consecutive
 // outputs of one token (N % 4 == 0) or one output (otherwise).
 __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f16 *y, int M, int64_t N, int S,
-                                                            int vec4) {
+                                                            int vec4, const void *bias, int bias_dtype) {
     // workgroup blk (on XCD blk % 8, like the slices of row block blk) adds
     // the S partials of rows [128 blk, 128 blk + 128) for every token.  The
     // loads of a group of 8 slices are issued before the first add (addresses
@@ -576,7 +578,8 @@ __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f
                     else if (s0 + u < S) v += w[u];
                 }
             }
-            const f16x2 lo = {(f16)v[0], (f16)v[1]}, hi = {(f16)v[2], (f16)v[3]};
+            const f16x2 lo = {out_f16(v[0], bias, bias_dtype, n), out_f16(v[1], bias, bias_dtype, n + 1)};
+            const f16x2 hi = {out_f16(v[2], bias, bias_dtype, n + 2), out_f16(v[3], bias, bias_dtype, n + 3)};
             *reinterpret_cast<uint2 *>(y + o) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
         }
     } else {
@@ -596,7 +599,7 @@ __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f
                     else if (s0 + u < S) v += w[u];
                 }
             }
-            y[o] = (f16)v;
+            y[o] = out_f16(v, bias, bias_dtype, n);
         }
     }
 }
@@ -728,6 +731,8 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     d.nnz = (int32_t)a.nnz;
     d.x = static_cast<const f16 *>(a.x);
     d.y = static_cast<f16 *>(a.y);
+    d.bias = a.bias;
+    d.bias_dtype = a.bias_dtype;
     d.M = (int)a.M;
     d.K = (int)a.K;
     d.N = a.N;
@@ -773,7 +778,7 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     if (e != hipSuccess || sh.S == 1) return e;
     const int vec4 = (a.N % 4 == 0) ? 1 : 0;
     hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)sh.nblocks), dim3(256), 0, stream, part,
-                       static_cast<f16 *>(a.y), (int)a.M, a.N, sh.S, vec4);
+                       static_cast<f16 *>(a.y), (int)a.M, a.N, sh.S, vec4, a.bias, a.bias_dtype);
     return hipGetLastError();
 }
 

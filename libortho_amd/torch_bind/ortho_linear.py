@@ -41,6 +41,17 @@ from ..tools.sieve import pack_ortho_sparse
 HAS_C_OPS = True  # the reference's flag (:15-28); this package has no fallback
 
 
+def load_checkpoint(model: nn.Module, path, map_location=None, strict: bool = True):
+    """Loads a ``torch.save``d state_dict (from this package or from the
+    reference's OrthoLinear modules) into ``model``.  The file is read with
+    ``weights_only=True``: tensors and plain containers only, nothing in it
+    is executed."""
+    sd = torch.load(path, map_location=map_location, weights_only=True)
+    if isinstance(sd, dict) and "state_dict" in sd and isinstance(sd["state_dict"], dict):
+        sd = sd["state_dict"]
+    return model.load_state_dict(sd, strict=strict)
+
+
 def pack_base_torch(base_weight: torch.Tensor, group_size: Optional[int] = None,
                     base_scales: Optional[torch.Tensor] = None):
     """The torch-op form of the Base packing of load_from_weights
@@ -164,12 +175,84 @@ class OrthoLinear(nn.Module):
         plan = None
         if self.alpha > 0:
             plan = self._ortho_plan()
+        # the bias is fused into the kernel's store (same bits as `output +=
+        # bias`) unless autograd must see the add
+        fuse = self.bias is not None and not (torch.is_grad_enabled() and self.bias.requires_grad) and \
+            self.bias.device == x.device
         _C.forward_planned(self.base_weight, self.base_scales, self.ortho_values,
                            self.ortho_col_indices, self.ortho_row_ptr, x_flat.contiguous(), output,
-                           self.alpha, plan)
-        if self.bias is not None:
+                           self.alpha, plan, bias=self.bias.detach().contiguous() if fuse else None)
+        if self.bias is not None and not fuse:
             output += self.bias
         return output.view(*original_shape[:-1], self.out_features)
+
+    # ------------------------------------------------------------ checkpoints
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        """Loads packed checkpoints of any nnz and either scale layout.
+
+        The reference's buffers start empty and are replaced when weights are
+        packed (/root/reference/torch_bind/ortho_linear.py:59-65,123-128), so
+        its saved CSR has a length a fresh module cannot know: the three CSR
+        buffers take the checkpoint's lengths (validated: row_ptr has
+        out_features + 1 entries, 0 first, nnz last).  ``base_scales`` may be
+        [out] (the reference layout: per-row scales) or [out, in/G]; the
+        module takes the checkpoint's layout and sets ``group_size`` to
+        match.  ``base_weight`` must be [out, in/2]."""
+        N, K = self.out_features, self.in_features
+        dev = self.base_weight.device
+
+        def get(name):
+            return state_dict.get(prefix + name)
+
+        bw = get("base_weight")
+        if bw is not None and tuple(bw.shape) != (N, K // 2):
+            error_msgs.append(f"{prefix}base_weight: expected [{N}, {K // 2}] packed INT4, got {list(bw.shape)}")
+            return
+        bs = get("base_scales")
+        if bs is not None:
+            if bs.dim() == 1 and bs.shape[0] == N:
+                self.group_size = None
+            elif bs.dim() == 2 and bs.shape[0] == N and bs.shape[1] > 0 and K % bs.shape[1] == 0:
+                self.group_size = K // int(bs.shape[1])
+            else:
+                error_msgs.append(f"{prefix}base_scales: expected [{N}] or [{N}, in/G], got {list(bs.shape)}")
+                return
+            self.base_scales = torch.zeros(tuple(bs.shape), dtype=torch.float16, device=dev)
+        vals, col, rp = get("ortho_values"), get("ortho_col_indices"), get("ortho_row_ptr")
+        if vals is not None or col is not None or rp is not None:
+            if vals is None or col is None or rp is None:
+                error_msgs.append(f"{prefix}ortho_*: the three CSR buffers must be saved together")
+                return
+            nnz = int(vals.numel())
+            ok = col.numel() == nnz and (rp.numel() == N + 1 or (nnz == 0 and rp.numel() in (0, N + 1)))
+            if ok and rp.numel() == N + 1:
+                ok = int(rp[0]) == 0 and int(rp[-1]) == nnz
+            if not ok:
+                error_msgs.append(f"{prefix}ortho CSR: row_ptr must have {N + 1} entries from 0 to nnz and "
+                                  f"col_indices nnz entries (got {rp.numel()}, {col.numel()}, nnz {nnz})")
+                return
+            self.ortho_values = torch.zeros(nnz, dtype=torch.float16, device=dev)
+            self.ortho_col_indices = torch.zeros(nnz, dtype=torch.int32, device=dev)
+            self.ortho_row_ptr = torch.zeros(rp.numel(), dtype=torch.int32, device=dev)
+        self._plan = None
+        self._plan_key = None
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
+
+    @torch.no_grad()
+    def expand_scales(self, group_size: int = 128) -> "OrthoLinear":
+        """Per-row scales (the reference layout) to ``group_size`` groups:
+        each row's scale repeated over its groups, so every dequantised weight
+        float(q) * float(s) is unchanged."""
+        K = self.in_features
+        if self.group_size is not None:
+            raise ValueError("base_scales are already per group")
+        if group_size <= 0 or K % group_size != 0:
+            raise ValueError(f"group_size {group_size} must divide in_features {K}")
+        self.base_scales = self.base_scales.reshape(-1, 1).repeat(1, K // group_size).contiguous()
+        self.group_size = group_size
+        return self
 
     def extra_repr(self) -> str:
         g = "row" if self.group_size is None else self.group_size

@@ -163,3 +163,33 @@ def test_load_from_weights_on_the_gpu_uses_the_kernels():
         assert np.array_equal(bits(layer.ortho_row_ptr), bits(rp_t))
         assert np.array_equal(bits(layer.ortho_col_indices), bits(col_t))
         assert np.array_equal(bits(layer.ortho_values), bits(vals_t.to(torch.float16)))
+
+
+def test_reference_checkpoint_forward_on_the_gpu(tmp_path, oracle_mod):
+    # a reference-layout checkpoint (per-row FP16 scales, CSR, FP32 bias)
+    # loaded with load_checkpoint onto the GPU; the forward (bias added after,
+    # as the reference) against the FP64 oracle, before and after the
+    # per-row scales are expanded to groups of 128
+    from libortho_amd import workloads as W
+    from libortho_amd.torch_bind import load_checkpoint
+    K, N = 1024, 320
+    lay = W.make_layer(K, N, None, 0.02, 1234)
+    bias = (torch.arange(N, dtype=torch.float32) * 0.001)
+    sd = {"base_weight": torch.from_numpy(lay.q.copy()), "base_scales": torch.from_numpy(lay.scales.copy()),
+          "ortho_values": torch.from_numpy(lay.vals.copy()),
+          "ortho_col_indices": torch.from_numpy(lay.col.copy()),
+          "ortho_row_ptr": torch.from_numpy(lay.row_ptr.copy()), "bias": bias}
+    path = tmp_path / "ref.pt"
+    torch.save(sd, path)
+    m = OrthoLinear(K, N, bias=True)
+    load_checkpoint(m, path, map_location="cuda")
+    m = m.cuda()
+    x_np = W.make_x(3, K, 99)
+    ref = oracle_mod.forward_f64(lay.q, lay.scales, lay.row_ptr, lay.col, lay.vals, x_np, 1.0) + bias.numpy()
+    for expand in (False, True):
+        if expand:
+            m.expand_scales(128)
+        with torch.no_grad():  # (the bias is fused into the store)
+            y = m(torch.from_numpy(x_np).cuda()).float().cpu().numpy()
+        err = float(np.abs(y - ref).max())
+        assert err <= 1e-2 * float(np.abs(ref).max()), f"expand={expand}: {err}"
