@@ -266,11 +266,12 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
     const int policy = g_policy.load(std::memory_order_relaxed);
     const bool dec_ok = decode_supported(a);
     const bool pre_ok = prefill_supported(a);
-    // the mid-batch kernel locates each row's ortho entries with the plan's
-    // chunk table; without a plan it filters whole rows, so batches the
-    // decode kernel takes go there instead
+    // the mid-batch kernel reads each row's ortho entries through the plan;
+    // without one it filters whole rows by column, which still beats the
+    // decode kernel from 9 tokens (c2: 26.5 against 29.2 us at 12 tokens,
+    // 26.7 against 33.9 at 16) but not up to 8 (21.7 against 19.3-21.0)
     const bool sk_ok = skinny_supported(a);
-    const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok);
+    const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok || a.M > 8);
     int kernel;
     switch (policy) {
         case 1:

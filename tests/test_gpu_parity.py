@@ -91,8 +91,8 @@ def test_dequant_odd_groups_bit_exact(oracle_mod):
 def auto_kernel(M, planned=False):
     """Kernel the dispatcher picks for fp16 I/O on the fast-path shapes: the
     mid-batch kernel reads the ortho plan, so without one (and with an ortho
-    term) batches up to 16 stay on the decode kernel."""
-    if M <= 4 or (M <= 16 and not planned):
+    term) batches up to 8 stay on the decode kernel."""
+    if M <= 4 or (M <= 8 and not planned):
         return "decode"
     return "skinny" if M <= 64 else "prefill"
 
