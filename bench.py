@@ -225,16 +225,19 @@ def time_pack(torch, steps=30):
         w[idx] = torch.randn(nnz, device="cuda", generator=gen) + 3.0
         wo.append(w.view(N, K))
     rps = [torch.empty(N + 1, dtype=torch.int32, device="cuda") for _ in range(copies)]
+    mb = int(L.orth_pack_csr_mask_bytes(P(wo[0]), _lib.DT_F32, N, K))  # the nonzero mask (5.6 MB)
+    masks = [torch.empty(mb, dtype=torch.uint8, device="cuda") for _ in range(copies)]
     for i in range(copies):
-        _lib.check(L.orth_pack_csr_rows_hip(P(wo[i]), _lib.DT_F32, N, K, P(rps[i]), S()))
+        _lib.check(L.orth_pack_csr_rows_hip(P(wo[i]), _lib.DT_F32, N, K, P(rps[i]), P(masks[i]), mb, S()))
     torch.cuda.synchronize()
     assert all(int(r[N]) == nnz for r in rps)
     col = torch.empty(nnz, dtype=torch.int32, device="cuda")
     vals = torch.empty(nnz, dtype=torch.float32, device="cuda")
     ms_rows = graph_time(torch, lambda i: _lib.check(L.orth_pack_csr_rows_hip(
-        P(wo[i % copies]), _lib.DT_F32, N, K, P(rps[i % copies]), S())), steps)
+        P(wo[i % copies]), _lib.DT_F32, N, K, P(rps[i % copies]), P(masks[i % copies]), mb, S())), steps)
     ms_fill = graph_time(torch, lambda i: _lib.check(L.orth_pack_csr_fill_hip(
-        P(wo[i % copies]), _lib.DT_F32, N, K, P(rps[i % copies]), P(col), P(vals), _lib.DT_F32, S())), steps)
+        P(wo[i % copies]), _lib.DT_F32, N, K, P(rps[i % copies]), P(masks[i % copies]), mb, P(col), P(vals),
+        _lib.DT_F32, S())), steps)
     b = N * K * 4 + 4 * (N + 1) + 8 * nnz
     ms = ms_rows + ms_fill
     out.append({"workload": "pack csr c2 fp32 1 %", "kernel": "csr_count+csr_scan, csr_fill",

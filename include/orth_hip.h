@@ -181,12 +181,18 @@ int orth_pack_base_path(const void *w, int32_t w_dtype, int64_t in_features, int
  * 2^31 - 1); the caller reads nnz = row_ptr[out_features] and allocates;
  * orth_pack_csr_fill_hip writes col_out int32 [nnz] (ascending within a
  * row) and values_out [nnz] in value_dtype (bit copies when it is w's dtype,
- * else rounded to nearest even). */
+ * else rounded to nearest even).  mask: optional device workspace of
+ * orth_pack_csr_mask_bytes bytes (0: none for these weights, pass NULL)
+ * where the first step records each element's nonzero bit, so that the
+ * second reads only the nonzero elements of w instead of all of it; the
+ * same mask must be passed to both steps (or NULL to both).  No reference
+ * counterpart for the mask. */
+int64_t orth_pack_csr_mask_bytes(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features);
 int orth_pack_csr_rows_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
-                           int32_t *row_ptr, void *stream);
+                           int32_t *row_ptr, void *mask, int64_t mask_bytes, void *stream);
 int orth_pack_csr_fill_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
-                           const int32_t *row_ptr, int32_t *col_out, void *values_out, int32_t value_dtype,
-                           void *stream);
+                           const int32_t *row_ptr, const void *mask, int64_t mask_bytes, int32_t *col_out,
+                           void *values_out, int32_t value_dtype, void *stream);
 
 /* Device facts.  Replaces check_tensor_core_support,
  * /root/reference/src/dual_gemm_tensor_core.cu:342-350. */

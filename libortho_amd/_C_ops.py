@@ -229,11 +229,13 @@ def pack_base_path(base_weight: torch.Tensor, group_size, q: torch.Tensor) -> in
                                           K if group_size is None else int(group_size), _ptr(q))
 
 
-def pack_csr(ortho_weight: torch.Tensor, values_dtype=None):
+def pack_csr(ortho_weight: torch.Tensor, values_dtype=None, use_mask: bool = True):
     """CSR of the nonzeros of dense ``ortho_weight`` [N, K] built on the GPU:
     (row_ptr int32 [N+1], col int32 [nnz], values [nnz] in ``values_dtype``,
     default the weight's dtype), as pack_ortho_sparse(W, "csr")
-    (/root/reference/tools/sieve.py:119-152).  Reads nnz back to the host."""
+    (/root/reference/tools/sieve.py:119-152).  Reads nnz back to the host.
+    With ``use_mask`` the first pass records the nonzero pattern in a
+    temporary mask and the second reads only the nonzero elements."""
     dev = ortho_weight.device
     _req(dev.type == "cuda", "pack_csr needs the weights on a ROCm GPU")
     _req(ortho_weight.dim() == 2 and ortho_weight.dtype in _DT,
@@ -245,13 +247,17 @@ def pack_csr(ortho_weight: torch.Tensor, values_dtype=None):
     row_ptr = torch.empty(N + 1, dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         L = _lib.lib()
-        _lib.check(L.orth_pack_csr_rows_hip(_ptr(w), _DT[w.dtype], N, K, _ptr(row_ptr), _stream(dev)))
+        mb = int(L.orth_pack_csr_mask_bytes(_ptr(w), _DT[w.dtype], N, K)) if use_mask else 0
+        _req(mb >= 0, _lib.last_error())
+        mask = torch.empty(mb, dtype=torch.uint8, device=dev) if mb > 0 else None
+        mp = _ptr(mask) if mask is not None else None
+        _lib.check(L.orth_pack_csr_rows_hip(_ptr(w), _DT[w.dtype], N, K, _ptr(row_ptr), mp, mb, _stream(dev)))
         nnz = int(row_ptr[N].item())  # synchronises the stream
         _req(nnz >= 0, "more than 2^31 - 1 nonzeros")
         col = torch.empty(nnz, dtype=torch.int32, device=dev)
         vals = torch.empty(nnz, dtype=vdt, device=dev)
         if nnz > 0:
-            _lib.check(L.orth_pack_csr_fill_hip(_ptr(w), _DT[w.dtype], N, K, _ptr(row_ptr), _ptr(col),
+            _lib.check(L.orth_pack_csr_fill_hip(_ptr(w), _DT[w.dtype], N, K, _ptr(row_ptr), mp, mb, _ptr(col),
                                                 _ptr(vals), _DT[vdt], _stream(dev)))
     return row_ptr, col, vals
 

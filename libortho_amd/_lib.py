@@ -64,8 +64,9 @@ SIGNATURES = {
     "orth_base_dequant_hip": (ctypes.c_int, [_LP, _P, _P]),
     "orth_pack_base_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _I32, _P, _P, _P]),
     "orth_pack_base_path": (ctypes.c_int, [_P, _I32, _I64, _I64, _P]),
-    "orth_pack_csr_rows_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P]),
-    "orth_pack_csr_fill_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _P, _I32, _P]),
+    "orth_pack_csr_mask_bytes": (_I64, [_P, _I32, _I64, _I64]),
+    "orth_pack_csr_rows_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _I64, _P]),
+    "orth_pack_csr_fill_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _I64, _P, _P, _I32, _P]),
     "orth_hip_device_info": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(OrthHipDeviceInfo)]),
     "orth_hip_set_kernel_policy": (ctypes.c_int, [ctypes.c_int]),
     "orth_hip_get_kernel_policy": (ctypes.c_int, []),

@@ -27,9 +27,11 @@ hipError_t launch_dequant(const ForwardArgs &a, float *out, hipStream_t stream);
 hipError_t launch_pack_base(const void *w, int wdt, int64_t N, int64_t K, int64_t G, const void *s_in,
                             int sdt, uint8_t *q, void *s_out, hipStream_t stream);
 int pack_base_path(const void *w, int wdt, int64_t K, int64_t G, const void *q);
-hipError_t launch_csr_rows(const void *w, int wdt, int64_t N, int64_t K, int32_t *row_ptr, hipStream_t stream);
-hipError_t launch_csr_fill(const void *w, int wdt, int64_t N, int64_t K, const int32_t *row_ptr, int32_t *col,
-                           void *vals, int vdt, hipStream_t stream);
+int64_t csr_mask_bytes(const void *w, int wdt, int64_t N, int64_t K);
+hipError_t launch_csr_rows(const void *w, int wdt, int64_t N, int64_t K, int32_t *row_ptr, void *mask,
+                           hipStream_t stream);
+hipError_t launch_csr_fill(const void *w, int wdt, int64_t N, int64_t K, const int32_t *row_ptr,
+                           const void *mask, int32_t *col, void *vals, int vdt, hipStream_t stream);
 bool decode_supported(const ForwardArgs &a);
 hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream);
 bool prefill_supported(const ForwardArgs &a);
@@ -451,29 +453,52 @@ int orth_pack_base_path(const void *w, int32_t w_dtype, int64_t in_features, int
     return pack_base_path(w, w_dtype, in_features, G, q_out);
 }
 
+int64_t orth_pack_csr_mask_bytes(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features) {
+    int rc = check_pack_dims(w, w_dtype, out_features, in_features);
+    if (rc != ORTH_OK) return -rc;
+    return csr_mask_bytes(w, w_dtype, out_features, in_features);
+}
+
+namespace {
+int check_mask(const void *w, int32_t w_dtype, int64_t N, int64_t K, const void *mask, int64_t mask_bytes) {
+    if (!mask) return ORTH_OK;
+    const int64_t need = csr_mask_bytes(w, w_dtype, N, K);
+    if (need == 0) return fail(ORTH_ERR_INVALID_ARGUMENT, "no nonzero mask for these weights (pass NULL)");
+    if (mask_bytes < need)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "mask_bytes %lld is smaller than %lld", (long long)mask_bytes,
+                    (long long)need);
+    return ORTH_OK;
+}
+}  // namespace
+
 int orth_pack_csr_rows_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
-                           int32_t *row_ptr, void *stream) {
+                           int32_t *row_ptr, void *mask, int64_t mask_bytes, void *stream) {
     int rc = check_pack_dims(w, w_dtype, out_features, in_features);
     if (rc != ORTH_OK) return rc;
     if (!row_ptr) return fail(ORTH_ERR_INVALID_ARGUMENT, "row_ptr is NULL");
+    rc = check_mask(w, w_dtype, out_features, in_features, mask, mask_bytes);
+    if (rc != ORTH_OK) return rc;
     rc = current_device_ok(nullptr);
     if (rc != ORTH_OK) return rc;
-    hipError_t e = launch_csr_rows(w, w_dtype, out_features, in_features, row_ptr, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_csr_rows(w, w_dtype, out_features, in_features, row_ptr, mask,
+                                   static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail_hip(e, "CSR row count launch");
     return ORTH_OK;
 }
 
 int orth_pack_csr_fill_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
-                           const int32_t *row_ptr, int32_t *col_out, void *values_out, int32_t value_dtype,
-                           void *stream) {
+                           const int32_t *row_ptr, const void *mask, int64_t mask_bytes, int32_t *col_out,
+                           void *values_out, int32_t value_dtype, void *stream) {
     int rc = check_pack_dims(w, w_dtype, out_features, in_features);
     if (rc != ORTH_OK) return rc;
     if (!row_ptr) return fail(ORTH_ERR_INVALID_ARGUMENT, "row_ptr is NULL");
+    rc = check_mask(w, w_dtype, out_features, in_features, mask, mask_bytes);
+    if (rc != ORTH_OK) return rc;
     if (!valid_dtype(value_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "value dtype %d is not F16, BF16 or F32", value_dtype);
     if (!col_out || !values_out) return fail(ORTH_ERR_INVALID_ARGUMENT, "col_out or values_out is NULL");
     rc = current_device_ok(nullptr);
     if (rc != ORTH_OK) return rc;
-    hipError_t e = launch_csr_fill(w, w_dtype, out_features, in_features, row_ptr, col_out, values_out,
+    hipError_t e = launch_csr_fill(w, w_dtype, out_features, in_features, row_ptr, mask, col_out, values_out,
                                    value_dtype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail_hip(e, "CSR fill launch");
     return ORTH_OK;

@@ -238,10 +238,14 @@ __global__ void __launch_bounds__(kPackNT) pack_generic_kernel(PackBaseArgs a) {
 
 // ---- CSR
 
+// words of the nonzero mask of one row: 8 per step of 256 elements
+__host__ __device__ inline int64_t csr_mask_words(int64_t K) { return (K + 255) / 256 * 8; }
+
 // row_ptr[n + 1] = nonzeros of row n (one wave per row); row_ptr[0] = 0.
 // V elements per lane per step (vector loads when V > 1).
 template <int DT, int V>
-__global__ void __launch_bounds__(kPackNT) csr_count_kernel(const void *w, int64_t N, int64_t K, int32_t *row_ptr) {
+__global__ void __launch_bounds__(kPackNT) csr_count_kernel(const void *w, int64_t N, int64_t K, int32_t *row_ptr,
+                                                            uint32_t *mask) {
     using E = Elem<DT>;
     constexpr int NW = V * E::kSize / 4 > 0 ? V * E::kSize / 4 : 1;
     const int64_t n = (int64_t)blockIdx.x * (kPackNT / 64) + (threadIdx.x >> 6);
@@ -256,18 +260,34 @@ __global__ void __launch_bounds__(kPackNT) csr_count_kernel(const void *w, int64
             cnt += E::nonzero(wd, 0) ? 1 : 0;
         }
     } else {
-        // U steps' loads issued together (addresses clamped into the row,
-        // elements past it not counted)
+        // U steps of 64 * V elements, their loads issued together (addresses
+        // clamped into the row, elements past it not counted).  With a mask
+        // (V == 4) each step's nonzero pattern is kept, lane l's 4 bits at
+        // bits 4 (l % 8) of word l / 8 of the step's 8 words.
         constexpr int U = 4;
-        for (int64_t k0 = (int64_t)lane * V; k0 < K; k0 += 64 * V * U) {
+        uint32_t *mrow = mask ? mask + n * csr_mask_words(K) : nullptr;
+        for (int64_t kb = 0; kb < K; kb += 64 * V * U) {
             uint32_t wd[U][NW];
 #pragma unroll
             for (int u = 0; u < U; u++)
-                load_words<NW>(reinterpret_cast<const uint32_t *>(row + min(k0 + 64 * V * u, K - V) * E::kSize), wd[u]);
+                load_words<NW>(reinterpret_cast<const uint32_t *>(
+                                   row + min(kb + 64 * V * u + (int64_t)lane * V, K - V) * E::kSize), wd[u]);
 #pragma unroll
-            for (int u = 0; u < U; u++)
+            for (int u = 0; u < U; u++) {
+                const int64_t k = kb + 64 * V * u + (int64_t)lane * V;
+                uint32_t nib = 0u;
 #pragma unroll
-                for (int j = 0; j < V; j++) cnt += (k0 + 64 * V * u < K && E::nonzero(wd[u], j)) ? 1 : 0;
+                for (int j = 0; j < V; j++) nib |= (k + j < K && E::nonzero(wd[u], j)) ? (1u << j) : 0u;
+                cnt += __builtin_popcount(nib);
+                if (V == 4 && mrow) {  // (uniform)
+                    uint32_t m = nib << (4 * (lane & 7));
+                    m |= (uint32_t)__shfl_xor((int)m, 1);
+                    m |= (uint32_t)__shfl_xor((int)m, 2);
+                    m |= (uint32_t)__shfl_xor((int)m, 4);
+                    const int64_t st = kb / (64 * V) + u;
+                    if ((lane & 7) == 0 && st * 64 * V < K) mrow[st * 8 + (lane >> 3)] = m;
+                }
+            }
         }
     }
     cnt = wave_sum_i32(cnt);
@@ -326,8 +346,8 @@ __global__ void __launch_bounds__(1024) csr_scan_kernel(int32_t *row_ptr, int64_
 // lanes' counts places them in column order.
 template <int DT, int V>
 __global__ void __launch_bounds__(kPackNT) csr_fill_kernel(const void *w, int64_t N, int64_t K,
-                                                           const int32_t *row_ptr, int32_t *col,
-                                                           void *vals, int vdt) {
+                                                           const int32_t *row_ptr, const uint32_t *mask,
+                                                           int32_t *col, void *vals, int vdt) {
     using E = Elem<DT>;
     constexpr int NW = V * E::kSize / 4 > 0 ? V * E::kSize / 4 : 1;
     const int64_t n = (int64_t)blockIdx.x * (kPackNT / 64) + (threadIdx.x >> 6);
@@ -336,8 +356,64 @@ __global__ void __launch_bounds__(kPackNT) csr_fill_kernel(const void *w, int64_
     const char *row = static_cast<const char *>(w) + n * K * E::kSize;
     int64_t pos = row_ptr[n];
     const int64_t end = row_ptr[n + 1];
-    // U steps' loads issued together (addresses clamped into the row)
     constexpr int U = 4;
+    auto store_entry = [&](int64_t at, int64_t k, uint32_t bits) {
+        col[at] = (int32_t)k;
+        if (vdt == DT) {
+            if (DT == ORTH_DT_F32) static_cast<uint32_t *>(vals)[at] = bits;
+            else static_cast<uint16_t *>(vals)[at] = (uint16_t)bits;
+        } else {
+            const uint32_t one[1] = {bits};
+            store_from_f32(vals, vdt, at, DT == ORTH_DT_F32 ? __uint_as_float(bits) : E::get(one, 0));
+        }
+    };
+    if (V == 4 && mask) {
+        // with the count pass's mask: only the elements it marked are read
+        const uint32_t *mrow = mask + n * csr_mask_words(K);
+        const int64_t nst = (K + 64 * V - 1) / (64 * V);
+        for (int64_t s0 = 0; s0 < nst; s0 += U) {
+            uint32_t nib[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const uint32_t m = mrow[min(s0 + u, nst - 1) * 8 + (lane >> 3)];
+                nib[u] = s0 + u < nst ? (m >> (4 * (lane & 7))) & 15u : 0u;
+            }
+            uint32_t vb[U][V];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int64_t k = (s0 + u) * 64 * V + (int64_t)lane * V;
+#pragma unroll
+                for (int j = 0; j < V; j++) {
+                    vb[u][j] = 0u;
+                    if ((nib[u] >> j) & 1u)
+                        vb[u][j] = DT == ORTH_DT_F32 ? reinterpret_cast<const uint32_t *>(row)[k + j]
+                                                    : (uint32_t)reinterpret_cast<const uint16_t *>(row)[k + j];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int64_t k = (s0 + u) * 64 * V + (int64_t)lane * V;
+                const int cnt = __builtin_popcount(nib[u]);
+                int incl = cnt;
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const int up = __shfl_up(incl, off);
+                    if (lane >= off) incl += up;
+                }
+                int64_t at = pos + incl - cnt;
+#pragma unroll
+                for (int j = 0; j < V; j++) {
+                    if (((nib[u] >> j) & 1u) && at < end) {
+                        store_entry(at, k + j, vb[u][j]);
+                        at++;
+                    }
+                }
+                pos += __shfl(incl, 63);
+            }
+        }
+        return;
+    }
+    // U steps' loads issued together (addresses clamped into the row)
     for (int64_t kb = 0; kb < K; kb += 64 * V * U) {
         uint32_t wd[U][NW];
 #pragma unroll
@@ -365,13 +441,7 @@ __global__ void __launch_bounds__(kPackNT) csr_fill_kernel(const void *w, int64_
 #pragma unroll
             for (int j = 0; j < V; j++) {
                 if (k + j < K && E::nonzero(wd[u], j) && at < end) {
-                    col[at] = (int32_t)(k + j);
-                    if (vdt == DT) {
-                        if (DT == ORTH_DT_F32) static_cast<uint32_t *>(vals)[at] = E::bits(wd[u], j);
-                        else static_cast<uint16_t *>(vals)[at] = (uint16_t)E::bits(wd[u], j);
-                    } else {
-                        store_from_f32(vals, vdt, at, E::get(wd[u], j));
-                    }
+                    store_entry(at, k + j, E::bits(wd[u], j));
                     at++;
                 }
             }
@@ -450,10 +520,16 @@ int csr_vec(const void *w, int wdt, int64_t K) {
 }
 }  // namespace
 
-hipError_t launch_csr_rows(const void *w, int wdt, int64_t N, int64_t K, int32_t *row_ptr, hipStream_t stream) {
+int64_t csr_mask_bytes(const void *w, int wdt, int64_t N, int64_t K) {
+    return csr_vec(w, wdt, K) == 4 ? N * csr_mask_words(K) * 4 : 0;
+}
+
+hipError_t launch_csr_rows(const void *w, int wdt, int64_t N, int64_t K, int32_t *row_ptr, void *mask_v,
+                           hipStream_t stream) {
     const unsigned blocks = (unsigned)((N + 3) / 4);
     const bool v4 = csr_vec(w, wdt, K) == 4;
-#define ORTH_COUNT(DT, V) hipLaunchKernelGGL((csr_count_kernel<DT, V>), dim3(blocks), dim3(kPackNT), 0, stream, w, N, K, row_ptr)
+    uint32_t *mask = static_cast<uint32_t *>(mask_v);
+#define ORTH_COUNT(DT, V) hipLaunchKernelGGL((csr_count_kernel<DT, V>), dim3(blocks), dim3(kPackNT), 0, stream, w, N, K, row_ptr, mask)
     if (wdt == ORTH_DT_F32) { if (v4) ORTH_COUNT(ORTH_DT_F32, 4); else ORTH_COUNT(ORTH_DT_F32, 1); }
     else if (wdt == ORTH_DT_F16) { if (v4) ORTH_COUNT(ORTH_DT_F16, 4); else ORTH_COUNT(ORTH_DT_F16, 1); }
     else { if (v4) ORTH_COUNT(ORTH_DT_BF16, 4); else ORTH_COUNT(ORTH_DT_BF16, 1); }
@@ -464,11 +540,12 @@ hipError_t launch_csr_rows(const void *w, int wdt, int64_t N, int64_t K, int32_t
     return hipGetLastError();
 }
 
-hipError_t launch_csr_fill(const void *w, int wdt, int64_t N, int64_t K, const int32_t *row_ptr, int32_t *col,
-                           void *vals, int vdt, hipStream_t stream) {
+hipError_t launch_csr_fill(const void *w, int wdt, int64_t N, int64_t K, const int32_t *row_ptr,
+                           const void *mask_v, int32_t *col, void *vals, int vdt, hipStream_t stream) {
     const unsigned blocks = (unsigned)((N + 3) / 4);
     const bool v4 = csr_vec(w, wdt, K) == 4;
-#define ORTH_FILL(DT, V) hipLaunchKernelGGL((csr_fill_kernel<DT, V>), dim3(blocks), dim3(kPackNT), 0, stream, w, N, K, row_ptr, col, vals, vdt)
+    const uint32_t *mask = static_cast<const uint32_t *>(mask_v);
+#define ORTH_FILL(DT, V) hipLaunchKernelGGL((csr_fill_kernel<DT, V>), dim3(blocks), dim3(kPackNT), 0, stream, w, N, K, row_ptr, mask, col, vals, vdt)
     if (wdt == ORTH_DT_F32) { if (v4) ORTH_FILL(ORTH_DT_F32, 4); else ORTH_FILL(ORTH_DT_F32, 1); }
     else if (wdt == ORTH_DT_F16) { if (v4) ORTH_FILL(ORTH_DT_F16, 4); else ORTH_FILL(ORTH_DT_F16, 1); }
     else { if (v4) ORTH_FILL(ORTH_DT_BF16, 4); else ORTH_FILL(ORTH_DT_BF16, 1); }

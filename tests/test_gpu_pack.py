@@ -125,6 +125,9 @@ def test_pack_csr_matches_oracle_and_torch_ops(N, K, dtype, density, layout):
     rp_t, col_t, vals_t = pack_ortho_sparse_torch(wt, "csr")
     assert np.array_equal(bits(rp), bits(rp_t)) and np.array_equal(bits(col), bits(col_t))
     assert np.array_equal(bits(vals), bits(vals_t))
+    # without the nonzero mask (the fill reads all of w): the same arrays
+    rp2, col2, vals2 = _C_ops.pack_csr(wt, use_mask=False)
+    assert torch.equal(rp2, rp) and torch.equal(col2, col) and np.array_equal(bits(vals2), bits(vals))
     # FP16 values straight from the kernel: rounded to nearest even
     _, _, v16 = _C_ops.pack_csr(wt, torch.float16)
     assert np.array_equal(bits(v16), PO.as_f32(vals_o, dtype).astype(np.float16).view(np.uint16))
