@@ -387,7 +387,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the dual GEMM shards by output rows "
-              "with no collective (see DESIGN.md), and multi-GPU runs are not part of it",
+              "with no collective (each GPU takes a contiguous block of rows and its CSR rows), "
+              "and multi-GPU runs are not part of it",
               file=sys.stderr)
         sys.exit(2)
 

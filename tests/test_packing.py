@@ -174,7 +174,7 @@ def test_skewed_layer_generator():
 
 
 def test_algorithmic_bytes_match_baseline_table():
-    # BASELINE.md section 2 / SURVEY.md section 8(d)
+    # the published per-config byte counts: c1 9.436 / 8.413 MB, c2 M=1..16, c3, c4, c5
     c1 = W.config_layer("c1")
     assert abs(W.algorithmic_bytes(c1, 1, 1.0) / 1e6 - 9.436) < 1e-3
     assert abs(W.algorithmic_bytes(c1, 1, 0.0) / 1e6 - 8.413) < 1e-3
