@@ -248,6 +248,40 @@ def time_pack(torch, steps=30):
     return out
 
 
+def time_module(torch, calls=300):
+    """Python-level OrthoLinear.forward at c2 M=1 (alpha = 1, cached plan),
+    called eagerly: wall time per call on the host (ctypes binding, tensor
+    checks, plan-cache lookup, launch) and the GPU time per call (HIP
+    events around the same loop).  The layer is loaded from a
+    reference-layout state_dict of the c2 buffers."""
+    import time as _t
+    from libortho_amd import OrthoLinear, workloads as W
+    lay = W.config_layer("c2")
+    m = OrthoLinear(lay.K, lay.N)
+    m.load_state_dict({"base_weight": torch.from_numpy(lay.q), "base_scales": torch.from_numpy(lay.scales),
+                       "ortho_values": torch.from_numpy(lay.vals),
+                       "ortho_col_indices": torch.from_numpy(lay.col),
+                       "ortho_row_ptr": torch.from_numpy(lay.row_ptr)})
+    m = m.cuda()
+    x = torch.from_numpy(W.make_x(1, lay.K, 77)).cuda()
+    with torch.no_grad():
+        for _ in range(20):
+            m(x)
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        w0 = _t.perf_counter()
+        t0.record()
+        for _ in range(calls):
+            m(x)
+        t1.record()
+        torch.cuda.synchronize()
+        wall = (_t.perf_counter() - w0) / calls
+    return {"workload": "OrthoLinear.forward c2 M=1 alpha=1 (eager Python calls)",
+            "us_per_call_wall": round(wall * 1e6, 2),
+            "us_per_call_gpu": round(t0.elapsed_time(t1) * 1e3 / calls, 2)}
+
+
 COPY_BYTES = 512 << 20  # calibration copy: reads and writes exactly this many bytes
 PROFILE_DECODE_STEPS = 100
 PROFILE_PREFILL_STEPS = 5
@@ -456,6 +490,8 @@ def main():
                                   "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
                 log(f"  {secondary[-1]}")
         secondary.extend(time_pack(torch))
+        secondary.append(time_module(torch))
+        log(f"  {secondary[-1]}")
 
     workload = "c2_m1_alpha1"
     out = {

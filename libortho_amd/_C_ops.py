@@ -159,6 +159,33 @@ def forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_r
     _lib.check(rc)
 
 
+def forward_layer(layer, input, output, plan=None, bias=None) -> None:
+    """``forward_planned`` with a descriptor from :func:`make_layer` built
+    earlier for the same, unchanged weight tensors (the caller keeps them
+    alive): skips re-validating and re-describing the weights on every call."""
+    _check_io(input, output)
+    dev = input.device
+    L = _lib.lib()
+    has_plan = plan is not None and plan.numel() > 0
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    if bias is not None:
+        _req(bias.device == dev and bias.dtype in _DT and bias.numel() == output.shape[1] and bias.is_contiguous(),
+             "bias must be a contiguous float tensor of out_features elements on input's device")
+
+    def call():
+        return L.orth_layer_forward_hip_ex(ctypes.byref(layer), _ptr(plan) if has_plan else None,
+                                           plan.numel() if has_plan else 0,
+                                           _ptr(bias) if bias is not None else None,
+                                           _DT[bias.dtype] if bias is not None else 0, _ptr(input),
+                                           _ptr(output), int(input.shape[0]), _DT[input.dtype], stream)
+    if dev.index == torch.cuda.current_device():
+        rc = call()
+    else:
+        with torch.cuda.device(dev):
+            rc = call()
+    _lib.check(rc)
+
+
 def build_plan(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr,
                in_features: int):
     """Build the ortho plan (derived layout of the CSR used by the prefill

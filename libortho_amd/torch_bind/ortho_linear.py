@@ -158,9 +158,22 @@ class OrthoLinear(nn.Module):
             self._plan_key = key
         return self._plan
 
+    def _layer_desc(self, device):
+        """The weights' C descriptor, cached until a buffer or alpha changes
+        (validated when built)."""
+        ts = (self.base_weight, self.base_scales, self.ortho_values, self.ortho_col_indices, self.ortho_row_ptr)
+        key = (tuple((t.data_ptr(), t._version, tuple(t.shape), t.dtype) for t in ts), float(self.alpha), device)
+        if getattr(self, "_desc_key", None) != key:
+            self._desc = _C.make_layer(self.base_weight, self.base_scales, self.ortho_values,
+                                       self.ortho_col_indices, self.ortho_row_ptr, self.in_features,
+                                       self.out_features, float(self.alpha), device)
+            self._desc_key = key
+        return self._desc
+
     def _apply(self, fn, *args, **kwargs):
         self._plan = None
         self._plan_key = None
+        self._desc_key = None
         return super()._apply(fn, *args, **kwargs)
 
     # --------------------------------------------------------------- forward
@@ -179,9 +192,8 @@ class OrthoLinear(nn.Module):
         # bias`) unless autograd must see the add
         fuse = self.bias is not None and not (torch.is_grad_enabled() and self.bias.requires_grad) and \
             self.bias.device == x.device
-        _C.forward_planned(self.base_weight, self.base_scales, self.ortho_values,
-                           self.ortho_col_indices, self.ortho_row_ptr, x_flat.contiguous(), output,
-                           self.alpha, plan, bias=self.bias.detach().contiguous() if fuse else None)
+        _C.forward_layer(self._layer_desc(x.device), x_flat.contiguous(), output, plan,
+                         self.bias.detach().contiguous() if fuse else None)
         if self.bias is not None and not fuse:
             output += self.bias
         return output.view(*original_shape[:-1], self.out_features)
