@@ -241,7 +241,8 @@ def pack_base(base_weight: torch.Tensor, group_size=None, base_scales=None):
              "base_scales must be float16/bfloat16/float32 on the weights' device with N * K/G elements")
         s_in = base_scales.contiguous()
     q = torch.empty((N, K // 2), dtype=torch.uint8, device=dev)
-    scales = torch.empty((N,) if G == K else (N, K // G), dtype=torch.float16, device=dev)
+    # [N] for per-row scales (group_size None, the reference layout), else [N, K/G]
+    scales = torch.empty((N,) if group_size is None else (N, K // G), dtype=torch.float16, device=dev)
     with torch.cuda.device(dev):
         _lib.check(_lib.lib().orth_pack_base_hip(
             _ptr(w), _DT[w.dtype], N, K, G, _ptr(s_in) if s_in is not None else None,
