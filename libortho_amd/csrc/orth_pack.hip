@@ -297,20 +297,23 @@ __global__ void __launch_bounds__(kPackNT) csr_count_kernel(const void *w, int64
     }
 }
 
+constexpr int kScanPer = 16;
+
 // In-place inclusive scan of row_ptr[1 .. N] by one workgroup of 1024
-// threads, 8 consecutive counts per thread per pass: thread sums, a wave
+// threads, kScanPer consecutive counts per thread per pass (one pass up
+// to 16,384 rows): thread sums, a wave
 // scan with lane shuffles, the 16 wave totals scanned through LDS.  A
 // running total past 2^31 - 1 stores -1 from there on.
 __global__ void __launch_bounds__(1024) csr_scan_kernel(int32_t *row_ptr, int64_t N) {
     __shared__ int64_t wsum[16];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     int64_t carry = 0;
-    for (int64_t base = 0; base < N; base += 8 * 1024) {
-        const int64_t i0 = base + 8 * (int64_t)t;
-        int64_t v[8];
+    for (int64_t base = 0; base < N; base += kScanPer * 1024) {
+        const int64_t i0 = base + kScanPer * (int64_t)t;
+        int64_t v[kScanPer];
         int64_t tsum = 0;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < kScanPer; j++) {
             v[j] = i0 + j < N ? (int64_t)row_ptr[i0 + j + 1] : 0;
             tsum += v[j];
             v[j] = tsum;  // inclusive within the thread
@@ -330,7 +333,7 @@ __global__ void __launch_bounds__(1024) csr_scan_kernel(int32_t *row_ptr, int64_
         }
         before += incl - tsum;  // lanes before this one in the wave
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < kScanPer; j++) {
             if (i0 + j < N) {
                 const int64_t tot = before + v[j];
                 row_ptr[i0 + j + 1] = (carry < 0 || tot > 0x7fffffffLL) ? -1 : (int32_t)tot;

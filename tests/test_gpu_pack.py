@@ -97,6 +97,7 @@ CSR_CASES = [
     (64, 4096, "f32", 0.01, "aligned"), (64, 4096, "f16", 0.05, "aligned"), (64, 4096, "bf16", 0.05, "aligned"),
     (50, 301, "f32", 0.1, "aligned"), (50, 300, "f16", 0.1, "offset"), (50, 4096, "f32", 0.02, "offset"),
     (70, 1000, "f32", 0.0, "aligned"), (9, 64, "f32", 1.0, "aligned"),
+    (40000, 64, "f16", 0.05, "aligned"),  # more rows than one scan pass (16,384): the carry
 ]
 
 
