@@ -12,7 +12,8 @@ no step finds its weights in the 256 MB Infinity Cache.  Each copy carries
 its ortho plan, built once before timing, as OrthoLinear builds and caches
 it on its first call with alpha > 0.  The K timed steps are one replay of a
 HIP graph holding exactly K launches (launch cost on the host is not what is
-measured), bracketed by synchronisation.
+measured), replayed right behind an untimed replay of the same graph and
+bracketed by HIP events on the launch stream.
 
 Printed: one JSON line with the contract fields plus
   roofline      the decode kernel: algorithmic bytes per launch / its average
@@ -20,11 +21,16 @@ Printed: one JSON line with the contract fields plus
                 timed graph replay, divided by K) against 8 TB/s
   cpu_baseline  the reference CPU forward restated (oracle/cpu_baseline.c,
                 reference flags, 1 pinned core) on a bounded sample
+                (c2 M=1), plus c1 (whole layer) and c3 (token subset,
+                extrapolated) in cpu_baseline.secondary
   secondary     the rest of the metric: M in {2,4,8,16} GB/s, and the
                 prefill TFLOP/s at M=2048 (4096->11008 and 4096->4096);
-                then the packing kernels (load time) on the c2 layer from
-                dense FP32 weights: GB/s of algorithmic bytes (W read once,
-                q / scales / CSR written once)
+                c1 M=1 (alpha 1 and 0), c4 M=8, the c5 block (seven
+                projections back to back, M 1 and 32); the reference's
+                8-argument _C_ops.forward called eagerly without a plan (c2
+                M=1, c3); then the packing kernels (load time) on the c2
+                layer from dense FP32 weights: GB/s of algorithmic bytes (W
+                read once, q / scales / CSR written once)
 """
 from __future__ import annotations
 
@@ -90,6 +96,33 @@ def cpu_baseline(layer, x, alpha, budget_s):
     return t, iters
 
 
+def cpu_secondary(budget_s):
+    """The same single-core restatement on c1 (4096 -> 4096, per-row
+    scales, M=1, alpha 1: the whole layer) and c3 (4096 -> 4096, M=2048,
+    alpha 1) timed on 8 of its 2048 tokens and scaled by 2048 / 8: each
+    token is an independent pass of the reference's loop over the weights
+    (/root/reference/src/ortho.c:352-398), so the time is linear in M."""
+    from libortho_amd import workloads as W
+    out = []
+    c1 = W.config_layer("c1")
+    t, n = cpu_baseline(c1, W.make_x(1, c1.K, 7001), 1.0, budget_s / 3)
+    b = W.algorithmic_bytes(c1, 1, 1.0)
+    out.append({"workload": "c1 M=1 alpha=1", "ms_per_call": round(t * 1e3, 3), "GB/s": round(b / t / 1e9, 4),
+                "cores": 1, "sample": f"whole layer, {n} timed calls"})
+    log(f"  cpu {out[-1]}")
+    c3 = W.config_layer("c3")
+    sub = 8
+    t, n = cpu_baseline(c3, W.make_x(sub, c3.K, 9048), 1.0, budget_s / 2)
+    t_full = t * 2048 / sub
+    f = W.algorithmic_flops(c3, 2048, 1.0)
+    out.append({"workload": "c3 M=2048 alpha=1", "ms_per_call": round(t_full * 1e3, 1),
+                "GFLOP/s": round(f / t_full / 1e9, 3), "cores": 1,
+                "sample": f"{sub} of 2048 tokens, {n} timed calls of {t * 1e3:.1f} ms, scaled by 2048/{sub} "
+                          "(linear extrapolation: the loop is per token)"})
+    log(f"  cpu {out[-1]}")
+    return out
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -127,8 +160,8 @@ class Rotation:
 def time_workload(torch, layer, M, alpha, steps, warmup, plan=False):
     """Returns dict(ms_per_step, kernel, copies) for `steps` forwards: HIP
     events on the launch stream around one replay of a graph of `steps`
-    launches, so ms_per_step is the average launch duration (graph gaps
-    included; they are ~0.3 us against rocprofv3's kernel durations)."""
+    launches (replay_timed), so ms_per_step is the average launch duration,
+    the gaps between the graph's launches included."""
     from libortho_amd import _C_ops, workloads as W
     rot = Rotation(layer, torch, plan=plan)
     x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda()
@@ -149,23 +182,32 @@ def time_workload(torch, layer, M, alpha, steps, warmup, plan=False):
     with torch.cuda.graph(g):
         for i in range(steps):
             rot.call(i, x, y, alpha)
-    g.replay()
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    g.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
+    ms = replay_timed(torch, g) / steps
     del g
     return dict(ms_per_step=ms, kernel=kernel, copies=rot.n)
 
 
+def replay_timed(torch, g):
+    """Milliseconds of one replay of graph g, HIP events on the launch stream
+    around it.  The graph is replayed once untimed first (clocks up, graph
+    resident), then again untimed immediately before the timed replay with
+    no host synchronisation in between, so the timed replay starts while the
+    GPU is busy: its own launches are all that the events bracket."""
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    g.replay()
+    t0.record()
+    g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1)
+
+
 def graph_time(torch, fn, steps):
     """Average duration of fn(i) for i < steps: HIP events around one replay
-    of a graph holding the steps launches (as time_workload)."""
+    of a graph holding the steps calls (replay_timed)."""
     fn(0)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -177,16 +219,68 @@ def graph_time(torch, fn, steps):
     with torch.cuda.graph(g):
         for i in range(steps):
             fn(i)
-    g.replay()
+    ms = replay_timed(torch, g) / steps
+    del g
+    return ms
+
+
+def time_block(torch, M, steps):
+    """Config c5: the seven projections of one Llama-2-7B block (q, k, v, o,
+    gate, up, down; group-128, ortho 2 %, alpha = 1) back to back per step,
+    each with its cached plan, weights rotated over enough block copies to
+    exceed the Infinity Cache.  Returns ms per block."""
+    from libortho_amd import workloads as W
+    layers = W.llama_block()
+    per = sum(W.algorithmic_bytes(l, 0, 1.0) for l in layers)
+    copies = max(4, -(-ROTATE_MIN_BYTES // per))
+    rots = [Rotation(l, torch, min_copies=copies, min_bytes=0, plan=True) for l in layers]
+    xs = {K: torch.from_numpy(W.make_x(M, K, 7100 + K)).cuda() for K in {l.K for l in layers}}
+    ys = [torch.empty(M, l.N, dtype=torch.float16, device="cuda") for l in layers]
+
+    def fn(i):
+        for j, l in enumerate(layers):
+            rots[j].call(i, xs[l.K], ys[j], 1.0)
+    fn(0)
+    torch.cuda.synchronize()
+    assert all(torch.isfinite(y).all().item() for y in ys), "non-finite output"
+    return graph_time(torch, fn, steps), sum(W.algorithmic_bytes(l, M, 1.0) for l in layers), \
+        sum(W.algorithmic_flops(l, M, 1.0) for l in layers)
+
+
+def time_dropin(torch, layer, M, alpha, calls, graph_steps=0):
+    """The reference's 8-argument entry, libortho._C_ops.forward(q_weight,
+    q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input, output,
+    alpha) (/root/reference/torch_bind/bindings.cpp:9-48), called eagerly
+    from Python with no plan: wall and GPU time per call; with graph_steps,
+    also the per-launch time of that many calls captured in a graph (weights
+    rotated as in time_workload)."""
+    import time as _t
+    import libortho._C_ops as C
+    from libortho_amd import workloads as W
+    d = W.to_device(layer)
+    x = torch.from_numpy(W.make_x(M, layer.K, 7200 + M)).cuda()
+    y = torch.empty(M, layer.N, dtype=torch.float16, device="cuda")
+    args = (d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y, alpha)
+    for _ in range(5):
+        C.forward(*args)
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    w0 = _t.perf_counter()
     t0.record()
-    g.replay()
+    for _ in range(calls):
+        C.forward(*args)
     t1.record()
     torch.cuda.synchronize()
-    del g
-    return t0.elapsed_time(t1) / steps
+    out = {"us_per_call_wall": round((_t.perf_counter() - w0) / calls * 1e6, 2),
+           "us_per_call_gpu": round(t0.elapsed_time(t1) * 1e3 / calls, 2)}
+    if graph_steps:
+        rot = Rotation(layer, torch, plan=False)
+        ms = graph_time(torch, lambda i: C.forward(*(lambda c: (c["q"], c["scales"], c["vals"], c["col"],
+                                                                   c["row_ptr"]))(rot.copies[i % rot.n]),
+                                                   x, y, alpha), graph_steps)
+        out["us_per_launch_graph"] = round(ms * 1e3, 3)
+    return out
 
 
 def time_pack(torch, steps=30):
@@ -450,6 +544,7 @@ def main():
                          f"-funroll-loops; host: {cpu_model()}, nproc={os.cpu_count()}",
                "ms_per_call": round(t_cpu * 1e3, 3)}
         log(f"  {t_cpu * 1e3:.2f} ms/call over {iters} calls")
+        cpu["secondary"] = cpu_secondary(args.cpu_seconds)
 
     import torch
     if not torch.cuda.is_available():
@@ -489,6 +584,38 @@ def main():
                                   "TFLOP/s": round(tf, 1),
                                   "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
                 log(f"  {secondary[-1]}")
+        for cfg, m, a in (("c1", 1, 1.0), ("c1", 1, 0.0), ("c4", 8, 1.0)):
+            lay = W.config_layer(cfg)
+            rr = time_workload(torch, lay, m, a, args.steps, 10, plan=True)
+            b = W.algorithmic_bytes(lay, m, a)
+            secondary.append({"workload": f"{cfg} M={m} alpha={a}", "kernel": rr["kernel"],
+                              "us_per_step": round(rr["ms_per_step"] * 1e3, 3),
+                              "GB/s": round(b / (rr["ms_per_step"] * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(b / (rr["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+            log(f"  {secondary[-1]}")
+        for m in (1, 32):
+            # 7 launches per step: a shorter graph (the capture holds them all)
+            ms, b, f = time_block(torch, m, max(20, min(args.steps, 300)))
+            secondary.append({"workload": f"c5 Llama-2-7B block (7 projections) M={m}", "kernel": "per projection",
+                              "us_per_step": round(ms * 1e3, 3),
+                              "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "TFLOP/s": round(f / (ms * 1e-3) / 1e12, 2)})
+            log(f"  {secondary[-1]}")
+        r1 = time_dropin(torch, layer, 1, 1.0, 300, graph_steps=max(20, min(args.steps, 2000)))
+        b = W.algorithmic_bytes(layer, 1, 1.0)
+        r1.update({"workload": "reference 8-argument _C_ops.forward, c2 M=1 alpha=1 (no plan: CSR read)",
+                   "GB/s_graph": round(b / (r1["us_per_launch_graph"] * 1e-6) / 1e9, 1)})
+        secondary.append(r1)
+        log(f"  {secondary[-1]}")
+        c3 = W.config_layer("c3")
+        r3 = time_dropin(torch, c3, 2048, 1.0, 20)
+        f = W.algorithmic_flops(c3, 2048, 1.0)
+        r3.update({"workload": "reference 8-argument _C_ops.forward, c3 M=2048 alpha=1 (no plan: "
+                               "temporary plan built per call)",
+                   "TFLOP/s_gpu": round(f / (r3["us_per_call_gpu"] * 1e-6) / 1e12, 1)})
+        secondary.append(r3)
+        log(f"  {secondary[-1]}")
         secondary.extend(time_pack(torch))
         secondary.append(time_module(torch))
         log(f"  {secondary[-1]}")

@@ -194,6 +194,42 @@ int orth_pack_csr_fill_hip(const void *w, int32_t w_dtype, int64_t out_features,
                            const int32_t *row_ptr, const void *mask, int64_t mask_bytes, int32_t *col_out,
                            void *values_out, int32_t value_dtype, void *stream);
 
+/* The offline Base/Ortho sieve on the device (a one-off step before
+ * packing; all pointers device memory, calls asynchronous on `stream`).
+ * Each replaces torch ops of /root/reference/tools/sieve.py with the same
+ * arithmetic on a GPU tensor (every intermediate rounded to the dtype the
+ * torch op returns).
+ *
+ * orth_sieve_quantize_hip: w_base [out_features, in_features] (w's dtype) =
+ * quantize_int4(w), /root/reference/tools/sieve.py:13-23: per-row scale
+ * clamp(max|w|, 1e-8) / 7, clamp(round(w / s), -8, 7) * s, non-finite -> 0. */
+int orth_sieve_quantize_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                            void *w_base, void *stream);
+
+/* orth_sieve_split_hip: hessian_sieve, /root/reference/tools/sieve.py:25-76.
+ * Writes w_base as above and w_ortho = residual * (score > t) (w's dtype),
+ * with residual = w - w_base and score = residual^2 / (h + 1e-6) (written to
+ * `score`, FP32 [out_features * in_features], holding values of score_dtype,
+ * the promotion of w's and h's dtypes).  h: element k at h_inv[k * h_stride]
+ * (the diagonal of a matrix H_inv: its two strides summed; a vector: 1).
+ * use_rank: t = the rank-th largest score (torch.topk(...).values[-1], NaN
+ * largest; rank 0 keeps nothing), found by a radix select in select_state
+ * (orth_sieve_select_bytes() bytes of device memory); else t = threshold. */
+int64_t orth_sieve_select_bytes(void);
+int orth_sieve_split_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                         const void *h_inv, int32_t h_dtype, int64_t h_stride, int32_t score_dtype,
+                         int32_t use_rank, int64_t rank, float threshold, void *w_base, void *w_ortho,
+                         float *score, void *select_state, void *stream);
+
+/* orth_sieve_hdiag_hip: out [in_features] (x's dtype) = diag(x^T x) / rows +
+ * 1e-6 for x [rows, in_features], /root/reference/tools/sieve.py:79-95 (the
+ * diagonal only: FP32 column sums of squares over row slices, then the
+ * division and the add of the torch ops).  workspace: FP32 device memory of
+ * orth_sieve_hdiag_workspace(rows, in_features) elements. */
+int64_t orth_sieve_hdiag_workspace(int64_t rows, int64_t in_features);
+int orth_sieve_hdiag_hip(const void *x, int32_t x_dtype, int64_t rows, int64_t in_features, float *workspace,
+                         int64_t workspace_floats, void *out, void *stream);
+
 /* Device facts.  Replaces check_tensor_core_support,
  * /root/reference/src/dual_gemm_tensor_core.cu:342-350. */
 typedef struct {

@@ -290,6 +290,72 @@ def pack_csr(ortho_weight: torch.Tensor, values_dtype=None, use_mask: bool = Tru
     return row_ptr, col, vals
 
 
+def sieve_quantize(weight: torch.Tensor) -> torch.Tensor:
+    """quantize_int4 (/root/reference/tools/sieve.py:13-23) of a 2-D GPU
+    tensor with the library's kernel: same dtype and shape as ``weight``."""
+    _req(weight.is_cuda and weight.dim() == 2 and weight.dtype in _DT,
+         "sieve_quantize needs a 2-D float16, bfloat16 or float32 tensor on a ROCm GPU")
+    w = weight.contiguous()
+    out = torch.empty_like(w)
+    if w.numel() == 0:
+        return out
+    with torch.cuda.device(w.device):
+        _lib.check(_lib.lib().orth_sieve_quantize_hip(_ptr(w), _DT[w.dtype], int(w.shape[0]), int(w.shape[1]),
+                                                      _ptr(out), _stream(w.device)))
+    return out
+
+
+def sieve_split(weight: torch.Tensor, H_inv: torch.Tensor, curvature_thresh: float = 10.0,
+                sparsity_target=None):
+    """hessian_sieve (/root/reference/tools/sieve.py:25-76) with the
+    library's kernels: (w_base, w_ortho), both of ``weight``'s dtype."""
+    _req(weight.is_cuda and weight.dim() == 2 and weight.dtype in _DT,
+         "sieve_split needs a 2-D float16, bfloat16 or float32 weight on a ROCm GPU")
+    _req(H_inv.device == weight.device and H_inv.dtype in _DT and H_inv.dim() in (1, 2),
+         "H_inv must be a 1-D or 2-D float tensor on the weight's device")
+    w = weight.contiguous()
+    N, K = int(w.shape[0]), int(w.shape[1])
+    h = torch.diagonal(H_inv) if H_inv.dim() > 1 else H_inv
+    if h.numel() == 1:
+        h_stride = 0
+    else:
+        _req(h.numel() == K, f"H_inv has {h.numel()} diagonal entries, the weight {K} columns")
+        h_stride = int(h.stride(0))
+    score_dt = torch.promote_types(w.dtype, h.dtype)
+    w_base = torch.empty_like(w)
+    w_ortho = torch.empty_like(w)
+    if w.numel() == 0:
+        return w_base, w_ortho
+    score = torch.empty(N * K, dtype=torch.float32, device=w.device)
+    L = _lib.lib()
+    use_rank = sparsity_target is not None
+    rank = int(sparsity_target * (N * K)) if use_rank else 0
+    sel = torch.empty(int(L.orth_sieve_select_bytes()), dtype=torch.uint8, device=w.device)
+    with torch.cuda.device(w.device):
+        _lib.check(L.orth_sieve_split_hip(_ptr(w), _DT[w.dtype], N, K, ctypes.c_void_p(h.data_ptr()), _DT[h.dtype],
+                                          h_stride, _DT[score_dt], 1 if use_rank else 0, rank,
+                                          float(curvature_thresh) if not use_rank else 0.0, _ptr(w_base),
+                                          _ptr(w_ortho), _ptr(score), _ptr(sel), _stream(w.device)))
+    return w_base, w_ortho
+
+
+def sieve_hdiag(inputs: torch.Tensor) -> torch.Tensor:
+    """compute_hessian_diag_approx (/root/reference/tools/sieve.py:79-95),
+    diag(X^T X) / n + 1e-6, of a 2-D GPU tensor with the library's kernels."""
+    _req(inputs.is_cuda and inputs.dim() == 2 and inputs.dtype in _DT,
+         "sieve_hdiag needs a 2-D float16, bfloat16 or float32 tensor on a ROCm GPU")
+    x = inputs.contiguous()
+    n, K = int(x.shape[0]), int(x.shape[1])
+    _req(n > 0 and K > 0, "inputs must have rows and columns")
+    L = _lib.lib()
+    ws_n = int(L.orth_sieve_hdiag_workspace(n, K))
+    ws = torch.empty(ws_n, dtype=torch.float32, device=x.device)
+    out = torch.empty(K, dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(L.orth_sieve_hdiag_hip(_ptr(x), _DT[x.dtype], n, K, _ptr(ws), ws_n, _ptr(out), _stream(x.device)))
+    return out
+
+
 def last_kernel() -> str:
     """Kernel used by this thread's last forward: decode, skinny (5..64
     tokens), prefill or general."""

@@ -47,13 +47,27 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every csrc/*.hip and link libortho_amd.so; returns its path."""
+def _stale(src: str, headers) -> bool:
+    obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(f) > t for f in [src, *headers])
+
+
+def build(verbose: bool = False, changed_only: bool = False) -> str:
+    """Compile every csrc/*.hip and link libortho_amd.so; returns its path.
+    ``changed_only`` recompiles only sources newer than their objects (or
+    than a header), for edit-compile loops."""
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
-    jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    headers.append(os.path.join(ROOT, "include", "orth_hip.h"))
+    todo = [s for s in srcs if _stale(s, headers)] if changed_only else srcs
+    jobs = min(max(1, len(todo)), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        list(ex.map(_compile, todo))
+    objs = [os.path.join(BUILD, os.path.basename(s).replace(".hip", ".o")) for s in srcs]
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -66,5 +80,5 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, changed_only="--changed" in sys.argv)
     sys.exit(0)

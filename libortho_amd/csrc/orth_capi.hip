@@ -45,6 +45,13 @@ hipError_t plan_prepare_device();
 bool skinny_supported(const ForwardArgs &a);
 int64_t skinny_workspace_bytes(const ForwardArgs &a, int cus);
 hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float *part, hipStream_t stream);
+hipError_t launch_sieve_quantize(const void *w, int dt, int64_t N, int64_t K, void *w_base, hipStream_t stream);
+hipError_t launch_sieve_split(const void *w, int dt, int64_t N, int64_t K, const void *h, int hdt, int64_t h_stride,
+                              int score_dt, int use_rank, int64_t rank, float thresh, void *w_base, void *w_ortho,
+                              float *score, void *sel, hipStream_t stream);
+int64_t sieve_hdiag_slices(int64_t n);
+hipError_t launch_sieve_hdiag(const void *x, int dt, int64_t n, int64_t K, float *partial, void *out,
+                              hipStream_t stream);
 }  // namespace orth
 
 using namespace orth;
@@ -501,6 +508,67 @@ int orth_pack_csr_fill_hip(const void *w, int32_t w_dtype, int64_t out_features,
     hipError_t e = launch_csr_fill(w, w_dtype, out_features, in_features, row_ptr, mask, col_out, values_out,
                                    value_dtype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail_hip(e, "CSR fill launch");
+    return ORTH_OK;
+}
+
+int orth_sieve_quantize_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                            void *w_base, void *stream) {
+    int rc = check_pack_dims(w, w_dtype, out_features, in_features);
+    if (rc != ORTH_OK) return rc;
+    if (!w_base) return fail(ORTH_ERR_INVALID_ARGUMENT, "w_base is NULL");
+    if (out_features > INT32_MAX) return fail(ORTH_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
+    rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipError_t e = launch_sieve_quantize(w, w_dtype, out_features, in_features, w_base, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "sieve quantize launch");
+    return ORTH_OK;
+}
+
+int64_t orth_sieve_select_bytes(void) { return 1040; }
+
+int orth_sieve_split_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
+                         const void *h_inv, int32_t h_dtype, int64_t h_stride, int32_t score_dtype,
+                         int32_t use_rank, int64_t rank, float threshold, void *w_base, void *w_ortho,
+                         float *score, void *select_state, void *stream) {
+    int rc = check_pack_dims(w, w_dtype, out_features, in_features);
+    if (rc != ORTH_OK) return rc;
+    if (!h_inv || !valid_dtype(h_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "h_inv is NULL or of a bad dtype");
+    if (!valid_dtype(score_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "score dtype %d is not F16, BF16 or F32", score_dtype);
+    if (h_stride < 0) return fail(ORTH_ERR_INVALID_ARGUMENT, "h_stride is negative");
+    if (!w_base || !w_ortho || !score) return fail(ORTH_ERR_INVALID_ARGUMENT, "an output or the score buffer is NULL");
+    if (use_rank && rank > 0 && !select_state) return fail(ORTH_ERR_INVALID_ARGUMENT, "select_state is NULL");
+    if (rank < 0 || rank > out_features * in_features)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "rank %lld is outside [0, %lld]", (long long)rank,
+                    (long long)(out_features * in_features));
+    if (out_features > INT32_MAX || out_features * in_features > (int64_t)UINT32_MAX)
+        return fail(ORTH_ERR_UNSUPPORTED, "the radix select counts in 32 bits: at most 2^32 - 1 weights");
+    rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipError_t e = launch_sieve_split(w, w_dtype, out_features, in_features, h_inv, h_dtype, h_stride, score_dtype,
+                                      use_rank, rank, threshold, w_base, w_ortho, score, select_state,
+                                      static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "sieve split launch");
+    return ORTH_OK;
+}
+
+int64_t orth_sieve_hdiag_workspace(int64_t rows, int64_t in_features) {
+    if (rows <= 0 || in_features <= 0) return 0;
+    return sieve_hdiag_slices(rows) * in_features;
+}
+
+int orth_sieve_hdiag_hip(const void *x, int32_t x_dtype, int64_t rows, int64_t in_features, float *workspace,
+                         int64_t workspace_floats, void *out, void *stream) {
+    if (!x || !out || !workspace) return fail(ORTH_ERR_INVALID_ARGUMENT, "x, out or workspace is NULL");
+    if (!valid_dtype(x_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "x dtype %d is not F16, BF16 or F32", x_dtype);
+    if (rows <= 0 || in_features <= 0) return fail(ORTH_ERR_INVALID_ARGUMENT, "rows and in_features must be positive");
+    if (workspace_floats < sieve_hdiag_slices(rows) * in_features)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "workspace holds %lld floats, %lld needed", (long long)workspace_floats,
+                    (long long)(sieve_hdiag_slices(rows) * in_features));
+    if (in_features > ((int64_t)1 << 40) / rows) return fail(ORTH_ERR_INVALID_ARGUMENT, "x is too large");
+    int rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipError_t e = launch_sieve_hdiag(x, x_dtype, rows, in_features, workspace, out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "hessian diagonal launch");
     return ORTH_OK;
 }
 

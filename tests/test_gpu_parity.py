@@ -249,6 +249,41 @@ def test_prefill_c3(oracle_mod, alpha, plan):
     assert_close(y[rows], ref, what=f"c3 alpha={alpha} plan={plan}")
 
 
+def prefill_rows(M, tile=256):
+    """One or two token rows in every 256-token tile of the prefill grid, at
+    positions that move across the tile (so different waves and MFMA rows
+    are checked in different tiles), plus the first and the last row."""
+    rows = {0, M - 1}
+    for bm in range((M + tile - 1) // tile):
+        lo, hi = bm * tile, min(M, (bm + 1) * tile)
+        rows.add(lo + (37 * bm + 5) % (hi - lo))
+        rows.add(hi - 1 - (53 * bm + 11) % (hi - lo))
+    return np.array(sorted(rows))
+
+
+# max|err| / ||y||_inf of the prefill kernel against the FP64 oracle, measured
+# at c3 and 4096->11008 on MI355X: 3.5e-4 .. 4.2e-4 (its weight operand is
+# fp16(fp16(q*s) + alpha*v), one rounding each); the bound is about twice
+# the largest seen
+PREFILL_TOL = 1e-3
+
+
+@pytest.mark.parametrize("shape", ["c3", "c2"])
+@pytest.mark.parametrize("alpha", [0.0, 0.5, 1.0])
+@pytest.mark.parametrize("plan", [True, "auto"])
+def test_prefill_every_tile(oracle_mod, shape, alpha, plan):
+    """M = 2048 at 4096->4096 (c3) and at the metric's 4096->11008 (the c2
+    layer), every output column of rows in every token tile."""
+    L = W.config_layer(shape)
+    x = W.make_x(2048, L.K, 3100 + L.N)
+    y, k = run(L, x, alpha, plan=plan)
+    assert k == "prefill"
+    rows = prefill_rows(2048)
+    ref = oracle_y(oracle_mod, L, x[rows], alpha)
+    rel = assert_close(y[rows], ref, tol=PREFILL_TOL, what=f"prefill {shape} alpha={alpha} plan={plan}")
+    print(f"prefill {shape} N={L.N} alpha={alpha} plan={plan}: max|err|/||y||_inf = {rel:.3e}")
+
+
 def test_prefill_skewed_plan(oracle_mod):
     # thousands of plan entries in one (row block, k step): the fold loops
     L = W.config_layer("c4")
