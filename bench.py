@@ -50,6 +50,8 @@ HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk, dense
 ROTATE_MIN_BYTES = 512 << 20
 ROTATE_MIN_COPIES = 16
+PRE_STEPS = 200      # untimed launches in the timing graph before its first event
+STEADY_STEPS = 2000  # launches of the long graph behind ms_per_step_steady
 
 
 def log(*a):
@@ -157,11 +159,11 @@ class Rotation:
                                self.plans[i % self.n])
 
 
-def time_workload(torch, layer, M, alpha, steps, warmup, plan=False):
-    """Returns dict(ms_per_step, kernel, copies) for `steps` forwards: HIP
-    events on the launch stream around one replay of a graph of `steps`
-    launches (replay_timed), so ms_per_step is the average launch duration,
-    the gaps between the graph's launches included."""
+def time_workload(torch, layer, M, alpha, steps, warmup, plan=False, steady=False):
+    """Returns dict(ms_per_step, kernel, copies) for `steps` forwards timed
+    by graph_steps_time, so ms_per_step is the average launch duration, the
+    gaps between launches included; with ``steady``, also
+    ms_per_step_steady from a graph of STEADY_STEPS launches."""
     from libortho_amd import _C_ops, workloads as W
     rot = Rotation(layer, torch, plan=plan)
     x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda()
@@ -172,19 +174,120 @@ def time_workload(torch, layer, M, alpha, steps, warmup, plan=False):
     kernel = _C_ops.last_kernel()
     assert torch.isfinite(y).all().item(), "non-finite output"
 
-    # K steps captured in one graph, replayed once untimed and once timed
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        rot.call(0, x, y, alpha)
-    torch.cuda.current_stream().wait_stream(s)
-    with torch.cuda.graph(g):
-        for i in range(steps):
-            rot.call(i, x, y, alpha)
-    ms = replay_timed(torch, g) / steps
-    del g
-    return dict(ms_per_step=ms, kernel=kernel, copies=rot.n)
+    ms = graph_steps_time(torch, lambda i: rot.call(i, x, y, alpha), steps, max(warmup, PRE_STEPS))
+    out = dict(ms_per_step=ms, kernel=kernel, copies=rot.n)
+    if steady:
+        # the same launches in one long graph (torch.cuda.CUDAGraph), events
+        # around its replay: the steady per-launch time a rocprofv3 kernel
+        # trace reports, with no fixed timing cost spread over few steps
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            rot.call(0, x, y, alpha)
+        torch.cuda.current_stream().wait_stream(s)
+        with torch.cuda.graph(g):
+            for i in range(STEADY_STEPS):
+                rot.call(i, x, y, alpha)
+        out["ms_per_step_steady"] = replay_timed(torch, g) / STEADY_STEPS
+        del g
+    return out
+
+
+class _Hip:
+    """The few HIP runtime calls the timer needs, through ctypes on the HIP
+    runtime torch already loaded (torch.cuda.Event cannot be recorded inside
+    a captured graph on ROCm)."""
+
+    def __init__(self):
+        import ctypes
+        self.c = ctypes
+        h = ctypes.CDLL("libamdhip64.so")
+        V, P = ctypes.c_void_p, ctypes.POINTER
+        for name, args in (("hipEventCreate", [P(V)]), ("hipEventDestroy", [V]), ("hipStreamCreate", [P(V)]),
+                           ("hipStreamDestroy", [V]), ("hipStreamBeginCapture", [V, ctypes.c_int]),
+                           ("hipStreamEndCapture", [V, P(V)]), ("hipGraphCreate", [P(V), ctypes.c_uint]),
+                           ("hipGraphAddChildGraphNode", [P(V), V, P(V), ctypes.c_size_t, V]),
+                           ("hipGraphAddEventRecordNode", [P(V), V, P(V), ctypes.c_size_t, V]),
+                           ("hipGraphInstantiate", [P(V), V, V, ctypes.c_char_p, ctypes.c_size_t]),
+                           ("hipGraphLaunch", [V, V]), ("hipGraphExecDestroy", [V]), ("hipGraphDestroy", [V]),
+                           ("hipStreamSynchronize", [V]),
+                           ("hipEventElapsedTime", [P(ctypes.c_float), V, V])):
+            fn = getattr(h, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        self.h = h
+
+    def __call__(self, name, *args):
+        rc = getattr(self.h, name)(*args)
+        if rc != 0:
+            raise RuntimeError(f"{name} failed: hipError {rc}")
+
+    def new(self, name, *args):
+        v = self.c.c_void_p()
+        self(name, self.c.byref(v), *args)
+        return v
+
+
+_HIP = None
+
+
+def graph_steps_time(torch, fn, steps, pre):
+    """Milliseconds per call of fn(pre + i), i < steps, timed by HIP events
+    recorded inside one HIP graph: [pre untimed calls] -> event -> [the
+    `steps` calls] -> event.  The untimed calls put graph start-up and the
+    clock ramp before the first event; the events bracket exactly `steps`
+    calls.  The graph is built on a stream of its own (default priority)
+    from two captured segments, replayed once untimed, then once timed."""
+    global _HIP
+    if _HIP is None:
+        _HIP = _Hip()
+    H, c = _HIP, _HIP.c
+    s = H.new("hipStreamCreate")
+    ts = torch.cuda.ExternalStream(s.value)
+    graphs, execs, events = [], [], []
+    try:
+        with torch.cuda.stream(ts):
+            fn(0)  # any per-stream set-up outside capture
+        torch.cuda.synchronize()
+
+        def capture(lo, n):
+            with torch.cuda.stream(ts):
+                H("hipStreamBeginCapture", s, 2)  # relaxed: other threads may allocate
+                for i in range(lo, lo + n):
+                    fn(i)
+                g = c.c_void_p()
+                H("hipStreamEndCapture", s, c.byref(g))
+            graphs.append(g)
+            return g
+        gA = capture(0, pre)
+        gB = capture(pre, steps)
+        e0, e1 = H.new("hipEventCreate"), H.new("hipEventCreate")
+        events += [e0, e1]
+        G = H.new("hipGraphCreate", 0)
+        graphs.append(G)
+        nA = H.new("hipGraphAddChildGraphNode", G, None, 0, gA)
+        n0 = H.new("hipGraphAddEventRecordNode", G, (c.c_void_p * 1)(nA), 1, e0)
+        nB = H.new("hipGraphAddChildGraphNode", G, (c.c_void_p * 1)(n0), 1, gB)
+        H.new("hipGraphAddEventRecordNode", G, (c.c_void_p * 1)(nB), 1, e1)
+        ex = H.new("hipGraphInstantiate", G, None, None, 0)
+        execs.append(ex)
+        H("hipGraphLaunch", ex, s)
+        H("hipStreamSynchronize", s)
+        H("hipGraphLaunch", ex, s)
+        H("hipStreamSynchronize", s)
+        ms = c.c_float()
+        H("hipEventElapsedTime", c.byref(ms), e0, e1)
+        return ms.value / steps
+    finally:
+        torch.cuda.synchronize()
+        for ex in execs:
+            H("hipGraphExecDestroy", ex)
+        for g in graphs:
+            H("hipGraphDestroy", g)
+        for e in events:
+            H("hipEventDestroy", e)
+        H("hipStreamDestroy", s)
 
 
 def replay_timed(torch, g):
@@ -206,22 +309,9 @@ def replay_timed(torch, g):
 
 
 def graph_time(torch, fn, steps):
-    """Average duration of fn(i) for i < steps: HIP events around one replay
-    of a graph holding the steps calls (replay_timed)."""
-    fn(0)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        fn(0)
-    torch.cuda.current_stream().wait_stream(s)
-    with torch.cuda.graph(g):
-        for i in range(steps):
-            fn(i)
-    ms = replay_timed(torch, g) / steps
-    del g
-    return ms
+    """Average duration of fn(i) for i < steps, by graph_steps_time with
+    min(steps, 50) untimed calls first."""
+    return graph_steps_time(torch, lambda i: fn(i), steps, min(steps, 50))
 
 
 def time_block(torch, M, steps):
@@ -555,10 +645,11 @@ def main():
     log(f"device: {info['arch']}, {info['compute_units']} CUs, clock {info['clock_khz'] / 1e3:.0f} MHz")
 
     log(f"decode c2 M=1: warmup {args.warmup}, steps {args.steps} ...")
-    r = time_workload(torch, layer, M, alpha, args.steps, args.warmup, plan=True)
+    r = time_workload(torch, layer, M, alpha, args.steps, args.warmup, plan=True, steady=True)
     gbs = bytes_step / (r["ms_per_step"] * 1e-3) / 1e9
     achieved = gbs  # one kernel per step: the step time is the launch duration
-    log(f"  {r['ms_per_step'] * 1e3:.2f} us/step -> {gbs:.0f} GB/s; kernel {r['kernel']}")
+    log(f"  {r['ms_per_step'] * 1e3:.2f} us/step -> {gbs:.0f} GB/s; kernel {r['kernel']}; "
+        f"steady {r['ms_per_step_steady'] * 1e3:.3f} us/launch")
 
     secondary = []
     if not args.no_secondary:
@@ -641,11 +732,17 @@ def main():
                    "bytes_per_step": bytes_step, "flops_per_step": flops_step,
                    "weight_copies_rotated": r["copies"], "kernel": r["kernel"],
                    "ortho_plan": "built once per copy before timing (as OrthoLinear caches it)",
-                   "timing": "K launches in one HIP graph, one timed replay"},
+                   "timing": f"HIP events recorded inside one HIP graph around the K launches, "
+                             f"after {PRE_STEPS} untimed launches in the same graph"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": (load_traffic(workload) or {}).get("bytes"),
                      "launch_us": round(r["ms_per_step"] * 1e3, 3),
+                     "launch_us_steady": round(r["ms_per_step_steady"] * 1e3, 3),
+                     "steady_note": f"launch_us_steady: {STEADY_STEPS} launches in one graph, events around "
+                                    "its replay (the per-launch time a kernel trace reports); launch_us: "
+                                    "the timed K steps, which also carry the fixed cost of the two "
+                                    "in-graph timing events",
                      "bytes_per_launch": bytes_step},
         "cpu_baseline": cpu,
         "secondary": secondary,

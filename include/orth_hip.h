@@ -101,10 +101,13 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
 /* Forward pass y = Base(x) + alpha * Ortho(x).
  *   input   [batch_size, in_features] of io_dtype (F16, BF16 or F32), row-major
  *   output  [batch_size, out_features] of io_dtype, written in full
- * Picks the decode kernel (batch <= 16), the MFMA prefill kernel (batch > 16)
- * or a general kernel for shapes and dtypes the fast kernels do not take.
- * A prefill launch without a plan builds one in stream-ordered temporary
- * memory.  Replaces orth_layer_forward_cuda, /root/reference/include/ortho.h:141-144
+ * Picks, for FP16 I/O and the supported shapes, the decode kernel (batch <=
+ * 4), the mid-batch kernel (5..64), the MFMA prefill kernel (above), and a
+ * general kernel for shapes and dtypes the fast kernels do not take
+ * (orth_hip_last_kernel() names the choice).  Kernels that need scratch
+ * memory (the mid-batch split-K partials, a prefill plan when none is
+ * given) take it from a per-stream workspace or stream-ordered allocations.
+ * Replaces orth_layer_forward_cuda, /root/reference/include/ortho.h:141-144
  * (/root/reference/src/dual_gemm.cu:295-372), the body of the torch binding
  * /root/reference/torch_bind/bindings.cpp:9-44, and the CPU entry
  * orth_layer_forward, /root/reference/include/ortho.h:132-135. */

@@ -36,6 +36,11 @@ from . import _lib
 
 _DT = {torch.float16: _lib.DT_F16, torch.bfloat16: _lib.DT_BF16, torch.float32: _lib.DT_F32}
 
+# the operator boundary as the reference names it, plus this build's extensions;
+# forward_layer and make_layer (descriptor reuse for OrthoLinear) stay internal
+__all__ = ["forward", "forward_planned", "build_plan", "dequant", "pack_base", "pack_csr", "sieve_quantize",
+           "sieve_split", "sieve_hdiag", "last_kernel", "set_kernel_policy", "get_kernel_policy", "device_info"]
+
 
 def _req(cond: bool, msg: str) -> None:
     if not cond:
@@ -164,9 +169,15 @@ def forward_layer(layer, input, output, plan=None, bias=None) -> None:
     earlier for the same, unchanged weight tensors (the caller keeps them
     alive): skips re-validating and re-describing the weights on every call."""
     _check_io(input, output)
+    _req(int(input.shape[1]) == layer.base.in_features,
+         f"input has {input.shape[1]} columns, the layer {layer.base.in_features} in_features")
+    _req(int(output.shape[1]) == layer.base.out_features,
+         f"output has {output.shape[1]} columns, the layer {layer.base.out_features} out_features")
     dev = input.device
     L = _lib.lib()
     has_plan = plan is not None and plan.numel() > 0
+    if has_plan:
+        _req(plan.device == dev and plan.dtype == torch.uint8, "plan must be a uint8 tensor on input's device")
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     if bias is not None:
         _req(bias.device == dev and bias.dtype in _DT and bias.numel() == output.shape[1] and bias.is_contiguous(),

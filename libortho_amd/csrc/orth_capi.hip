@@ -38,6 +38,8 @@ bool prefill_supported(const ForwardArgs &a);
 bool plan_supported(const ForwardArgs &a);
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz);
 hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t stream);
+int64_t plan_prefill_bytes(int64_t N, int64_t K, int64_t nnz);
+hipError_t launch_plan_build_prefill(const ForwardArgs &a, void *plan, hipStream_t stream);
 hipError_t plan_read_flags(const void *plan, hipStream_t stream, uint32_t *flags);
 hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream);
 hipError_t prefill_prepare_device();
@@ -159,7 +161,7 @@ int resolve(const orth_hip_layer_t *L, const void *input, void *output, int64_t 
 // Per-device check that the current device is a gfx950 (the only code object
 // this library carries) and one-time kernel attribute set-up.
 struct DeviceState {
-    int checked = 0;  // 0 unknown, 1 ok, -1 not gfx950
+    std::atomic<int> checked{0};  // 0 unknown, 1 ok, -1 not gfx950 (published after the fields below)
     int cus = 256;
     char arch[64] = {0};
 };
@@ -173,9 +175,9 @@ int current_device_ok(int *dev_out) {
     if (dev < 0 || dev >= 64) return fail(ORTH_ERR_NO_DEVICE, "device index %d out of range", dev);
     if (dev_out) *dev_out = dev;
     DeviceState &st = g_dev[dev];
-    if (st.checked == 0) {
+    if (st.checked.load(std::memory_order_acquire) == 0) {
         std::lock_guard<std::mutex> lk(g_dev_mu);
-        if (st.checked == 0) {
+        if (st.checked.load(std::memory_order_relaxed) == 0) {
             hipDeviceProp_t p;
             e = hipGetDeviceProperties(&p, dev);
             if (e != hipSuccess) return fail_hip(e, "hipGetDeviceProperties");
@@ -187,10 +189,10 @@ int current_device_ok(int *dev_out) {
                 if (e == hipSuccess) e = plan_prepare_device();
                 if (e != hipSuccess) return fail_hip(e, "kernel attribute set-up");
             }
-            st.checked = ok ? 1 : -1;
+            st.checked.store(ok ? 1 : -1, std::memory_order_release);
         }
     }
-    if (st.checked < 0)
+    if (st.checked.load(std::memory_order_acquire) < 0)
         return fail(ORTH_ERR_NO_DEVICE, "device %d is %s; this library carries gfx950 code only", dev,
                     st.arch);
     return ORTH_OK;
@@ -199,9 +201,10 @@ int current_device_ok(int *dev_out) {
 // Split-K workspace of the mid-batch kernel, one per (device, stream): the
 // FP32 partials its reduction kernel sums.  Calls on one stream are ordered;
 // calls on different streams use different workspaces.  Allocation happens
-// on first use (and on growth) outside graph capture.  A stream captured
-// before it has a workspace borrows the device's largest one, so its graph
-// must not replay concurrently with calls on the stream that owns it.
+// on first use (and on growth) outside graph capture.  Inside a capture the
+// call gets a stream-ordered workspace of its own (hipMallocAsync before the
+// launch, hipFreeAsync after it, both recorded in the graph), so a graph
+// never shares partials with eager calls or with another graph.
 struct Workspace {
     void *buf = nullptr;
     int64_t part_bytes = 0;
@@ -210,36 +213,29 @@ std::mutex g_ws_mu;
 std::map<std::pair<int, void *>, Workspace> g_ws;
 std::vector<void *> g_ws_retired;
 
-int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part) {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    auto it = g_ws.find({dev, static_cast<void *>(stream)});
-    if (it != g_ws.end() && it->second.buf && it->second.part_bytes >= part_bytes) {
-        *part = static_cast<float *>(it->second.buf);
-        return ORTH_OK;
-    }
+// *part: the workspace; *temp: true when it is stream-ordered memory the
+// caller must release with hipFreeAsync after the launch.
+int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part, bool *temp) {
+    *temp = false;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     hipError_t e = hipStreamIsCapturing(stream, &cs);
     if (e != hipSuccess) return fail_hip(e, "hipStreamIsCapturing");
     if (cs != hipStreamCaptureStatusNone) {
-        // nothing can be allocated while a stream is captured: borrow the
-        // largest workspace of this device (frameworks capture on streams of
-        // their own, after eager warm-up calls on another)
-        const Workspace *best = nullptr;
-        for (const auto &kv : g_ws)
-            if (kv.first.first == dev && kv.second.buf && kv.second.part_bytes >= part_bytes &&
-                (!best || kv.second.part_bytes > best->part_bytes))
-                best = &kv.second;
-        if (!best)
-            return fail(ORTH_ERR_UNSUPPORTED,
-                        "the mid-batch kernel needs a %lld-byte workspace; run the call once outside "
-                        "graph capture first", (long long)part_bytes);
-        *part = static_cast<float *>(best->buf);
+        void *tmp = nullptr;
+        e = hipMallocAsync(&tmp, (size_t)part_bytes, stream);
+        if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (mid-batch workspace in a captured graph)");
+        *part = static_cast<float *>(tmp);
+        *temp = true;
         return ORTH_OK;
     }
+    std::lock_guard<std::mutex> lk(g_ws_mu);
     Workspace &w = g_ws[{dev, static_cast<void *>(stream)}];
+    if (w.buf && w.part_bytes >= part_bytes) {
+        *part = static_cast<float *>(w.buf);
+        return ORTH_OK;
+    }
     if (w.buf) {
-        // a smaller buffer is retired, not freed: in-flight work or a
-        // captured graph may still use it
+        // a smaller buffer is retired, not freed: in-flight work may still use it
         g_ws_retired.push_back(w.buf);
         w = Workspace();
     }
@@ -312,21 +308,27 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
         const int cus = g_dev[dev].cus;
         const int64_t pbytes = skinny_workspace_bytes(a, cus);
         float *part = nullptr;
+        bool temp = false;
         if (pbytes > 0) {
-            rc = workspace_for(dev, stream, pbytes, &part);
+            rc = workspace_for(dev, stream, pbytes, &part, &temp);
             if (rc != ORTH_OK) return rc;
         }
         // without a plan the kernel filters each row's CSR by column
         e = launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
+        if (temp) {
+            hipError_t f = hipFreeAsync(part, stream);
+            if (e == hipSuccess) e = f;
+        }
     } else if (kernel == KERNEL_PREFILL) {
         if (a.has_ortho && !plan) {
-            // stream-ordered temporary plan: allocated, built, used and freed
-            // in stream order, so the call stays asynchronous
-            const int64_t pb = plan_bytes_for(a.N, a.K, a.nnz);
+            // stream-ordered temporary plan (its prefill part): allocated,
+            // built, used and freed in stream order, so the call stays
+            // asynchronous
+            const int64_t pb = plan_prefill_bytes(a.N, a.K, a.nnz);
             void *tmp = nullptr;
             e = hipMallocAsync(&tmp, (size_t)pb, stream);
             if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (temporary ortho plan)");
-            e = launch_plan_build(a, tmp, stream);
+            e = launch_plan_build_prefill(a, tmp, stream);
             if (e == hipSuccess) e = launch_prefill(a, tmp, stream);
             hipError_t f = hipFreeAsync(tmp, stream);
             if (e == hipSuccess) e = f;

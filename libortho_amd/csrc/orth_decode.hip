@@ -11,9 +11,10 @@
 //    inside the workgroup, reduced through LDS: deterministic, no atomics).
 //  * Per chunk every lane issues ONE 16-byte nontemporal load: lane (row
 //    r = lane%16, quarter g = lane/16) takes bytes [64c + 16g, +16) of row r.
-//    Every load of the kernel is issued at entry, before anything waits, and
-//    none is scattered: measured on MI355X, per-lane 2- and 4-byte loads
-//    touching 16 rows per instruction cost more than the weight stream.
+//    The first chunk pairs are issued at entry and the rest a fixed number
+//    of pairs ahead of the main loop; none is scattered: measured on MI355X,
+//    per-lane 2- and 4-byte loads touching 16 rows per instruction cost more
+//    than the weight stream.
 //  * Each 32-bit word (8 nibbles) becomes 8 FP16 values in registers and
 //    feeds v_mfma_f32_16x16x32_f16 as the B operand; the activations (tokens
 //    padded to 16) are the A operand.  The tensor core does the K reduction.
@@ -41,6 +42,7 @@
 //    flight; no workgroup barrier is needed since a wave's entries use only
 //    the activations it staged.  A quarter whose entries did not fit its
 //    record reads the rows' CSR, filtered to the quarter's columns.
+#include <atomic>
 #include <type_traits>
 
 #include "orth_common.h"
@@ -709,14 +711,16 @@ static int64_t decode_lds_layout(DecodeArgs &d, int mt, bool xlds, int cpw_bound
 
 template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, int PD>
 static hipError_t launch_decode_kp(const DecodeArgs &d, int64_t lds, hipStream_t stream) {
-    // more than 64 KB of dynamic LDS must be allowed once per device
-    static int allowed[64] = {0};
+    // more than 64 KB of dynamic LDS must be allowed once per device (the
+    // attribute call is idempotent, so two threads racing to set it is harmless)
+    static std::atomic<int> allowed[64];
     int dev = 0;
-    if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !allowed[dev]) {
+    if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 &&
+        !allowed[dev].load(std::memory_order_acquire)) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecodeLdsMax);
         if (e != hipSuccess) return e;
-        allowed[dev] = 1;
+        allowed[dev].store(1, std::memory_order_release);
     }
     const unsigned blocks = (unsigned)((d.N + 15) / 16);
     hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD>), dim3(blocks), dim3(kDecodeNT),

@@ -20,10 +20,12 @@
 //
 // Bandwidth: every kernel reads W once from HBM (the per-row kernel keeps
 // the row in registers between its two passes) and writes q, the scales or
-// the CSR arrays once.  The CSR is built in three launches: per-row counts,
-// one scan, and a fill that re-reads W (the counts are needed to place a
-// row's entries); the host reads row_ptr[N] between the first two and the
-// fill to size the outputs.
+// the CSR arrays once.  The CSR is built in three launches: per-row counts
+// (which also record each element's nonzero bit in a mask when the caller
+// gives one), one scan, and a fill that reads the mask and only the nonzero
+// elements of W (without a mask it reads W again); the counts place each
+// row's entries, and the host reads row_ptr[N] between the first two and
+// the fill to size the outputs.
 #include "orth_common.h"
 
 namespace orth {

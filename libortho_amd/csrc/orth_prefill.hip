@@ -3,9 +3,10 @@
 // Design intent of /root/reference/src/dual_gemm_tensor_core.cu:215-337
 // (matrix-core base GEMM with the ortho term fused), built for CDNA4:
 //
-//  * Workgroup tile 256 tokens x 128 output rows, 4 waves in a 2x2 grid,
-//    each wave 128x64 with v_mfma_f32_32x32x16_f16 (FP32 accumulation).
-//    K advances in steps of 64 through double-buffered LDS tiles.
+//  * Workgroup tile 256 tokens x 128 output rows, 8 waves in a 4x2 grid,
+//    each wave 64x64 with v_mfma_f32_32x32x16_f16 (FP32 accumulation).
+//    K advances in steps of 64 through LDS: activations in 2 stages,
+//    dequantised weights in 3.
 //  * The activation tile is copied to LDS as is.  The INT4 weight tile is
 //    dequantised on the way in: each thread turns one 16-byte load (32
 //    nibbles of one row) into 32 FP16 weights q*s (one rounding of the exact
@@ -338,6 +339,28 @@ hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t strea
         hipLaunchKernelGGL(plan_cell_kernel, dim3(ngroups * (unsigned)nslices), dim3(64), 0, stream, a, srec,
                            swords, nslices, 1024, kCellSlice);
     }
+    return hipGetLastError();
+}
+
+// The prefill part of a plan alone (header, offsets, entries; no chunk
+// table and no cell records): what a prefill launch without a caller's plan
+// builds for itself.  Its header says it holds no records.
+int64_t plan_prefill_bytes(int64_t N, int64_t K, int64_t nnz) {
+    if (nnz <= 0) return 0;
+    return plan_chunks_at(N, K, nnz);
+}
+
+hipError_t launch_plan_build_prefill(const ForwardArgs &a, void *plan, hipStream_t stream) {
+    const int nblocks = (int)((a.N + kPlanBN - 1) / kPlanBN);
+    const int nksteps = (int)(a.K / kPlanBK);
+    PlanHeader *h = static_cast<PlanHeader *>(plan);
+    int32_t *offsets = reinterpret_cast<int32_t *>(static_cast<char *>(plan) + sizeof(PlanHeader));
+    uint32_t *entries = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(offsets) +
+                                                     plan_offsets_bytes(a.N, a.K));
+    hipLaunchKernelGGL(plan_init_kernel, dim3(1), dim3(64), 0, stream, h, nblocks, nksteps, a.N, a.K, a.nnz, 0, 0);
+    const size_t lds = ((size_t)nksteps * kPlanBN + 256) * sizeof(int32_t);
+    hipLaunchKernelGGL(plan_build_kernel, dim3(nblocks), dim3(256), lds, stream, a, h, offsets, entries,
+                       static_cast<uint16_t *>(nullptr), nksteps);
     return hipGetLastError();
 }
 

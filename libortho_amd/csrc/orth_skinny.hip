@@ -42,6 +42,8 @@
 //    this part write back and invalidate the L2 of every XCD.)
 #include <algorithm>
 
+#include <atomic>
+
 #include "orth_common.h"
 
 namespace orth {
@@ -655,14 +657,16 @@ bool skinny_supported(const ForwardArgs &a) {
 
 template <int NTT, int GMODE, int CPS, int SPARSE>
 static hipError_t skinny_launch_t(const SkinnyArgs &d, int blocks, int lds, hipStream_t s) {
-    // more than 64 KB of dynamic LDS must be allowed once per device
-    static int allowed[64] = {0};
+    // more than 64 KB of dynamic LDS must be allowed once per device (the
+    // attribute call is idempotent, so two threads racing to set it is harmless)
+    static std::atomic<int> allowed[64];
     int dev = 0;
-    if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !allowed[dev]) {
+    if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 &&
+        !allowed[dev].load(std::memory_order_acquire)) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(skinny_kernel<NTT, GMODE, CPS, SPARSE>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
         if (e != hipSuccess) return e;
-        allowed[dev] = 1;
+        allowed[dev].store(1, std::memory_order_release);
     }
     hipLaunchKernelGGL((skinny_kernel<NTT, GMODE, CPS, SPARSE>), dim3(blocks), dim3(kSkNT), (uint32_t)lds, s, d);
     return hipGetLastError();

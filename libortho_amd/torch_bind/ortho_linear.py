@@ -144,15 +144,24 @@ class OrthoLinear(nn.Module):
 
     # ------------------------------------------------------------------ plan
     def _csr_key(self):
+        # the tensors themselves (compared by identity, kept alive by the key,
+        # so a new tensor reusing a freed block is never taken for the old
+        # one) and their versions (in-place writes)
         ts = (self.ortho_values, self.ortho_col_indices, self.ortho_row_ptr)
-        return tuple((t.data_ptr(), t.numel(), t._version, str(t.device)) for t in ts)
+        return ts, tuple((t._version, t.data_ptr(), t.numel()) for t in ts)
+
+    def _plan_valid(self, key) -> bool:
+        if self._plan_key is None:
+            return False
+        (ts0, v0), (ts1, v1) = self._plan_key, key
+        return all(a is b for a, b in zip(ts0, ts1)) and v0 == v1
 
     def _ortho_plan(self):
         """The cached ortho plan, rebuilt when the CSR buffers change."""
         if self.ortho_values.numel() == 0 or not self.ortho_values.is_cuda:
             return None
         key = self._csr_key()
-        if self._plan_key != key:
+        if not self._plan_valid(key):
             self._plan = _C.build_plan(self.base_weight, self.base_scales, self.ortho_values,
                                        self.ortho_col_indices, self.ortho_row_ptr, self.in_features)
             self._plan_key = key
@@ -217,22 +226,25 @@ class OrthoLinear(nn.Module):
         def get(name):
             return state_dict.get(prefix + name)
 
+        # every check first: the module is changed only once the whole
+        # checkpoint has been found consistent
         bw = get("base_weight")
         if bw is not None and tuple(bw.shape) != (N, K // 2):
             error_msgs.append(f"{prefix}base_weight: expected [{N}, {K // 2}] packed INT4, got {list(bw.shape)}")
             return
         bs = get("base_scales")
+        group = self.group_size
         if bs is not None:
             if bs.dim() == 1 and bs.shape[0] == N:
-                self.group_size = None
+                group = None
             elif bs.dim() == 2 and bs.shape[0] == N and bs.shape[1] > 0 and K % bs.shape[1] == 0:
-                self.group_size = K // int(bs.shape[1])
+                group = K // int(bs.shape[1])
             else:
                 error_msgs.append(f"{prefix}base_scales: expected [{N}] or [{N}, in/G], got {list(bs.shape)}")
                 return
-            self.base_scales = torch.zeros(tuple(bs.shape), dtype=torch.float16, device=dev)
         vals, col, rp = get("ortho_values"), get("ortho_col_indices"), get("ortho_row_ptr")
-        if vals is not None or col is not None or rp is not None:
+        has_csr = vals is not None or col is not None or rp is not None
+        if has_csr:
             if vals is None or col is None or rp is None:
                 error_msgs.append(f"{prefix}ortho_*: the three CSR buffers must be saved together")
                 return
@@ -244,6 +256,10 @@ class OrthoLinear(nn.Module):
                 error_msgs.append(f"{prefix}ortho CSR: row_ptr must have {N + 1} entries from 0 to nnz and "
                                   f"col_indices nnz entries (got {rp.numel()}, {col.numel()}, nnz {nnz})")
                 return
+        if bs is not None:
+            self.group_size = group
+            self.base_scales = torch.zeros(tuple(bs.shape), dtype=torch.float16, device=dev)
+        if has_csr:
             self.ortho_values = torch.zeros(nnz, dtype=torch.float16, device=dev)
             self.ortho_col_indices = torch.zeros(nnz, dtype=torch.int32, device=dev)
             self.ortho_row_ptr = torch.zeros(rp.numel(), dtype=torch.int32, device=dev)

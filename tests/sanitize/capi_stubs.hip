@@ -1,0 +1,45 @@
+// Host-only stand-ins for the kernel launchers of libortho_amd, so that the
+// C ABI's host side (orth_capi.hip: validation, dispatch, error reporting)
+// can be built alone under AddressSanitizer and UBSan and driven on a
+// machine without a GPU (tests/test_sanitizers.py).  Every launcher fails
+// and every capability query says "no"; the driver only reaches them through
+// paths that stop at the device check.
+#include "orth_common.h"
+
+namespace orth {
+hipError_t launch_general(const ForwardArgs &, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t launch_dequant(const ForwardArgs &, float *, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t launch_pack_base(const void *, int, int64_t, int64_t, int64_t, const void *, int, uint8_t *, void *,
+                            hipStream_t) { return hipErrorInvalidValue; }
+int pack_base_path(const void *, int, int64_t, int64_t, const void *) { return 3; }
+int64_t csr_mask_bytes(const void *, int, int64_t N, int64_t K) { return ((N * K + 31) / 32) * 4; }
+hipError_t launch_csr_rows(const void *, int, int64_t, int64_t, int32_t *, void *, hipStream_t) {
+    return hipErrorInvalidValue;
+}
+hipError_t launch_csr_fill(const void *, int, int64_t, int64_t, const int32_t *, const void *, int32_t *, void *, int,
+                           hipStream_t) { return hipErrorInvalidValue; }
+bool decode_supported(const ForwardArgs &) { return false; }
+hipError_t launch_decode(const ForwardArgs &, const void *, int, hipStream_t) { return hipErrorInvalidValue; }
+bool prefill_supported(const ForwardArgs &) { return false; }
+bool plan_supported(const ForwardArgs &a) { return a.K % 64 == 0 && a.K <= 12288; }
+int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) { return nnz > 0 ? 64 + 4 * nnz + N + K : 0; }
+hipError_t launch_plan_build(const ForwardArgs &, void *, hipStream_t) { return hipErrorInvalidValue; }
+int64_t plan_prefill_bytes(int64_t N, int64_t K, int64_t nnz) { return nnz > 0 ? 64 + 4 * nnz + N + K : 0; }
+hipError_t launch_plan_build_prefill(const ForwardArgs &, void *, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t plan_read_flags(const void *, hipStream_t, uint32_t *) { return hipErrorInvalidValue; }
+hipError_t launch_prefill(const ForwardArgs &, const void *, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t prefill_prepare_device() { return hipSuccess; }
+hipError_t plan_prepare_device() { return hipSuccess; }
+bool skinny_supported(const ForwardArgs &) { return false; }
+int64_t skinny_workspace_bytes(const ForwardArgs &, int) { return 0; }
+hipError_t launch_skinny(const ForwardArgs &, const void *, int, float *, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t launch_sieve_quantize(const void *, int, int64_t, int64_t, void *, hipStream_t) {
+    return hipErrorInvalidValue;
+}
+hipError_t launch_sieve_split(const void *, int, int64_t, int64_t, const void *, int, int64_t, int, int, int64_t, float,
+                              void *, void *, float *, void *, hipStream_t) { return hipErrorInvalidValue; }
+int64_t sieve_hdiag_slices(int64_t n) { return n < 64 ? (n > 0 ? n : 1) : 64; }
+hipError_t launch_sieve_hdiag(const void *, int, int64_t, int64_t, float *, void *, hipStream_t) {
+    return hipErrorInvalidValue;
+}
+}  // namespace orth

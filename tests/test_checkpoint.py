@@ -104,3 +104,22 @@ def test_an_empty_csr_checkpoint_loads():
     m = OrthoLinear(256, 32)
     m.load_state_dict(dict(sd, ortho_row_ptr=torch.tensor([], dtype=torch.int32)))
     assert m.ortho_values.numel() == 0 and m.ortho_row_ptr.numel() == 0
+
+
+def test_a_refused_checkpoint_leaves_the_module_unchanged():
+    """Every check runs before any buffer is replaced: a checkpoint whose
+    group scales are valid but whose CSR is not leaves group_size, the
+    scales and the CSR as they were."""
+    lay, sd = reference_state_dict(256, 64, 0.02, seed=9)
+    m = OrthoLinear(256, 64, bias=True)
+    m.load_state_dict(sd)
+    before = {k: v.clone() for k, v in m.state_dict().items()}
+    bad = dict(sd)
+    bad["base_scales"] = torch.ones(64, 2, dtype=torch.float16)      # valid group-128 layout
+    bad["ortho_row_ptr"] = sd["ortho_row_ptr"].clone()
+    bad["ortho_row_ptr"][-1] += 1                                    # does not end at nnz
+    with pytest.raises(RuntimeError):
+        m.load_state_dict(bad)
+    assert m.group_size is None
+    for k, v in m.state_dict().items():
+        assert torch.equal(v, before[k]), k

@@ -580,3 +580,72 @@ def test_empty_batch_is_a_no_op():
     L = W.make_layer(256, 64, 128, 0.02, seed=7)
     y, k = run(L, np.zeros((0, 256), np.float16), 1.0)
     assert y.shape == (0, 64) and k == "none"
+
+
+def test_forward_layer_checks_the_io_shapes():
+    L = W.make_layer(512, 384, 128, 0.01, seed=77)
+    d = W.to_device(L)
+    desc = _C_ops.make_layer(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], L.K, L.N, 1.0,
+                             torch.device("cuda:0"))
+    x = torch.zeros(2, L.K + 64, dtype=torch.float16, device="cuda")
+    y = torch.zeros(2, L.N, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="in_features"):
+        _C_ops.forward_layer(desc, x, y)
+    x = torch.zeros(2, L.K, dtype=torch.float16, device="cuda")
+    y = torch.zeros(2, L.N - 16, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="out_features"):
+        _C_ops.forward_layer(desc, x, y)
+
+
+def test_plan_cache_follows_replaced_csr_buffers(oracle_mod):
+    """Two CSR replacements in a row with no forward between them (the
+    second may reuse the first's freed blocks): the next forward rebuilds
+    the plan and matches the oracle on the final buffers."""
+    from libortho_amd import OrthoLinear
+    K, N = 1024, 512
+    a = W.make_layer(K, N, None, 0.02, seed=81)
+    m = OrthoLinear(K, N)
+    m.load_state_dict({"base_weight": torch.from_numpy(a.q), "base_scales": torch.from_numpy(a.scales),
+                       "ortho_values": torch.from_numpy(a.vals), "ortho_col_indices": torch.from_numpy(a.col),
+                       "ortho_row_ptr": torch.from_numpy(a.row_ptr)})
+    m = m.cuda()
+    x_np = W.make_x(2, K, 82)
+    x = torch.from_numpy(x_np).cuda()
+    with torch.no_grad():
+        m(x)
+        for seed in (83, 84):
+            b = W.make_layer(K, N, None, 0.02, seed=seed)
+            m.ortho_values = torch.from_numpy(b.vals).cuda()
+            m.ortho_col_indices = torch.from_numpy(b.col).cuda()
+            m.ortho_row_ptr = torch.from_numpy(b.row_ptr).cuda()
+        y = m(x).float().cpu().numpy()
+    ref = oracle_mod.forward_f64(a.q, a.scales, b.row_ptr, b.col, b.vals, x_np, 1.0)
+    assert_close(y, ref, tol=2e-3, what="replaced CSR")
+
+
+@pytest.mark.parametrize("M", [8, 32])
+def test_mid_batch_forward_captured_on_a_fresh_stream(c2, M):
+    """A mid-batch forward captured in a HIP graph on a stream that never
+    ran it eagerly (its split-K workspace is allocated inside the graph),
+    replayed several times with eager forwards of other shapes between the
+    replays: every replay equals the eager result bit for bit."""
+    d = W.to_device(c2)
+    plan = _C_ops.build_plan(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], c2.K)
+    x = torch.from_numpy(W.make_x(M, c2.K, 2700 + M)).cuda()
+    y_eager = torch.empty(M, c2.N, dtype=torch.float16, device="cuda")
+    _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y_eager, 1.0, plan)
+    assert _C_ops.last_kernel() == "skinny"
+    torch.cuda.synchronize()
+    y = torch.empty_like(y_eager)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=s):
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y, 1.0, plan)
+    x2 = torch.from_numpy(W.make_x(24, c2.K, 2799)).cuda()
+    y2 = torch.empty(24, c2.N, dtype=torch.float16, device="cuda")
+    for r in range(4):
+        y.fill_(float("nan"))
+        g.replay()
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x2, y2, 1.0, plan)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y_eager.view(torch.int16)), f"replay {r}"
