@@ -131,6 +131,26 @@ int orth_layer_forward_hip_ex(const orth_hip_layer_t *layer, const void *plan, i
                               const void *bias, int32_t bias_dtype, const void *input, void *output,
                               int64_t batch_size, int32_t io_dtype, void *stream);
 
+/* Same as orth_layer_forward_hip_ex, but it allocates nothing: no
+ * hipMalloc, hipFree or stream-ordered allocation, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it).  No counterpart in the reference.  The scratch memory the
+ * kernels need (the mid-batch kernel's split-K partials, the prefill part of
+ * an ortho plan when the caller passes none) comes from a static device
+ * array of ORTH_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends;
+ * a call that would need more returns ORTH_ERR_UNSUPPORTED before launching
+ * anything.  Every call on one GPU shares that GPU's array: calls that
+ * overlap in time on one GPU (two streams, or two threads) race and give
+ * wrong results; calls ordered on one stream are safe.  Each call writes all
+ * the scratch it reads, so nothing carries over from an earlier call. */
+#define ORTH_NOALLOC_SCRATCH_BYTES (32u << 20)
+int orth_layer_forward_hip_noalloc(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
+                                   const void *bias, int32_t bias_dtype, const void *input, void *output,
+                                   int64_t batch_size, int32_t io_dtype, void *stream);
+
+/* ORTH_NOALLOC_SCRATCH_BYTES, for bindings that cannot read the macro. */
+int64_t orth_noalloc_scratch_bytes(void);
+
 /* Size in bytes of the ortho plan for this layer (0 when count == 0), or a
  * negative orth_status_t on invalid arguments. */
 int64_t orth_ortho_plan_bytes(const orth_hip_layer_t *layer);

@@ -59,6 +59,8 @@ SIGNATURES = {
     "orth_layer_forward_hip": (ctypes.c_int, [_LP, _P, _P, _I64, _I32, _P]),
     "orth_layer_forward_hip_planned": (ctypes.c_int, [_LP, _P, _I64, _P, _P, _I64, _I32, _P]),
     "orth_layer_forward_hip_ex": (ctypes.c_int, [_LP, _P, _I64, _P, _I32, _P, _P, _I64, _I32, _P]),
+    "orth_layer_forward_hip_noalloc": (ctypes.c_int, [_LP, _P, _I64, _P, _I32, _P, _P, _I64, _I32, _P]),
+    "orth_noalloc_scratch_bytes": (_I64, []),
     "orth_ortho_plan_bytes": (_I64, [_LP]),
     "orth_ortho_plan_build": (ctypes.c_int, [_LP, _P, _I64, _P]),
     "orth_base_dequant_hip": (ctypes.c_int, [_LP, _P, _P]),

@@ -158,12 +158,22 @@ int resolve(const orth_hip_layer_t *L, const void *input, void *output, int64_t 
     return ORTH_OK;
 }
 
+// Scratch memory of orth_layer_forward_hip_noalloc: one array per device
+// (each GPU holds its own copy for the life of the process).  Host code
+// never passes the array's name to a kernel: that is a host-side stand-in,
+// not a device address.  Its device address is looked up once per device
+// (hipGetSymbolAddress, in the device set-up below) and only that pointer
+// is used.
+static __device__ __align__(256) unsigned char scratch[ORTH_NOALLOC_SCRATCH_BYTES];
+
 // Per-device check that the current device is a gfx950 (the only code object
-// this library carries) and one-time kernel attribute set-up.
+// this library carries), one-time kernel attribute set-up, and the device
+// address of the scratch array.
 struct DeviceState {
     std::atomic<int> checked{0};  // 0 unknown, 1 ok, -1 not gfx950 (published after the fields below)
     int cus = 256;
     char arch[64] = {0};
+    void *scratch = nullptr;      // device address of this device's scratch array
 };
 std::mutex g_dev_mu;
 DeviceState g_dev[64];
@@ -188,6 +198,10 @@ int current_device_ok(int *dev_out) {
                 e = prefill_prepare_device();
                 if (e == hipSuccess) e = plan_prepare_device();
                 if (e != hipSuccess) return fail_hip(e, "kernel attribute set-up");
+                void *ptr = nullptr;
+                e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+                if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress (scratch)");
+                st.scratch = ptr;
             }
             st.checked.store(ok ? 1 : -1, std::memory_order_release);
         }
@@ -246,9 +260,11 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part,
     return ORTH_OK;
 }
 
+// noalloc: scratch from the device's scratch array instead of the stream's
+// workspace or stream-ordered allocations (orth_layer_forward_hip_noalloc).
 int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
                  const void *input, void *output, int64_t batch, int32_t io_dtype, void *stream_v,
-                 const void *bias = nullptr, int32_t bias_dtype = ORTH_DT_F32) {
+                 const void *bias = nullptr, int32_t bias_dtype = ORTH_DT_F32, bool noalloc = false) {
     ForwardArgs a;
     int rc = resolve(layer, input, output, batch, io_dtype, true, a);
     if (rc != ORTH_OK) return rc;
@@ -309,7 +325,13 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
         const int64_t pbytes = skinny_workspace_bytes(a, cus);
         float *part = nullptr;
         bool temp = false;
-        if (pbytes > 0) {
+        if (pbytes > 0 && noalloc) {
+            if (pbytes > (int64_t)ORTH_NOALLOC_SCRATCH_BYTES)
+                return fail(ORTH_ERR_UNSUPPORTED,
+                            "the mid-batch kernel needs %lld bytes of scratch for this call; the no-allocation "
+                            "entry point has %lld", (long long)pbytes, (long long)ORTH_NOALLOC_SCRATCH_BYTES);
+            part = static_cast<float *>(g_dev[dev].scratch);
+        } else if (pbytes > 0) {
             rc = workspace_for(dev, stream, pbytes, &part, &temp);
             if (rc != ORTH_OK) return rc;
         }
@@ -320,7 +342,17 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
             if (e == hipSuccess) e = f;
         }
     } else if (kernel == KERNEL_PREFILL) {
-        if (a.has_ortho && !plan) {
+        if (a.has_ortho && !plan && noalloc) {
+            // the prefill part of a plan, built in the scratch array
+            const int64_t pb = plan_prefill_bytes(a.N, a.K, a.nnz);
+            if (pb > (int64_t)ORTH_NOALLOC_SCRATCH_BYTES)
+                return fail(ORTH_ERR_UNSUPPORTED,
+                            "the prefill kernel needs a %lld-byte ortho plan for this layer; the no-allocation "
+                            "entry point has %lld bytes of scratch (pass a plan from orth_ortho_plan_build)",
+                            (long long)pb, (long long)ORTH_NOALLOC_SCRATCH_BYTES);
+            e = launch_plan_build_prefill(a, g_dev[dev].scratch, stream);
+            if (e == hipSuccess) e = launch_prefill(a, g_dev[dev].scratch, stream);
+        } else if (a.has_ortho && !plan) {
             // stream-ordered temporary plan (its prefill part): allocated,
             // built, used and freed in stream order, so the call stays
             // asynchronous
@@ -374,6 +406,15 @@ int orth_layer_forward_hip_ex(const orth_hip_layer_t *layer, const void *plan, i
     return forward_impl(layer, plan, plan_bytes, input, output, batch_size, io_dtype, stream, bias,
                         bias_dtype);
 }
+
+int orth_layer_forward_hip_noalloc(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
+                                   const void *bias, int32_t bias_dtype, const void *input, void *output,
+                                   int64_t batch_size, int32_t io_dtype, void *stream) {
+    return forward_impl(layer, plan, plan_bytes, input, output, batch_size, io_dtype, stream, bias, bias_dtype,
+                        true);
+}
+
+int64_t orth_noalloc_scratch_bytes(void) { return (int64_t)ORTH_NOALLOC_SCRATCH_BYTES; }
 
 int64_t orth_ortho_plan_bytes(const orth_hip_layer_t *layer) {
     ForwardArgs a;

@@ -111,6 +111,11 @@ int main(void) {
     expect(orth_layer_forward_hip_ex(&L, NULL, 0, sbuf, 9, xbuf, ybuf, 2, ORTH_DT_F16, NULL),
            ORTH_ERR_INVALID_ARGUMENT, "bias dtype");
     expect(orth_ortho_plan_build(&L, NULL, 0, NULL), ORTH_ERR_INVALID_ARGUMENT, "plan build NULL");
+    expect(orth_layer_forward_hip_noalloc(&L, NULL, 0, NULL, 0, xbuf, ybuf, 2, ORTH_DT_F16, NULL), ORTH_ERR_NO_DEVICE,
+           "noalloc no device");
+    expect(orth_layer_forward_hip_noalloc(NULL, NULL, 0, NULL, 0, xbuf, ybuf, 2, ORTH_DT_F16, NULL),
+           ORTH_ERR_INVALID_ARGUMENT, "noalloc NULL layer");
+    if (orth_noalloc_scratch_bytes() != (int64_t)ORTH_NOALLOC_SCRATCH_BYTES) failures++;
     expect(orth_base_dequant_hip(&L, NULL, NULL), ORTH_ERR_INVALID_ARGUMENT, "dequant NULL out");
     /* packing and sieve argument checks */
     expect(orth_pack_base_hip(NULL, ORTH_DT_F32, 4, 8, 8, NULL, 0, qbuf, sbuf, NULL), ORTH_ERR_INVALID_ARGUMENT,
