@@ -216,9 +216,12 @@ int current_device_ok(int *dev_out) {
 // FP32 partials its reduction kernel sums.  Calls on one stream are ordered;
 // calls on different streams use different workspaces.  Allocation happens
 // on first use (and on growth) outside graph capture.  Inside a capture the
-// call gets a stream-ordered workspace of its own (hipMallocAsync before the
-// launch, hipFreeAsync after it, both recorded in the graph), so a graph
-// never shares partials with eager calls or with another graph.
+// call uses the capturing stream's own workspace when it has one large
+// enough (the graph is then ordered with that stream's work when it is
+// replayed on that stream, the usual pattern of eager warm-up, capture and
+// replay); otherwise it gets a stream-ordered workspace of its own
+// (hipMallocAsync before the launch, hipFreeAsync after it, both recorded
+// in the graph).  A capture never takes another stream's workspace.
 struct Workspace {
     void *buf = nullptr;
     int64_t part_bytes = 0;
@@ -235,6 +238,14 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part,
     hipError_t e = hipStreamIsCapturing(stream, &cs);
     if (e != hipSuccess) return fail_hip(e, "hipStreamIsCapturing");
     if (cs != hipStreamCaptureStatusNone) {
+        {
+            std::lock_guard<std::mutex> lk(g_ws_mu);
+            auto it = g_ws.find({dev, static_cast<void *>(stream)});
+            if (it != g_ws.end() && it->second.buf && it->second.part_bytes >= part_bytes) {
+                *part = static_cast<float *>(it->second.buf);
+                return ORTH_OK;
+            }
+        }
         void *tmp = nullptr;
         e = hipMallocAsync(&tmp, (size_t)part_bytes, stream);
         if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (mid-batch workspace in a captured graph)");
