@@ -70,6 +70,9 @@ def parse():
     ap.add_argument("--profile", action="store_true",
                     help="eager launches for rocprofv3 --pmc: decode c2 M=1 (alpha 1 and 0), "
                          "prefill c3 M=2048, then a plain device copy of known size")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="six eager planned prefill forwards at c3 (M=2048, alpha=1), for counter passes "
+                         "of rocprofv3 --pmc over the prefill kernel alone")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two --profile counter runs into profiles/traffic.json")
     return ap.parse_args()
@@ -613,6 +616,19 @@ def main():
     if args.profile:
         import torch
         profile_run(torch)
+        return
+    if args.profile_prefill:
+        import torch
+        from libortho_amd import _C_ops, workloads as W
+        c3 = W.config_layer("c3")
+        d = W.to_device(c3)
+        plan = _C_ops.build_plan(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], c3.K)
+        x = torch.from_numpy(W.make_x(2048, c3.K, 9048)).cuda()
+        y = torch.empty(2048, c3.N, dtype=torch.float16, device="cuda")
+        for _ in range(6):
+            _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y, 1.0, plan)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_prefill": "done", "kernel": _C_ops.last_kernel(), "launches": 6}), flush=True)
         return
 
     from libortho_amd import workloads as W

@@ -458,6 +458,21 @@ __device__ __forceinline__ void pf_store_a(const PfLane &L, const PfA &r, f16 *A
     for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4 *>(As + pf_swz(L.arow[i], L.achunk[i])) = r.v[i];
 }
 
+// Byte i of word w (weights 2i, 2i+1, low nibble first) as the FP16 pair
+// (q_2i * s, q_2i+1 * s), one rounding of each exact product: the byte is
+// copied into both halves (v_perm), one and-xor keeps the low nibble in
+// bits 0..3 of the low half under 1024.0 (0x6400) and the high nibble in
+// bits 4..7 of the high half under 64.0 (0x5400), so the halves read
+// 1024 + u and 64 + u with u = n ^ 8 = q + 8 (the xor by 8 folded into the
+// constant); subtracting (1032, 72) gives q exactly, then the scale.
+__device__ __forceinline__ uint32_t dq_byte(uint32_t w, f16x2 s2, int i) {
+    const uint32_t sel = 0x0c000c00u | (uint32_t)(i * 0x00010001u);
+    const uint32_t b = __builtin_amdgcn_perm(0u, w, sel);
+    const uint32_t p = (b & 0x00F0000Fu) ^ 0x54806408u;
+    const f16x2 bias = {(f16)-1032.0f, (f16)-72.0f};
+    return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p) + bias) * s2);
+}
+
 __device__ __forceinline__ void pf_store_b(const PfB &r, f16 *Bs) {
     const f16 sc = __builtin_bit_cast(f16, (uint16_t)r.s);
     const f16x2 s2 = {sc, sc};
@@ -465,9 +480,9 @@ __device__ __forceinline__ void pf_store_b(const PfB &r, f16 *Bs) {
     const uint32_t words[2] = {r.v.x, r.v.y};
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        uint32_t o[4];
-        int4x8_to_f16_scaled(words[j], s2, o);
-        *reinterpret_cast<u32x4 *>(Bs + pf_swz(row, c0 + j)) = u32x4{o[0], o[1], o[2], o[3]};
+        const u32x4 o = {dq_byte(words[j], s2, 0), dq_byte(words[j], s2, 1), dq_byte(words[j], s2, 2),
+                         dq_byte(words[j], s2, 3)};
+        *reinterpret_cast<u32x4 *>(Bs + pf_swz(row, c0 + j)) = o;
     }
 }
 
@@ -721,12 +736,9 @@ hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t st
     p.nbm = (int)((a.M + PF_BM - 1) / PF_BM);
     p.nbn = (int)((a.N + PF_BN - 1) / PF_BN);
     const unsigned blocks = (unsigned)(p.nbm * p.nbn);
-    if (p.fold) {
-        if (p.nnz <= 0) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(prefill_kernel<true>, dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
-    } else {
-        hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
-    }
+    if (p.fold && p.nnz <= 0) return hipErrorInvalidValue;
+    if (p.fold) hipLaunchKernelGGL(prefill_kernel<true>, dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    else hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
     return hipGetLastError();
 }
 
