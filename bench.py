@@ -147,6 +147,7 @@ class Rotation:
                  plan=False):
         from libortho_amd import _C_ops, workloads as W
         d = W.to_device(layer)
+        self.K, self.N = layer.K, layer.N
         per = sum(t.numel() * t.element_size() for t in d.values())
         self.n = max(min_copies, -(-min_bytes // per))
         self.copies = [d] + [{k: v.clone() for k, v in d.items()} for _ in range(self.n - 1)]
@@ -154,6 +155,18 @@ class Rotation:
         if plan:
             self.plans = [_C_ops.build_plan(c["q"], c["scales"], c["vals"], c["col"], c["row_ptr"],
                                             layer.K) for c in self.copies]
+
+    def desc(self, i, alpha):
+        """The C descriptor of copy i % n (built once per copy and alpha)."""
+        from libortho_amd import _C_ops
+        k = (i % self.n, float(alpha))
+        if not hasattr(self, "_descs"):
+            self._descs = {}
+        if k not in self._descs:
+            c = self.copies[k[0]]
+            self._descs[k] = _C_ops.make_layer(c["q"], c["scales"], c["vals"], c["col"], c["row_ptr"],
+                                               self.K, self.N, alpha, c["q"].device)
+        return self._descs[k]
 
     def call(self, i, x, y, alpha):
         from libortho_amd import _C_ops
@@ -317,27 +330,38 @@ def graph_time(torch, fn, steps):
     return graph_steps_time(torch, lambda i: fn(i), steps, min(steps, 50))
 
 
-def time_block(torch, M, steps):
+def time_block(torch, M, steps, grouped=False):
     """Config c5: the seven projections of one Llama-2-7B block (q, k, v, o,
     gate, up, down; group-128, ortho 2 %, alpha = 1) back to back per step,
     each with its cached plan, weights rotated over enough block copies to
-    exceed the Infinity Cache.  Returns ms per block."""
-    from libortho_amd import workloads as W
+    exceed the Infinity Cache; with ``grouped``, q/k/v and gate/up each as
+    one orth_layers_forward_hip call (one launch at decode sizes).  Returns
+    ms per block, algorithmic bytes and flops, and the kernels of the last
+    step."""
+    from libortho_amd import _C_ops, workloads as W
     layers = W.llama_block()
     per = sum(W.algorithmic_bytes(l, 0, 1.0) for l in layers)
     copies = max(4, -(-ROTATE_MIN_BYTES // per))
     rots = [Rotation(l, torch, min_copies=copies, min_bytes=0, plan=True) for l in layers]
     xs = {K: torch.from_numpy(W.make_x(M, K, 7100 + K)).cuda() for K in {l.K for l in layers}}
     ys = [torch.empty(M, l.N, dtype=torch.float16, device="cuda") for l in layers]
+    groups = [[0, 1, 2], [3], [4, 5], [6]] if grouped else [[j] for j in range(len(layers))]
+    kernels = []
 
     def fn(i):
-        for j, l in enumerate(layers):
-            rots[j].call(i, xs[l.K], ys[j], 1.0)
+        kernels.clear()
+        for g in groups:
+            if len(g) == 1:
+                rots[g[0]].call(i, xs[layers[g[0]].K], ys[g[0]], 1.0)
+            else:
+                _C_ops.forward_group([rots[j].desc(i, 1.0) for j in g], xs[layers[g[0]].K], [ys[j] for j in g],
+                                     [rots[j].plans[i % rots[j].n] for j in g])
+            kernels.append(_C_ops.last_kernel())
     fn(0)
     torch.cuda.synchronize()
     assert all(torch.isfinite(y).all().item() for y in ys), "non-finite output"
     return graph_time(torch, fn, steps), sum(W.algorithmic_bytes(l, M, 1.0) for l in layers), \
-        sum(W.algorithmic_flops(l, M, 1.0) for l in layers)
+        sum(W.algorithmic_flops(l, M, 1.0) for l in layers), list(kernels)
 
 
 def time_dropin(torch, layer, M, alpha, calls, graph_steps=0):
@@ -701,14 +725,16 @@ def main():
                               "frac_hbm": round(b / (rr["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
             log(f"  {secondary[-1]}")
         for m in (1, 32):
-            # 7 launches per step: a shorter graph (the capture holds them all)
-            ms, b, f = time_block(torch, m, max(20, min(args.steps, 300)))
-            secondary.append({"workload": f"c5 Llama-2-7B block (7 projections) M={m}", "kernel": "per projection",
-                              "us_per_step": round(ms * 1e3, 3),
-                              "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
-                              "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                              "TFLOP/s": round(f / (ms * 1e-3) / 1e12, 2)})
-            log(f"  {secondary[-1]}")
+            for grouped in (False, True):
+                # 7 launches per step: a shorter graph (the capture holds them all)
+                ms, b, f, ks = time_block(torch, m, max(20, min(args.steps, 300)), grouped)
+                secondary.append({"workload": f"c5 Llama-2-7B block (7 projections) M={m}"
+                                  + (", q/k/v and gate/up grouped" if grouped else ""),
+                                  "kernel": "+".join(ks), "us_per_step": round(ms * 1e3, 3),
+                                  "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                                  "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "TFLOP/s": round(f / (ms * 1e-3) / 1e12, 2)})
+                log(f"  {secondary[-1]}")
         r1 = time_dropin(torch, layer, 1, 1.0, 300, graph_steps=max(20, min(args.steps, 2000)))
         b = W.algorithmic_bytes(layer, 1, 1.0)
         r1.update({"workload": "reference 8-argument _C_ops.forward, c2 M=1 alpha=1 (no plan: CSR read)",

@@ -151,6 +151,25 @@ int orth_layer_forward_hip_noalloc(const orth_hip_layer_t *layer, const void *pl
 /* ORTH_NOALLOC_SCRATCH_BYTES, for bindings that cannot read the macro. */
 int64_t orth_noalloc_scratch_bytes(void);
 
+/* Forward of `count` (1..ORTH_GROUP_MAX) layers that read the same input,
+ * outputs[l] = layers[l](input) as orth_layer_forward_hip_ex computes it
+ * (plans, plan_bytes, biases and bias_dtypes: arrays of `count` entries, or
+ * NULL for none; a NULL entry is no plan / no bias).  When every layer takes
+ * the decode kernel with the same instantiation (the same in_features,
+ * scale layout, ortho mode and plan record size) the layers share one
+ * launch, each layer's output rows dealt to their own workgroups
+ * (orth_hip_last_kernel() then returns 5); otherwise each layer is its own
+ * forward call.  Outputs must not overlap.  No counterpart in the
+ * reference, which calls its forward once per projection
+ * (OrthoLinear.forward, /root/reference/torch_bind/ortho_linear.py:130-168, per module): for the
+ * projections of one block that read one activation (q/k/v, gate/up) it
+ * saves the launch gaps between them. */
+#define ORTH_GROUP_MAX 4
+int orth_layers_forward_hip(const orth_hip_layer_t *const *layers, const void *const *plans,
+                            const int64_t *plan_bytes, const void *const *biases, const int32_t *bias_dtypes,
+                            int32_t count, const void *input, void *const *outputs, int64_t batch_size,
+                            int32_t io_dtype, void *stream);
+
 /* Size in bytes of the ortho plan for this layer (0 when count == 0), or a
  * negative orth_status_t on invalid arguments. */
 int64_t orth_ortho_plan_bytes(const orth_hip_layer_t *layer);
@@ -278,7 +297,8 @@ int orth_hip_set_kernel_policy(int policy);
 int orth_hip_get_kernel_policy(void);
 
 /* The kernel the calling thread's last successful forward launched:
- * 1 decode, 2 prefill, 3 general, 4 mid-batch, 0 none. */
+ * 1 decode, 2 prefill, 3 general, 4 mid-batch, 5 decode for a group of
+ * layers in one launch (orth_layers_forward_hip), 0 none. */
 int orth_hip_last_kernel(void);
 
 /* Message of the calling thread's last failure ("" if none). */

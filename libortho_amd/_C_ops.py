@@ -37,8 +37,9 @@ from . import _lib
 _DT = {torch.float16: _lib.DT_F16, torch.bfloat16: _lib.DT_BF16, torch.float32: _lib.DT_F32}
 
 # the operator boundary as the reference names it, plus this build's extensions;
-# forward_layer and make_layer (descriptor reuse for OrthoLinear) stay internal
-__all__ = ["forward", "forward_planned", "build_plan", "dequant", "pack_base", "pack_csr", "sieve_quantize",
+# forward_layer and make_layer (descriptor reuse for OrthoLinear) stay internal;
+# forward_group takes make_layer descriptors (OrthoLinear.forward_group wraps it)
+__all__ = ["forward", "forward_planned", "forward_group", "build_plan", "dequant", "pack_base", "pack_csr", "sieve_quantize",
            "sieve_split", "sieve_hdiag", "last_kernel", "set_kernel_policy", "get_kernel_policy", "device_info"]
 
 
@@ -189,6 +190,52 @@ def forward_layer(layer, input, output, plan=None, bias=None) -> None:
                                            _ptr(bias) if bias is not None else None,
                                            _DT[bias.dtype] if bias is not None else 0, _ptr(input),
                                            _ptr(output), int(input.shape[0]), _DT[input.dtype], stream)
+    if dev.index == torch.cuda.current_device():
+        rc = call()
+    else:
+        with torch.cuda.device(dev):
+            rc = call()
+    _lib.check(rc)
+
+
+def forward_group(layers, input, outputs, plans=None, biases=None) -> None:
+    """Several layers over one input, ``outputs[l] = layers[l](input)``, in a
+    single decode launch when the layers allow it (same in_features, scale
+    layout, ortho mode; decode-sized batches), else one launch per layer.
+    ``layers``: descriptors from :func:`make_layer`, as for
+    :func:`forward_layer`; ``plans`` / ``biases``: lists of the same length
+    with None entries for none."""
+    n = len(layers)
+    _req(1 <= n <= _lib.GROUP_MAX, f"a group holds 1..{_lib.GROUP_MAX} layers, got {n}")
+    _req(len(outputs) == n, f"{len(outputs)} outputs for {n} layers")
+    plans = list(plans) if plans is not None else [None] * n
+    biases = list(biases) if biases is not None else [None] * n
+    _req(len(plans) == n and len(biases) == n, "plans and biases must have one entry per layer")
+    dev = input.device
+    for layer, out, plan, bias in zip(layers, outputs, plans, biases):
+        _check_io(input, out)
+        _req(int(input.shape[1]) == layer.base.in_features,
+             f"input has {input.shape[1]} columns, a layer {layer.base.in_features} in_features")
+        _req(int(out.shape[1]) == layer.base.out_features,
+             f"an output has {out.shape[1]} columns, its layer {layer.base.out_features} out_features")
+        if plan is not None and plan.numel() > 0:
+            _req(plan.device == dev and plan.dtype == torch.uint8, "plan must be a uint8 tensor on input's device")
+        if bias is not None:
+            _req(bias.device == dev and bias.dtype in _DT and bias.numel() == out.shape[1] and bias.is_contiguous(),
+                 "bias must be a contiguous float tensor of out_features elements on input's device")
+    has = [p is not None and p.numel() > 0 for p in plans]
+    c_layers = (ctypes.c_void_p * n)(*[ctypes.addressof(layer) for layer in layers])
+    c_plans = (ctypes.c_void_p * n)(*[p.data_ptr() if h else None for p, h in zip(plans, has)])
+    c_pbytes = (ctypes.c_int64 * n)(*[p.numel() if h else 0 for p, h in zip(plans, has)])
+    c_bias = (ctypes.c_void_p * n)(*[b.data_ptr() if b is not None else None for b in biases])
+    c_bdt = (ctypes.c_int32 * n)(*[_DT[b.dtype] if b is not None else 0 for b in biases])
+    c_out = (ctypes.c_void_p * n)(*[o.data_ptr() if o.numel() > 0 else None for o in outputs])
+    L = _lib.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def call():
+        return L.orth_layers_forward_hip(c_layers, c_plans, c_pbytes, c_bias, c_bdt, n, _ptr(input), c_out,
+                                         int(input.shape[0]), _DT[input.dtype], stream)
     if dev.index == torch.cuda.current_device():
         rc = call()
     else:
@@ -369,7 +416,8 @@ def sieve_hdiag(inputs: torch.Tensor) -> torch.Tensor:
 
 def last_kernel() -> str:
     """Kernel used by this thread's last forward: decode, skinny (5..64
-    tokens), prefill or general."""
+    tokens), prefill, general, or decode_group (one decode launch for the
+    layers of a :func:`forward_group` call)."""
     return _lib.last_kernel()
 
 

@@ -21,7 +21,8 @@ STATUS_NAMES = {OK: "ORTH_OK", ERR_INVALID_ARGUMENT: "ORTH_ERR_INVALID_ARGUMENT"
                 ERR_UNSUPPORTED: "ORTH_ERR_UNSUPPORTED", ERR_HIP: "ORTH_ERR_HIP",
                 ERR_NO_DEVICE: "ORTH_ERR_NO_DEVICE"}
 # kernel ids (orth_hip_last_kernel) and policies (orth_hip_set_kernel_policy)
-KERNEL_NAMES = {0: "none", 1: "decode", 2: "prefill", 3: "general", 4: "skinny"}
+KERNEL_NAMES = {0: "none", 1: "decode", 2: "prefill", 3: "general", 4: "skinny", 5: "decode_group"}
+GROUP_MAX = 4
 POLICIES = {"auto": 0, "decode": 1, "prefill": 2, "general": 3, "skinny": 4}
 
 
@@ -61,6 +62,7 @@ SIGNATURES = {
     "orth_layer_forward_hip_ex": (ctypes.c_int, [_LP, _P, _I64, _P, _I32, _P, _P, _I64, _I32, _P]),
     "orth_layer_forward_hip_noalloc": (ctypes.c_int, [_LP, _P, _I64, _P, _I32, _P, _P, _I64, _I32, _P]),
     "orth_noalloc_scratch_bytes": (_I64, []),
+    "orth_layers_forward_hip": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _P, _P, _I64, _I32, _P]),
     "orth_ortho_plan_bytes": (_I64, [_LP]),
     "orth_ortho_plan_build": (ctypes.c_int, [_LP, _P, _I64, _P]),
     "orth_base_dequant_hip": (ctypes.c_int, [_LP, _P, _P]),

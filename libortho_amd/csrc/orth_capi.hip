@@ -34,6 +34,8 @@ hipError_t launch_csr_fill(const void *w, int wdt, int64_t N, int64_t K, const i
                            const void *mask, int32_t *col, void *vals, int vdt, hipStream_t stream);
 bool decode_supported(const ForwardArgs &a);
 hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream);
+bool decode_group_ok(const ForwardArgs *as, const void *const *plans, int n);
+hipError_t launch_decode_group(const ForwardArgs *as, const void *const *plans, int n, int cus, hipStream_t stream);
 bool prefill_supported(const ForwardArgs &a);
 bool plan_supported(const ForwardArgs &a);
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz);
@@ -90,6 +92,7 @@ int fail_hip(hipError_t e, const char *what) {
 }
 
 bool valid_dtype(int32_t d) { return d == ORTH_DT_F16 || d == ORTH_DT_BF16 || d == ORTH_DT_F32; }
+int64_t dtype_size(int32_t d) { return d == ORTH_DT_F32 ? 4 : 2; }
 
 // Validates a layer (and, when check_io, the activations) and fills args.
 int resolve(const orth_hip_layer_t *L, const void *input, void *output, int64_t batch,
@@ -271,6 +274,41 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part,
     return ORTH_OK;
 }
 
+// The kernel a forward call takes under `policy` (orth_hip_set_kernel_policy).
+int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel) {
+    const bool dec_ok = decode_supported(a);
+    const bool pre_ok = prefill_supported(a);
+    // the mid-batch kernel reads each row's ortho entries through the plan;
+    // without one it filters whole rows by column, which still beats the
+    // decode kernel from 9 tokens (c2: 26.5 against 29.2 us at 12 tokens,
+    // 26.7 against 33.9 at 16) but not up to 8 (21.7 against 19.3-21.0)
+    const bool sk_ok = skinny_supported(a);
+    const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok || a.M > 8);
+    switch (policy) {
+        case 1:
+            if (!dec_ok) return fail(ORTH_ERR_UNSUPPORTED, "decode kernel forced but it cannot take this call");
+            *kernel = KERNEL_DECODE;
+            break;
+        case 2:
+            if (!pre_ok) return fail(ORTH_ERR_UNSUPPORTED, "prefill kernel forced but it cannot take this call");
+            *kernel = KERNEL_PREFILL;
+            break;
+        case 3:
+            *kernel = KERNEL_GENERAL;
+            break;
+        case 4:
+            if (!sk_ok) return fail(ORTH_ERR_UNSUPPORTED, "mid-batch kernel forced but it cannot take this call");
+            *kernel = KERNEL_SKINNY;
+            break;
+        default:
+            if (dec_ok && a.M <= 4) *kernel = KERNEL_DECODE;
+            else if (sk_pref) *kernel = KERNEL_SKINNY;
+            else if (dec_ok) *kernel = KERNEL_DECODE;
+            else *kernel = pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL;
+    }
+    return ORTH_OK;
+}
+
 // noalloc: scratch from the device's scratch array instead of the stream's
 // workspace or stream-ordered allocations (orth_layer_forward_hip_noalloc).
 int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
@@ -295,38 +333,9 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
     if (rc != ORTH_OK) return rc;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
 
-    const int policy = g_policy.load(std::memory_order_relaxed);
-    const bool dec_ok = decode_supported(a);
-    const bool pre_ok = prefill_supported(a);
-    // the mid-batch kernel reads each row's ortho entries through the plan;
-    // without one it filters whole rows by column, which still beats the
-    // decode kernel from 9 tokens (c2: 26.5 against 29.2 us at 12 tokens,
-    // 26.7 against 33.9 at 16) but not up to 8 (21.7 against 19.3-21.0)
-    const bool sk_ok = skinny_supported(a);
-    const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok || a.M > 8);
-    int kernel;
-    switch (policy) {
-        case 1:
-            if (!dec_ok) return fail(ORTH_ERR_UNSUPPORTED, "decode kernel forced but it cannot take this call");
-            kernel = KERNEL_DECODE;
-            break;
-        case 2:
-            if (!pre_ok) return fail(ORTH_ERR_UNSUPPORTED, "prefill kernel forced but it cannot take this call");
-            kernel = KERNEL_PREFILL;
-            break;
-        case 3:
-            kernel = KERNEL_GENERAL;
-            break;
-        case 4:
-            if (!sk_ok) return fail(ORTH_ERR_UNSUPPORTED, "mid-batch kernel forced but it cannot take this call");
-            kernel = KERNEL_SKINNY;
-            break;
-        default:
-            if (dec_ok && a.M <= 4) kernel = KERNEL_DECODE;
-            else if (sk_pref) kernel = KERNEL_SKINNY;
-            else if (dec_ok) kernel = KERNEL_DECODE;
-            else kernel = pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL;
-    }
+    int kernel = KERNEL_NONE;
+    rc = pick_kernel(a, plan, g_policy.load(std::memory_order_relaxed), &kernel);
+    if (rc != ORTH_OK) return rc;
 
     hipError_t e = hipSuccess;
     if (kernel == KERNEL_DECODE) {
@@ -386,6 +395,68 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
     return ORTH_OK;
 }
 
+// Layers that read one input: a single decode launch when every layer takes
+// the decode kernel and they share its instantiation (decode_group_ok),
+// else one forward_impl call per layer.
+int group_forward_impl(const orth_hip_layer_t *const *layers, const void *const *plans, const int64_t *plan_bytes,
+                       const void *const *biases, const int32_t *bias_dtypes, int32_t count, const void *input,
+                       void *const *outputs, int64_t batch, int32_t io_dtype, void *stream_v) {
+    if (count < 1 || count > ORTH_GROUP_MAX)
+        return fail(ORTH_ERR_INVALID_ARGUMENT, "count %d is outside 1..%d", (int)count, (int)ORTH_GROUP_MAX);
+    if (!layers || !outputs) return fail(ORTH_ERR_INVALID_ARGUMENT, "layers and outputs must not be NULL");
+    ForwardArgs as[ORTH_GROUP_MAX];
+    const void *pl[ORTH_GROUP_MAX];
+    for (int l = 0; l < count; l++) {
+        int rc = resolve(layers[l], input, outputs[l], batch, io_dtype, true, as[l]);
+        if (rc != ORTH_OK) return rc;
+        const void *bias = biases ? biases[l] : nullptr;
+        const int32_t bdt = bias_dtypes ? bias_dtypes[l] : ORTH_DT_F32;
+        if (bias && !valid_dtype(bdt))
+            return fail(ORTH_ERR_INVALID_ARGUMENT, "bias %d dtype %d is not F16, BF16 or F32", l, (int)bdt);
+        as[l].bias = bias;
+        as[l].bias_dtype = bdt;
+        pl[l] = plans ? plans[l] : nullptr;
+        if (pl[l] && (!plan_bytes || plan_bytes[l] < plan_bytes_for(as[l].N, as[l].K, as[l].nnz)))
+            return fail(ORTH_ERR_INVALID_ARGUMENT, "plan %d is smaller than the plan size %lld", l,
+                        (long long)plan_bytes_for(as[l].N, as[l].K, as[l].nnz));
+        // outputs written by one launch must not overlap each other
+        const int64_t esz = dtype_size(io_dtype);
+        const char *b0 = static_cast<const char *>(outputs[l]);
+        for (int j = 0; j < l; j++) {
+            const char *b1 = static_cast<const char *>(outputs[j]);
+            if (batch > 0 && b0 < b1 + batch * as[j].N * esz && b1 < b0 + batch * as[l].N * esz)
+                return fail(ORTH_ERR_INVALID_ARGUMENT, "outputs %d and %d overlap", j, l);
+        }
+    }
+    if (batch == 0) {
+        t_last_kernel = KERNEL_NONE;
+        return ORTH_OK;
+    }
+    int dev = 0;
+    int rc = current_device_ok(&dev);
+    if (rc != ORTH_OK) return rc;
+    bool grouped = count > 1;
+    const int policy = g_policy.load(std::memory_order_relaxed);
+    for (int l = 0; l < count && grouped; l++) {
+        int kernel = KERNEL_NONE;
+        rc = pick_kernel(as[l], pl[l], policy, &kernel);
+        if (rc != ORTH_OK) return rc;
+        grouped = kernel == KERNEL_DECODE;
+    }
+    if (grouped && decode_group_ok(as, pl, count)) {
+        hipError_t e = launch_decode_group(as, pl, count, g_dev[dev].cus, static_cast<hipStream_t>(stream_v));
+        if (e != hipSuccess) return fail_hip(e, "kernel launch");
+        t_last_kernel = KERNEL_DECODE_GROUP;
+        return ORTH_OK;
+    }
+    for (int l = 0; l < count; l++) {
+        rc = forward_impl(layers[l], pl[l], pl[l] ? plan_bytes[l] : 0, input, outputs[l], batch, io_dtype, stream_v,
+                          as[l].bias, as[l].bias_dtype);
+        if (rc != ORTH_OK) return rc;
+    }
+    return ORTH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -426,6 +497,14 @@ int orth_layer_forward_hip_noalloc(const orth_hip_layer_t *layer, const void *pl
 }
 
 int64_t orth_noalloc_scratch_bytes(void) { return (int64_t)ORTH_NOALLOC_SCRATCH_BYTES; }
+
+int orth_layers_forward_hip(const orth_hip_layer_t *const *layers, const void *const *plans,
+                            const int64_t *plan_bytes, const void *const *biases, const int32_t *bias_dtypes,
+                            int32_t count, const void *input, void *const *outputs, int64_t batch_size,
+                            int32_t io_dtype, void *stream) {
+    return group_forward_impl(layers, plans, plan_bytes, biases, bias_dtypes, count, input, outputs, batch_size,
+                              io_dtype, stream);
+}
 
 int64_t orth_ortho_plan_bytes(const orth_hip_layer_t *layer) {
     ForwardArgs a;
@@ -662,6 +741,6 @@ int orth_hip_last_kernel(void) { return t_last_kernel; }
 
 const char *orth_hip_last_error(void) { return t_error.c_str(); }
 
-int orth_hip_abi_version(void) { return 101; }
+int orth_hip_abi_version(void) { return 102; }
 
 }  // extern "C"

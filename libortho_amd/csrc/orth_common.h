@@ -22,7 +22,14 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Which kernel served a forward call (orth_hip_last_kernel()).
-enum KernelId { KERNEL_NONE = 0, KERNEL_DECODE = 1, KERNEL_PREFILL = 2, KERNEL_GENERAL = 3, KERNEL_SKINNY = 4 };
+enum KernelId {
+    KERNEL_NONE = 0,
+    KERNEL_DECODE = 1,
+    KERNEL_PREFILL = 2,
+    KERNEL_GENERAL = 3,
+    KERNEL_SKINNY = 4,
+    KERNEL_DECODE_GROUP = 5  // one decode launch for several layers
+};
 
 // Everything a forward launch needs, resolved on the host.
 struct ForwardArgs {
@@ -185,30 +192,6 @@ __device__ __forceinline__ u32x4 permute_x8(u32x4 d) {
 
 // Position of element r (0..7) of an 8-chunk in the interleaved order.
 __device__ __forceinline__ int interleaved_pos(int r) { return ((r & 3) << 1) | (r >> 2); }
-
-// "Natural" order: four f16x2 words holding k-pairs (0,1) (2,3) (4,5) (6,7),
-// each weight multiplied by the fp16 scale s (one rounding of the exact
-// product q*s).  Used where the activation tile is copied untouched.
-// Each 16-bit half of the packed word is duplicated into both halves of a
-// word (v_perm), then a per-half shift (v_pk_lshrrev_b16) moves nibble j
-// into bits 0..3 of the low half and nibble j+1 into bits 0..3 of the high.
-typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ void int4x8_to_f16_scaled(uint32_t w, f16x2 s2, uint32_t out[4]) {
-    const uint32_t wf = w ^ 0x88888888u;
-    const u16x2 lo = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(wf, wf, 0x01000100u));
-    const u16x2 hi = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(wf, wf, 0x03020302u));
-    const u16x2 sh01 = {0, 4}, sh23 = {8, 12};
-    const uint32_t p0 = (__builtin_bit_cast(uint32_t, lo >> sh01) & 0x000F000Fu) | 0x64006400u;
-    const uint32_t p1 = (__builtin_bit_cast(uint32_t, lo >> sh23) & 0x000F000Fu) | 0x64006400u;
-    const uint32_t p2 = (__builtin_bit_cast(uint32_t, hi >> sh01) & 0x000F000Fu) | 0x64006400u;
-    const uint32_t p3 = (__builtin_bit_cast(uint32_t, hi >> sh23) & 0x000F000Fu) | 0x64006400u;
-    const f16x2 bias = {(f16)-1032.0f, (f16)-1032.0f};
-    out[0] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p0) + bias) * s2);
-    out[1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p1) + bias) * s2);
-    out[2] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p2) + bias) * s2);
-    out[3] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p3) + bias) * s2);
-}
 
 // ------------------------------------------------------------ reductions
 

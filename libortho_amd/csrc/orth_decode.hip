@@ -54,6 +54,25 @@ constexpr int kDecodeNT = 64 * kDecodeW;
 constexpr int kDecodeESlots = 2;  // CSR entries staged per thread: 4 * slots
 constexpr int kDecodeEStaged = kDecodeESlots * 4 * kDecodeNT;
 
+constexpr int kDecodeMaxGroup = 4;  // layers one decode launch may take
+
+// The per-layer part of a decode launch (weights, ortho, output).
+struct DecodeLayerArgs {
+    const uint8_t *q;
+    const f16 *scales;
+    const int32_t *row_ptr;
+    const int32_t *col;
+    const f16 *vals;
+    int32_t nnz;
+    int csr_vec;
+    f16 *y;
+    int64_t N;
+    float alpha;
+    const uint32_t *rec;
+    const void *bias;
+    int bias_dtype;
+};
+
 struct DecodeArgs {
     const uint8_t *q;
     const f16 *scales;
@@ -84,6 +103,13 @@ struct DecodeArgs {
     int deep;              // (host) fewer than two workgroups per CU: deeper weight prefetch
     const void *bias;      // [N] added after rounding (out_f16), or null
     int bias_dtype;
+    // A group launch: layers 1 .. nextra of the same shape class (K, scale
+    // layout, token count, ortho mode, record size) reading the same
+    // activations; layer 0 is the fields above.  Workgroups [blk0[l],
+    // blk0[l + 1]) take layer l.
+    int nextra;
+    DecodeLayerArgs extra[kDecodeMaxGroup - 1];
+    int blk0[kDecodeMaxGroup + 1];
 };
 
 // Weights pass through LDS (whole-line loads, transposed on the way) for
@@ -116,6 +142,33 @@ constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 // kernel behind its own weight stream.
 template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, int PD>
 __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
+    // a group launch: this workgroup's layer and its block within the layer.
+    // Constant indices only: an index computed at run time into the
+    // argument struct would move the whole struct to scratch memory.
+    static_assert(kDecodeMaxGroup == 4, "the layer pick below takes up to four layers");
+    int bid = blockIdx.x;
+    if (a.nextra > 0) {
+        const int b1 = a.blk0[1], b2 = a.blk0[2], b3 = a.blk0[3];
+        const int l = (bid >= b1 ? 1 : 0) + (a.nextra >= 2 && bid >= b2 ? 1 : 0) + (a.nextra >= 3 && bid >= b3 ? 1 : 0);
+        if (l > 0) {
+            bid -= l == 1 ? b1 : (l == 2 ? b2 : b3);
+#define ORTH_PICK(f) a.f = l == 1 ? a.extra[0].f : (l == 2 ? a.extra[1].f : a.extra[2].f)
+            ORTH_PICK(q);
+            ORTH_PICK(scales);
+            ORTH_PICK(row_ptr);
+            ORTH_PICK(col);
+            ORTH_PICK(vals);
+            ORTH_PICK(nnz);
+            ORTH_PICK(csr_vec);
+            ORTH_PICK(y);
+            ORTH_PICK(N);
+            ORTH_PICK(alpha);
+            ORTH_PICK(rec);
+            ORTH_PICK(bias);
+            ORTH_PICK(bias_dtype);
+#undef ORTH_PICK
+        }
+    }
     constexpr int W = kDecodeW;
     constexpr int NT = kDecodeNT;
     constexpr int RT = 16;
@@ -162,7 +215,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     const int lane = tid & 63;
     const int nl = lane & 15;  // B column (weight row) and A row (token) of this lane
     const int g = lane >> 4;   // which 32-k quarter of a chunk
-    const int64_t n0 = (int64_t)blockIdx.x * RT;
+    const int64_t n0 = (int64_t)bid * RT;
     const int K = a.K;
     const int c_lo = wave * a.cpw;
     const int nci = max(0, min(a.cpw, a.nchunks - c_lo));  // uniform
@@ -192,7 +245,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     //      the weights and returns with the activations
     u32x4 rv[ER];
     if (REC) {
-        const uint32_t *rb = a.rec + ((int64_t)blockIdx.x * 4 + wave) * a.qwords;
+        const uint32_t *rb = a.rec + ((int64_t)bid * 4 + wave) * a.qwords;
 #pragma unroll
         for (int r = 0; r < ER; r++)
             rv[r] = *reinterpret_cast<const u32x4 *>(rb + min(4 * (lane + 64 * r), a.qwords - 4));
@@ -370,7 +423,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 sacc[m] = __builtin_fmaf(ok_e ? vv : 0.f, ok_e ? xv : 0.f, sacc[m]);
             }
         };
-        const bool ok = (er[0] == plan_cell_tag(kCellQuarter, a.N, K, a.nnz, a.qwords, blockIdx.x, wave)) &
+        const bool ok = (er[0] == plan_cell_tag(kCellQuarter, a.N, K, a.nnz, a.qwords, bid, wave)) &
                         (er[1] == 0u);  // (uniform)
         if (ok) {
             const uint32_t h = er[2 + qr];
@@ -722,7 +775,7 @@ static hipError_t launch_decode_kp(const DecodeArgs &d, int64_t lds, hipStream_t
         if (e != hipSuccess) return e;
         allowed[dev].store(1, std::memory_order_release);
     }
-    const unsigned blocks = (unsigned)((d.N + 15) / 16);
+    const unsigned blocks = d.nextra > 0 ? (unsigned)d.blk0[d.nextra + 1] : (unsigned)((d.N + 15) / 16);
     hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD>), dim3(blocks), dim3(kDecodeNT),
                        (uint32_t)lds, stream, d);
     return hipGetLastError();
@@ -818,24 +871,55 @@ bool decode_supported(const ForwardArgs &a) {
 int plan_qrec_words(int64_t N, int64_t K, int64_t nnz);  // orth_prefill.hip
 int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz);
 
-// plan: an ortho plan of at least plan_bytes_for(N, K, nnz) bytes, or null;
-// cus: the device's compute units.
-hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream) {
-    DecodeArgs d;
-    d.deep = (a.N + 15) / 16 < 2 * (int64_t)cus;
-    d.q = a.q;
-    d.scales = static_cast<const f16 *>(a.scales);
-    d.ngroups = (int)a.ngroups;
-    d.row_ptr = a.row_ptr;
-    d.col = a.col;
-    d.vals = static_cast<const f16 *>(a.vals);
-    d.nnz = (int32_t)a.nnz;
-    d.csr_vec = a.nnz >= 4 && ((reinterpret_cast<uintptr_t>(a.col) & 15) == 0) &&
+// The per-layer fields of a decode launch for layer a (with its plan or null).
+static DecodeLayerArgs decode_layer_args(const ForwardArgs &a, const void *plan) {
+    DecodeLayerArgs e;
+    e.q = a.q;
+    e.scales = static_cast<const f16 *>(a.scales);
+    e.row_ptr = a.row_ptr;
+    e.col = a.col;
+    e.vals = static_cast<const f16 *>(a.vals);
+    e.nnz = (int32_t)a.nnz;
+    e.csr_vec = a.nnz >= 4 && ((reinterpret_cast<uintptr_t>(a.col) & 15) == 0) &&
                 ((reinterpret_cast<uintptr_t>(a.vals) & 7) == 0);
+    e.y = static_cast<f16 *>(a.y);
+    e.N = a.N;
+    e.alpha = a.alpha;
+    const bool rec = plan && a.has_ortho;
+    e.rec = rec ? reinterpret_cast<const uint32_t *>(static_cast<const char *>(plan) + plan_rec_at(a.N, a.K, a.nnz))
+                : nullptr;
+    e.bias = a.bias;
+    e.bias_dtype = a.bias_dtype;
+    return e;
+}
+
+// Everything that selects the kernel instantiation and its shared fields:
+// layers of one group launch must agree on all of it.
+struct DecodeClass {
+    int mt, gmode;
+    bool xlds;
+    int qwords, has_ortho, csr_vec;
+    int64_t M, K, ngroups;
+    bool operator==(const DecodeClass &o) const {
+        return mt == o.mt && gmode == o.gmode && xlds == o.xlds && qwords == o.qwords && has_ortho == o.has_ortho &&
+               csr_vec == o.csr_vec && M == o.M && K == o.K && ngroups == o.ngroups;
+    }
+};
+
+static DecodeClass decode_class(const ForwardArgs &a, const void *plan, DecodeArgs &d) {
+    const DecodeLayerArgs e = decode_layer_args(a, plan);
+    d.q = e.q;
+    d.scales = e.scales;
+    d.ngroups = (int)a.ngroups;
+    d.row_ptr = e.row_ptr;
+    d.col = e.col;
+    d.vals = e.vals;
+    d.nnz = e.nnz;
+    d.csr_vec = e.csr_vec;
     d.x = static_cast<const f16 *>(a.x);
-    d.y = static_cast<f16 *>(a.y);
-    d.bias = a.bias;
-    d.bias_dtype = a.bias_dtype;
+    d.y = e.y;
+    d.bias = e.bias;
+    d.bias_dtype = e.bias_dtype;
     d.M = (int)a.M;
     d.nchunks = (int)(a.K / 128);
     d.K = (int)a.K;
@@ -844,32 +928,85 @@ hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStr
     d.xstride = (int)(a.K + 8);  // +16 bytes: rows start in different LDS banks
     d.alpha = a.alpha;
     d.has_ortho = a.has_ortho;
-    const bool rec = plan && a.has_ortho;
-    d.rec = rec ? reinterpret_cast<const uint32_t *>(static_cast<const char *>(plan) + plan_rec_at(a.N, a.K, a.nnz))
-                : nullptr;
-    d.qwords = rec ? plan_qrec_words(a.N, a.K, a.nnz) : 0;
+    d.rec = e.rec;
+    d.qwords = e.rec ? plan_qrec_words(a.N, a.K, a.nnz) : 0;
+    d.nextra = 0;
 
-    int mt = 1;
-    while (mt < a.M) mt <<= 1;
+    DecodeClass c;
+    c.mt = 1;
+    while (c.mt < a.M) c.mt <<= 1;
     const bool grouped = a.ngroups != 1;
     d.gshift = 0;
     if (grouped)
         while ((128LL << d.gshift) < a.G) d.gshift++;
     d.scale_pairs = (a.ngroups % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.scales) & 3) == 0);
-    const bool xlds = decode_xlds(a.M, a.K);
+    c.xlds = decode_xlds(a.M, a.K);
     // 16-byte scale vectors: 8 chunks per vector, each wave's chunks start
     // on a vector boundary
     const bool scale_vec = d.gshift == 0 && a.ngroups % 8 == 0 && d.cpw % 8 == 0 &&
                            (reinterpret_cast<uintptr_t>(a.scales) & 15) == 0;
     // every wave takes exactly the chunk bound (8, 16 or 24 chunks)
     const bool full = d.nchunks == 4 * d.cpw && (d.cpw == 8 || d.cpw == 16 || d.cpw == 24);
-    const int gmode = !grouped ? (full ? 4 : 0)
-                               : (d.gshift != 0 ? 2 : (scale_vec && full ? 1 : (d.scale_pairs ? 3 : 2)));
-    if (gmode == 1) return xlds ? launch_decode_mt<1, true>(mt, d, stream) : launch_decode_mt<1, false>(mt, d, stream);
-    if (gmode == 3) return xlds ? launch_decode_mt<3, true>(mt, d, stream) : launch_decode_mt<3, false>(mt, d, stream);
-    if (gmode == 4) return xlds ? launch_decode_mt<4, true>(mt, d, stream) : launch_decode_mt<4, false>(mt, d, stream);
-    if (gmode == 2) return xlds ? launch_decode_mt<2, true>(mt, d, stream) : launch_decode_mt<2, false>(mt, d, stream);
-    return xlds ? launch_decode_mt<0, true>(mt, d, stream) : launch_decode_mt<0, false>(mt, d, stream);
+    c.gmode = !grouped ? (full ? 4 : 0) : (d.gshift != 0 ? 2 : (scale_vec && full ? 1 : (d.scale_pairs ? 3 : 2)));
+    c.qwords = d.qwords;
+    c.has_ortho = d.has_ortho;
+    c.csr_vec = d.csr_vec;
+    c.M = a.M;
+    c.K = a.K;
+    c.ngroups = a.ngroups;
+    return c;
+}
+
+static hipError_t decode_dispatch(const DecodeClass &c, const DecodeArgs &d, hipStream_t stream) {
+    const int mt = c.mt;
+    if (c.gmode == 1) return c.xlds ? launch_decode_mt<1, true>(mt, d, stream) : launch_decode_mt<1, false>(mt, d, stream);
+    if (c.gmode == 3) return c.xlds ? launch_decode_mt<3, true>(mt, d, stream) : launch_decode_mt<3, false>(mt, d, stream);
+    if (c.gmode == 4) return c.xlds ? launch_decode_mt<4, true>(mt, d, stream) : launch_decode_mt<4, false>(mt, d, stream);
+    if (c.gmode == 2) return c.xlds ? launch_decode_mt<2, true>(mt, d, stream) : launch_decode_mt<2, false>(mt, d, stream);
+    return c.xlds ? launch_decode_mt<0, true>(mt, d, stream) : launch_decode_mt<0, false>(mt, d, stream);
+}
+
+// plan: an ortho plan of at least plan_bytes_for(N, K, nnz) bytes, or null;
+// cus: the device's compute units.
+hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream) {
+    DecodeArgs d;
+    const DecodeClass c = decode_class(a, plan, d);
+    d.deep = (a.N + 15) / 16 < 2 * (int64_t)cus;
+    return decode_dispatch(c, d, stream);
+}
+
+// Whether layers as[0 .. n) (each decode_supported, the same activations)
+// can share one decode launch: at most kDecodeMaxGroup layers of one
+// instantiation class.
+bool decode_group_ok(const ForwardArgs *as, const void *const *plans, int n) {
+    if (n < 1 || n > kDecodeMaxGroup) return false;
+    DecodeArgs d;
+    const DecodeClass c0 = decode_class(as[0], plans ? plans[0] : nullptr, d);
+    for (int l = 1; l < n; l++) {
+        if (as[l].x != as[0].x) return false;
+        DecodeArgs dl;
+        if (!(decode_class(as[l], plans ? plans[l] : nullptr, dl) == c0)) return false;
+    }
+    int64_t blocks = 0;
+    for (int l = 0; l < n; l++) blocks += (as[l].N + 15) / 16;
+    return blocks <= INT32_MAX;
+}
+
+// One decode launch for the layers as[0 .. n) (decode_group_ok): workgroups
+// are dealt to the layers in order, each layer's blocks contiguous.
+hipError_t launch_decode_group(const ForwardArgs *as, const void *const *plans, int n, int cus, hipStream_t stream) {
+    DecodeArgs d;
+    const DecodeClass c = decode_class(as[0], plans ? plans[0] : nullptr, d);
+    d.nextra = n - 1;
+    int64_t blk = 0;
+    for (int l = 0; l < n; l++) {
+        d.blk0[l] = (int)blk;
+        blk += (as[l].N + 15) / 16;
+        if (l > 0) d.extra[l - 1] = decode_layer_args(as[l], plans ? plans[l] : nullptr);
+    }
+    for (int l = n; l <= kDecodeMaxGroup; l++) d.blk0[l] = (int)blk;
+    d.deep = blk < 2 * (int64_t)cus;
+    return decode_dispatch(c, d, stream);
 }
 
 }  // namespace orth

@@ -36,6 +36,7 @@ import torch
 import torch.nn as nn
 
 from .. import _C_ops as _C
+from .. import _lib
 from ..tools.sieve import pack_ortho_sparse
 
 HAS_C_OPS = True  # the reference's flag (:15-28); this package has no fallback
@@ -206,6 +207,40 @@ class OrthoLinear(nn.Module):
         if self.bias is not None and not fuse:
             output += self.bias
         return output.view(*original_shape[:-1], self.out_features)
+
+    @staticmethod
+    def forward_group(modules, x: torch.Tensor):
+        """``[m(x) for m in modules]`` for up to four OrthoLinear layers that
+        read the same input (a block's q/k/v or gate/up projections), with
+        the same results as the separate calls.  At decode batch sizes,
+        layers of the same in_features and weight layout share one kernel
+        launch; otherwise each runs its own.  No counterpart in the reference,
+        which calls each projection's forward in turn."""
+        modules = list(modules)
+        if not 1 <= len(modules) <= _lib.GROUP_MAX:
+            raise ValueError(f"forward_group takes 1..{_lib.GROUP_MAX} layers, got {len(modules)}")
+        if not x.is_cuda:
+            raise RuntimeError("OrthoLinear runs on a ROCm GPU only; move the modules and the input "
+                               "to a cuda device")
+        K = modules[0].in_features
+        if any(m.in_features != K for m in modules):
+            raise ValueError("the layers of a group must share in_features")
+        x_flat = x.reshape(-1, K).contiguous()
+        outs, plans, biases, late = [], [], [], []
+        for m in modules:
+            outs.append(torch.empty(x_flat.shape[0], m.out_features, device=x.device, dtype=x.dtype))
+            plans.append(m._ortho_plan() if m.alpha > 0 else None)
+            fuse = m.bias is not None and not (torch.is_grad_enabled() and m.bias.requires_grad) and \
+                m.bias.device == x.device
+            biases.append(m.bias.detach().contiguous() if fuse else None)
+            late.append(m.bias is not None and not fuse)
+        _C.forward_group([m._layer_desc(x.device) for m in modules], x_flat, outs, plans, biases)
+        res = []
+        for m, out, add in zip(modules, outs, late):
+            if add:
+                out += m.bias
+            res.append(out.view(*x.shape[:-1], m.out_features))
+        return res
 
     # ------------------------------------------------------------ checkpoints
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,

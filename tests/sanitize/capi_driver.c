@@ -21,7 +21,7 @@ static void expect(int got, int want, const char *what) {
     }
 }
 
-static char qbuf[4096], sbuf[4096], xbuf[4096], ybuf[4096];
+static char qbuf[4096], sbuf[4096], xbuf[4096], ybuf[4096], zbuf[4096];
 static int32_t rp[65], col[64];
 static unsigned short vals[64];
 
@@ -116,6 +116,24 @@ int main(void) {
     expect(orth_layer_forward_hip_noalloc(NULL, NULL, 0, NULL, 0, xbuf, ybuf, 2, ORTH_DT_F16, NULL),
            ORTH_ERR_INVALID_ARGUMENT, "noalloc NULL layer");
     if (orth_noalloc_scratch_bytes() != (int64_t)ORTH_NOALLOC_SCRATCH_BYTES) failures++;
+    /* grouped forward: count, NULL arrays, overlapping outputs, batch 0 */
+    {
+        const orth_hip_layer_t *ls[2] = {&L, &L};
+        void *outs[2] = {ybuf, ybuf};
+        expect(orth_layers_forward_hip(ls, NULL, NULL, NULL, NULL, 0, xbuf, outs, 2, ORTH_DT_F16, NULL),
+               ORTH_ERR_INVALID_ARGUMENT, "group count 0");
+        expect(orth_layers_forward_hip(ls, NULL, NULL, NULL, NULL, ORTH_GROUP_MAX + 1, xbuf, outs, 2, ORTH_DT_F16,
+                                       NULL), ORTH_ERR_INVALID_ARGUMENT, "group count above max");
+        expect(orth_layers_forward_hip(NULL, NULL, NULL, NULL, NULL, 2, xbuf, outs, 2, ORTH_DT_F16, NULL),
+               ORTH_ERR_INVALID_ARGUMENT, "group NULL layers");
+        expect(orth_layers_forward_hip(ls, NULL, NULL, NULL, NULL, 2, xbuf, outs, 2, ORTH_DT_F16, NULL),
+               ORTH_ERR_INVALID_ARGUMENT, "group overlapping outputs");
+        outs[1] = zbuf;
+        expect(orth_layers_forward_hip(ls, NULL, NULL, NULL, NULL, 2, xbuf, outs, 0, ORTH_DT_F16, NULL), ORTH_OK,
+               "group batch 0");
+        expect(orth_layers_forward_hip(ls, NULL, NULL, NULL, NULL, 2, xbuf, outs, 2, ORTH_DT_F16, NULL),
+               ORTH_ERR_NO_DEVICE, "group no device");
+    }
     expect(orth_base_dequant_hip(&L, NULL, NULL), ORTH_ERR_INVALID_ARGUMENT, "dequant NULL out");
     /* packing and sieve argument checks */
     expect(orth_pack_base_hip(NULL, ORTH_DT_F32, 4, 8, 8, NULL, 0, qbuf, sbuf, NULL), ORTH_ERR_INVALID_ARGUMENT,

@@ -20,6 +20,10 @@ hipError_t launch_csr_fill(const void *, int, int64_t, int64_t, const int32_t *,
                            hipStream_t) { return hipErrorInvalidValue; }
 bool decode_supported(const ForwardArgs &) { return false; }
 hipError_t launch_decode(const ForwardArgs &, const void *, int, hipStream_t) { return hipErrorInvalidValue; }
+bool decode_group_ok(const ForwardArgs *, const void *const *, int) { return false; }
+hipError_t launch_decode_group(const ForwardArgs *, const void *const *, int, int, hipStream_t) {
+    return hipErrorInvalidValue;
+}
 bool prefill_supported(const ForwardArgs &) { return false; }
 bool plan_supported(const ForwardArgs &a) { return a.K % 64 == 0 && a.K <= 12288; }
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) { return nnz > 0 ? 64 + 4 * nnz + N + K : 0; }
