@@ -202,7 +202,9 @@ def time_workload(torch, layer, M, alpha, steps, warmup, plan=False, steady=Fals
         with torch.cuda.stream(s):
             rot.call(0, x, y, alpha)
         torch.cuda.current_stream().wait_stream(s)
-        with torch.cuda.graph(g):
+        # captured on the warmed-up stream: a library workspace it owns is
+        # reused by the graph instead of stream-ordered allocations
+        with torch.cuda.graph(g, stream=s):
             for i in range(STEADY_STEPS):
                 rot.call(i, x, y, alpha)
         out["ms_per_step_steady"] = replay_timed(torch, g) / STEADY_STEPS

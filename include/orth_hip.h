@@ -290,15 +290,16 @@ typedef struct {
 int orth_hip_device_info(int device, orth_hip_device_info_t *info);
 
 /* Kernel choice override for benchmarking and tests: 0 = automatic (the
- * default), 1 = decode, 2 = prefill, 3 = general, 4 = mid-batch (5..64
- * tokens).  A forced kernel that cannot take a call returns
+ * default), 1 = decode, 2 = prefill, 3 = general, 4 = split-K mid-batch
+ * (5..64 tokens), 5 = one-launch mid-batch (5..16 tokens).  A forced kernel that cannot take a call returns
  * ORTH_ERR_UNSUPPORTED.  Process-wide. */
 int orth_hip_set_kernel_policy(int policy);
 int orth_hip_get_kernel_policy(void);
 
 /* The kernel the calling thread's last successful forward launched:
- * 1 decode, 2 prefill, 3 general, 4 mid-batch, 5 decode for a group of
- * layers in one launch (orth_layers_forward_hip), 0 none. */
+ * 1 decode, 2 prefill, 3 general, 4 split-K mid-batch, 5 decode for a
+ * group of layers in one launch (orth_layers_forward_hip), 6 one-launch
+ * mid-batch, 0 none. */
 int orth_hip_last_kernel(void);
 
 /* Message of the calling thread's last failure ("" if none). */

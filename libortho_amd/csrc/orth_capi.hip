@@ -46,6 +46,8 @@ hipError_t plan_read_flags(const void *plan, hipStream_t stream, uint32_t *flags
 hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream);
 hipError_t prefill_prepare_device();
 hipError_t plan_prepare_device();
+bool mid_supported(const ForwardArgs &a, const void *plan);
+hipError_t launch_mid(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream);
 bool skinny_supported(const ForwardArgs &a);
 int64_t skinny_workspace_bytes(const ForwardArgs &a, int cus);
 hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float *part, hipStream_t stream);
@@ -72,6 +74,7 @@ int policy_from_env() {
     if (!std::strcmp(e, "prefill")) return 2;
     if (!std::strcmp(e, "general")) return 3;
     if (!std::strcmp(e, "skinny")) return 4;
+    if (!std::strcmp(e, "mid")) return 5;
     return 0;
 }
 
@@ -284,6 +287,7 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
     // 26.7 against 33.9 at 16) but not up to 8 (21.7 against 19.3-21.0)
     const bool sk_ok = skinny_supported(a);
     const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok || a.M > 8);
+    const bool mid_ok = mid_supported(a, a.has_ortho ? plan : nullptr);
     switch (policy) {
         case 1:
             if (!dec_ok) return fail(ORTH_ERR_UNSUPPORTED, "decode kernel forced but it cannot take this call");
@@ -300,8 +304,16 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
             if (!sk_ok) return fail(ORTH_ERR_UNSUPPORTED, "mid-batch kernel forced but it cannot take this call");
             *kernel = KERNEL_SKINNY;
             break;
+        case 5:
+            if (!mid_ok) return fail(ORTH_ERR_UNSUPPORTED, "one-launch mid-batch kernel forced but it cannot take this call");
+            *kernel = KERNEL_MID;
+            break;
         default:
+            // the one-launch mid-batch kernel beats the split-K one on every
+            // shape both take (c2 M=8 alpha=1 10.3 against 14.4 us, M=16
+            // 13.6 against 16.6, 4096x4096 M=16 8.2 against 12.2)
             if (dec_ok && a.M <= 4) *kernel = KERNEL_DECODE;
+            else if (mid_ok) *kernel = KERNEL_MID;
             else if (sk_pref) *kernel = KERNEL_SKINNY;
             else if (dec_ok) *kernel = KERNEL_DECODE;
             else *kernel = pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL;
@@ -340,6 +352,8 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
     hipError_t e = hipSuccess;
     if (kernel == KERNEL_DECODE) {
         e = launch_decode(a, plan, g_dev[dev].cus, stream);
+    } else if (kernel == KERNEL_MID) {
+        e = launch_mid(a, a.has_ortho ? plan : nullptr, g_dev[dev].cus, stream);
     } else if (kernel == KERNEL_SKINNY) {
         const int cus = g_dev[dev].cus;
         const int64_t pbytes = skinny_workspace_bytes(a, cus);
@@ -730,7 +744,7 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info) {
 }
 
 int orth_hip_set_kernel_policy(int policy) {
-    if (policy < 0 || policy > 4) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..4");
+    if (policy < 0 || policy > 5) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..5");
     g_policy.store(policy);
     return ORTH_OK;
 }

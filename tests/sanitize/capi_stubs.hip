@@ -21,6 +21,8 @@ hipError_t launch_csr_fill(const void *, int, int64_t, int64_t, const int32_t *,
 bool decode_supported(const ForwardArgs &) { return false; }
 hipError_t launch_decode(const ForwardArgs &, const void *, int, hipStream_t) { return hipErrorInvalidValue; }
 bool decode_group_ok(const ForwardArgs *, const void *const *, int) { return false; }
+bool mid_supported(const ForwardArgs &, const void *) { return false; }
+hipError_t launch_mid(const ForwardArgs &, const void *, int, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_decode_group(const ForwardArgs *, const void *const *, int, int, hipStream_t) {
     return hipErrorInvalidValue;
 }

@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 CASES = [
     # K, N, group, M, policy, expected kernel (unplanned, planned)
     (4096, 1040, 128, 1, "auto", ("decode", "decode")), (4096, 1040, 128, 3, "auto", ("decode", "decode")),
-    (4096, 1040, 128, 8, "auto", ("decode", "skinny")), (4096, 1040, 128, 8, "skinny", ("skinny", "skinny")),
+    (4096, 1040, 128, 8, "auto", ("decode", "mid")), (4096, 1040, 128, 8, "skinny", ("skinny", "skinny")),
     (4096, 1040, 128, 40, "auto", ("skinny", "skinny")), (4096, 1040, 128, 300, "auto", ("prefill", "prefill")),
     (200, 96, 40, 5, "auto", ("general", "general")), (4096, 1040, None, 1, "auto", ("decode", "decode")),
 ]

@@ -88,12 +88,15 @@ def test_dequant_odd_groups_bit_exact(oracle_mod):
     assert np.array_equal(got.view(np.uint32), oracle_mod.dequant_f32(L.q, L.scales).view(np.uint32))
 
 
-def auto_kernel(M, planned=False):
+def auto_kernel(M, planned=False, K=4096):
     """Kernel the dispatcher picks for fp16 I/O on the fast-path shapes: the
-    mid-batch kernel reads the ortho plan, so without one (and with an ortho
-    term) batches up to 8 stay on the decode kernel."""
+    mid-batch kernels read the ortho plan, so without one (and with an ortho
+    term) batches up to 8 stay on the decode kernel; with one (or without an
+    ortho term) 5..16 tokens at K = 4096 take the one-launch kernel."""
     if M <= 4 or (M <= 8 and not planned):
         return "decode"
+    if planned and M <= 16 and K == 4096:
+        return "mid"
     return "skinny" if M <= 64 else "prefill"
 
 
@@ -124,12 +127,12 @@ def test_decode_c1_per_row_scales(oracle_mod, alpha):
     assert_close(y, oracle_y(oracle_mod, L, x, alpha), what=f"c1 alpha={alpha}")
 
 
-@pytest.mark.parametrize("policy", ["auto", "decode"])
+@pytest.mark.parametrize("policy", ["auto", "decode", "skinny"])
 def test_c4_skewed(oracle_mod, policy):
     L = W.config_layer("c4")
     x = W.make_x(8, L.K, 4001)
     y, k = run(L, x, 1.0, policy=policy, plan=True)
-    assert k == ("skinny" if policy == "auto" else "decode")
+    assert k == {"auto": "mid"}.get(policy, policy)
     assert_close(y, oracle_y(oracle_mod, L, x, 1.0), what=f"c4 {policy}")
 
 
@@ -298,7 +301,7 @@ def test_llama_block_c5(oracle_mod, M):
     for L in W.llama_block():
         x = W.make_x(M, L.K, 5100 + M)
         y, k = run(L, x, 1.0, plan=True)
-        assert k == auto_kernel(M, planned=True)
+        assert k == auto_kernel(M, planned=True, K=L.K)
         rows = np.arange(M) if M <= 8 else np.array([0, 7, 15, 16, 31])
         assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"c5 {L.name} M={M}")
 
@@ -421,7 +424,7 @@ def test_skinny_workspace_reuse_and_determinism(oracle_mod, c2):
     outs = {}
     for M in (8, 32, 8, 32):
         x = W.make_x(M, c2.K, 2700 + M)
-        y, k = run(c2, x, 1.0, plan=True)
+        y, k = run(c2, x, 1.0, policy="skinny", plan=True)
         assert k == "skinny"
         if M in outs:
             assert np.array_equal(y, outs[M])
@@ -437,7 +440,7 @@ def test_ragged_shapes(oracle_mod, M):
     L = W.make_layer(512, 1000, 128, 0.02, seed=70 + M)  # N not a multiple of 16 or 128
     x = W.make_x(M, L.K, 71 + M)
     y, k = run(L, x, 1.0)
-    assert k == auto_kernel(M)
+    assert k == auto_kernel(M, K=L.K)
     rows = np.unique(np.linspace(0, M - 1, min(M, 12)).astype(int))
     assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"ragged M={M}")
 
@@ -626,15 +629,16 @@ def test_plan_cache_follows_replaced_csr_buffers(oracle_mod):
 @pytest.mark.parametrize("M", [8, 32])
 def test_mid_batch_forward_captured_on_a_fresh_stream(c2, M):
     """A mid-batch forward captured in a HIP graph on a stream that never
-    ran it eagerly (its split-K workspace is allocated inside the graph),
-    replayed several times with eager forwards of other shapes between the
-    replays: every replay equals the eager result bit for bit."""
+    ran it eagerly (M = 8: the one-launch kernel; M = 32: the split-K kernel,
+    its workspace allocated inside the graph), replayed several times with
+    eager forwards of other shapes between the replays: every replay equals
+    the eager result bit for bit."""
     d = W.to_device(c2)
     plan = _C_ops.build_plan(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], c2.K)
     x = torch.from_numpy(W.make_x(M, c2.K, 2700 + M)).cuda()
     y_eager = torch.empty(M, c2.N, dtype=torch.float16, device="cuda")
     _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y_eager, 1.0, plan)
-    assert _C_ops.last_kernel() == "skinny"
+    assert _C_ops.last_kernel() == ("mid" if M <= 16 else "skinny")
     torch.cuda.synchronize()
     y = torch.empty_like(y_eager)
     g = torch.cuda.CUDAGraph()

@@ -55,6 +55,10 @@ def test_prefill_plan_in_scratch(gpu):
     compare(W.config_layer("c3"), (2048, 600), 1.0, "prefill", 8200)
 
 
+def test_one_launch_mid_batch_needs_no_scratch(gpu):
+    compare(W.config_layer("c2"), (16, 8), 0.0, "mid", 8400)
+
+
 def test_decode_needs_no_scratch(gpu):
     compare(W.config_layer("c2"), (2, 1), 1.0, "decode", 8300)
 
