@@ -102,10 +102,12 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  *   input   [batch_size, in_features] of io_dtype (F16, BF16 or F32), row-major
  *   output  [batch_size, out_features] of io_dtype, written in full
  * Picks, for FP16 I/O and the supported shapes, the decode kernel (batch <=
- * 4), the mid-batch kernel (5..64), the MFMA prefill kernel (above), and a
- * general kernel for shapes and dtypes the fast kernels do not take
- * (orth_hip_last_kernel() names the choice).  Kernels that need scratch
- * memory (the mid-batch split-K partials, a prefill plan when none is
+ * 4), the one-launch mid-batch kernel (5..16, K = 4096, a plan or no ortho
+ * term), the quarter-split kernel (17..32, the same conditions), the
+ * split-K mid-batch kernel (other batches up to 64), the MFMA prefill
+ * kernel (above), and a general kernel for shapes and dtypes the fast
+ * kernels do not take (orth_hip_last_kernel() names the choice).  Kernels
+ * that need scratch memory (split-K partials, a prefill plan when none is
  * given) take it from a per-stream workspace or stream-ordered allocations.
  * Replaces orth_layer_forward_cuda, /root/reference/include/ortho.h:141-144
  * (/root/reference/src/dual_gemm.cu:295-372), the body of the torch binding
@@ -291,7 +293,8 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info);
 
 /* Kernel choice override for benchmarking and tests: 0 = automatic (the
  * default), 1 = decode, 2 = prefill, 3 = general, 4 = split-K mid-batch
- * (5..64 tokens), 5 = one-launch mid-batch (5..16 tokens).  A forced kernel that cannot take a call returns
+ * (5..64 tokens), 5 = one-launch mid-batch (5..16 tokens), 6 = K quarters
+ * over the grid (17..32 tokens).  A forced kernel that cannot take a call returns
  * ORTH_ERR_UNSUPPORTED.  Process-wide. */
 int orth_hip_set_kernel_policy(int policy);
 int orth_hip_get_kernel_policy(void);
@@ -299,7 +302,7 @@ int orth_hip_get_kernel_policy(void);
 /* The kernel the calling thread's last successful forward launched:
  * 1 decode, 2 prefill, 3 general, 4 split-K mid-batch, 5 decode for a
  * group of layers in one launch (orth_layers_forward_hip), 6 one-launch
- * mid-batch, 0 none. */
+ * mid-batch, 7 K quarters over the grid, 0 none. */
 int orth_hip_last_kernel(void);
 
 /* Message of the calling thread's last failure ("" if none). */

@@ -47,6 +47,9 @@ hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t st
 hipError_t prefill_prepare_device();
 hipError_t plan_prepare_device();
 bool mid_supported(const ForwardArgs &a, const void *plan);
+bool quarter_supported(const ForwardArgs &a, const void *plan);
+int64_t quarter_workspace_bytes(const ForwardArgs &a);
+hipError_t launch_quarter(const ForwardArgs &a, const void *plan, float *part, hipStream_t stream);
 hipError_t launch_mid(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream);
 bool skinny_supported(const ForwardArgs &a);
 int64_t skinny_workspace_bytes(const ForwardArgs &a, int cus);
@@ -75,6 +78,7 @@ int policy_from_env() {
     if (!std::strcmp(e, "general")) return 3;
     if (!std::strcmp(e, "skinny")) return 4;
     if (!std::strcmp(e, "mid")) return 5;
+    if (!std::strcmp(e, "quarter")) return 6;
     return 0;
 }
 
@@ -288,6 +292,7 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
     const bool sk_ok = skinny_supported(a);
     const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok || a.M > 8);
     const bool mid_ok = mid_supported(a, a.has_ortho ? plan : nullptr);
+    const bool qu_ok = quarter_supported(a, a.has_ortho ? plan : nullptr);
     switch (policy) {
         case 1:
             if (!dec_ok) return fail(ORTH_ERR_UNSUPPORTED, "decode kernel forced but it cannot take this call");
@@ -308,12 +313,17 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
             if (!mid_ok) return fail(ORTH_ERR_UNSUPPORTED, "one-launch mid-batch kernel forced but it cannot take this call");
             *kernel = KERNEL_MID;
             break;
+        case 6:
+            if (!qu_ok) return fail(ORTH_ERR_UNSUPPORTED, "quarter-split kernel forced but it cannot take this call");
+            *kernel = KERNEL_QUARTER;
+            break;
         default:
             // the one-launch mid-batch kernel beats the split-K one on every
             // shape both take (c2 M=8 alpha=1 10.3 against 14.4 us, M=16
             // 13.6 against 16.6, 4096x4096 M=16 8.2 against 12.2)
             if (dec_ok && a.M <= 4) *kernel = KERNEL_DECODE;
             else if (mid_ok) *kernel = KERNEL_MID;
+            else if (qu_ok) *kernel = KERNEL_QUARTER;
             else if (sk_pref) *kernel = KERNEL_SKINNY;
             else if (dec_ok) *kernel = KERNEL_DECODE;
             else *kernel = pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL;
@@ -354,23 +364,26 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
         e = launch_decode(a, plan, g_dev[dev].cus, stream);
     } else if (kernel == KERNEL_MID) {
         e = launch_mid(a, a.has_ortho ? plan : nullptr, g_dev[dev].cus, stream);
-    } else if (kernel == KERNEL_SKINNY) {
+    } else if (kernel == KERNEL_SKINNY || kernel == KERNEL_QUARTER) {
         const int cus = g_dev[dev].cus;
-        const int64_t pbytes = skinny_workspace_bytes(a, cus);
+        const bool qk = kernel == KERNEL_QUARTER;
+        const int64_t pbytes = qk ? quarter_workspace_bytes(a) : skinny_workspace_bytes(a, cus);
         float *part = nullptr;
         bool temp = false;
         if (pbytes > 0 && noalloc) {
             if (pbytes > (int64_t)ORTH_NOALLOC_SCRATCH_BYTES)
                 return fail(ORTH_ERR_UNSUPPORTED,
-                            "the mid-batch kernel needs %lld bytes of scratch for this call; the no-allocation "
-                            "entry point has %lld", (long long)pbytes, (long long)ORTH_NOALLOC_SCRATCH_BYTES);
+                            "the %s kernel needs %lld bytes of scratch for this call; the no-allocation "
+                            "entry point has %lld", qk ? "quarter-split" : "mid-batch", (long long)pbytes,
+                            (long long)ORTH_NOALLOC_SCRATCH_BYTES);
             part = static_cast<float *>(g_dev[dev].scratch);
         } else if (pbytes > 0) {
             rc = workspace_for(dev, stream, pbytes, &part, &temp);
             if (rc != ORTH_OK) return rc;
         }
-        // without a plan the kernel filters each row's CSR by column
-        e = launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
+        // without a plan the split-K kernel filters each row's CSR by column
+        e = qk ? launch_quarter(a, a.has_ortho ? plan : nullptr, part, stream)
+               : launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
         if (temp) {
             hipError_t f = hipFreeAsync(part, stream);
             if (e == hipSuccess) e = f;
@@ -744,7 +757,7 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info) {
 }
 
 int orth_hip_set_kernel_policy(int policy) {
-    if (policy < 0 || policy > 5) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..5");
+    if (policy < 0 || policy > 6) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..6");
     g_policy.store(policy);
     return ORTH_OK;
 }

@@ -22,6 +22,9 @@ bool decode_supported(const ForwardArgs &) { return false; }
 hipError_t launch_decode(const ForwardArgs &, const void *, int, hipStream_t) { return hipErrorInvalidValue; }
 bool decode_group_ok(const ForwardArgs *, const void *const *, int) { return false; }
 bool mid_supported(const ForwardArgs &, const void *) { return false; }
+bool quarter_supported(const ForwardArgs &, const void *) { return false; }
+int64_t quarter_workspace_bytes(const ForwardArgs &) { return 0; }
+hipError_t launch_quarter(const ForwardArgs &, const void *, float *, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_mid(const ForwardArgs &, const void *, int, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_decode_group(const ForwardArgs *, const void *const *, int, int, hipStream_t) {
     return hipErrorInvalidValue;

@@ -62,7 +62,7 @@ def test_every_kernel_runs_without_scratch(tmp_path):
     notes = code_object_notes(tmp_path)
     ks = [k for n in notes for k in kernels(n)]
     names = " ".join(n for n, _ in ks)
-    for family in ("decode_kernel", "prefill_kernel", "skinny", "sieve", "plan"):
+    for family in ("decode_kernel", "prefill_kernel", "skinny", "mid_kernel", "quarter_kernel", "sieve", "plan"):
         assert family in names, f"no {family} kernels found in the code objects"
     spilled = [(n, p) for n, p in ks if p != 0]
     assert not spilled, f"kernels with a private segment: {spilled[:5]} ({len(spilled)} in all)"

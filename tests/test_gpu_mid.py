@@ -1,7 +1,8 @@
 """The one-launch mid-batch kernel (orth_mid.hip, 5..16 tokens, K = 4096)
-against the FP64 oracle, forced through the kernel policy: group-128 and
-per-row scales, alpha in {0, 0.5, 1}, ragged N (a partial last row block,
-fewer blocks than workgroups), the c2 and c4 shapes, records that overflow
+and the quarter-split kernel (orth_quarter.hip, 17..32 tokens) against the
+FP64 oracle, forced through the kernel policy: group-128 and per-row
+scales, alpha in {0, 0.5, 1}, ragged N (a partial last row block, fewer
+blocks than workgroups), the c2, c4 and c5 shapes, records that overflow
 (skewed rows read from the CSR), the fused bias; and against the split-K
 mid-batch kernel on the same inputs."""
 import numpy as np
@@ -98,3 +99,42 @@ def test_mid_refuses_what_it_cannot_take():
     lay = W.config_layer("c2")
     with pytest.raises(RuntimeError, match="mid-batch"):  # ortho term without a plan
         run(lay, W.make_x(8, lay.K, 1), 1.0, "mid", plan=False)
+
+
+@pytest.mark.parametrize("M", [17, 24, 32])
+@pytest.mark.parametrize("alpha", [1.0, 0.0, 0.5])
+def test_quarter_c2(oracle_mod, M, alpha):
+    lay = W.config_layer("c2")
+    x = W.make_x(M, lay.K, 4600 + M)
+    y, k = run(lay, x, alpha, "quarter")
+    assert k == "quarter"
+    rows = np.unique(np.linspace(0, M - 1, 9).astype(int))
+    check(oracle_mod, lay, x[rows], alpha, y[rows], f"quarter c2 M={M} alpha={alpha}")
+    y2, k2 = run(lay, x, alpha, "skinny")
+    assert k2 == "skinny"
+    assert float(np.abs(y - y2).max()) <= 2e-3 * float(np.abs(y2).max())
+
+
+@pytest.mark.parametrize("N,group,M,density", [(4096, 128, 32, 0.02), (11008, 128, 32, 0.02), (1000, 128, 19, 0.01),
+                                               (4096, None, 32, 0.01), (40, 128, 32, 0.01), (3000, 128, 25, 0.0)])
+def test_quarter_shapes(oracle_mod, N, group, M, density):
+    lay = W.make_layer(4096, N, group, density, 91 + N + M)
+    x = W.make_x(M, 4096, 92 + M)
+    y, k = run(lay, x, 1.0, "quarter")
+    assert k == "quarter"
+    check(oracle_mod, lay, x, 1.0, y, f"quarter N={N} G={group} M={M}")
+
+
+def test_quarter_skewed_records_and_bias(oracle_mod):
+    """c4's Zipf rows overflow some record cells (read from the CSR); the
+    bias is added by the reduction with the bits of the unfused add."""
+    lay = W.config_layer("c4")
+    x = W.make_x(32, lay.K, 4700)
+    y, k = run(lay, x, 1.0, "quarter")
+    assert k == "quarter"
+    rows = np.array([0, 5, 16, 31])
+    check(oracle_mod, lay, x[rows], 1.0, y[rows], "quarter c4")
+    b = (torch.randn(lay.N, generator=torch.Generator(device="cpu").manual_seed(3)) * 0.5).half().cuda()
+    yb, _ = run(lay, x, 1.0, "quarter", bias=b)
+    want = (torch.from_numpy(y).half().float() + b.float().cpu()).half().float().numpy()
+    assert np.array_equal(yb, want)

@@ -92,11 +92,14 @@ def auto_kernel(M, planned=False, K=4096):
     """Kernel the dispatcher picks for fp16 I/O on the fast-path shapes: the
     mid-batch kernels read the ortho plan, so without one (and with an ortho
     term) batches up to 8 stay on the decode kernel; with one (or without an
-    ortho term) 5..16 tokens at K = 4096 take the one-launch kernel."""
+    ortho term) 5..16 tokens at K = 4096 take the one-launch kernel and
+    17..32 the quarter-split one."""
     if M <= 4 or (M <= 8 and not planned):
         return "decode"
     if planned and M <= 16 and K == 4096:
         return "mid"
+    if planned and M <= 32 and K == 4096:
+        return "quarter"
     return "skinny" if M <= 64 else "prefill"
 
 
@@ -328,7 +331,7 @@ def test_skinny_c2_sweep(oracle_mod, c2, M, alpha, plan):
 def test_skinny_scale_modes_and_slicing(oracle_mod, K, N, G, M):
     L = W.make_layer(K, N, G, 0.01, seed=K + N + M)
     x = W.make_x(M, K, 2600 + M)
-    y, k = run(L, x, 1.0, plan=True)
+    y, k = run(L, x, 1.0, policy="skinny", plan=True)
     assert k == "skinny"
     rows = np.unique(np.linspace(0, M - 1, min(M, 6)).astype(int))
     assert_close(y[rows], oracle_y(oracle_mod, L, x[rows], 1.0), what=f"skinny K={K} N={N} G={G} M={M}")
@@ -629,8 +632,8 @@ def test_plan_cache_follows_replaced_csr_buffers(oracle_mod):
 @pytest.mark.parametrize("M", [8, 32])
 def test_mid_batch_forward_captured_on_a_fresh_stream(c2, M):
     """A mid-batch forward captured in a HIP graph on a stream that never
-    ran it eagerly (M = 8: the one-launch kernel; M = 32: the split-K kernel,
-    its workspace allocated inside the graph), replayed several times with
+    ran it eagerly (M = 8: the one-launch kernel; M = 32: the quarter-split
+    kernel, its workspace allocated inside the graph), replayed several times with
     eager forwards of other shapes between the replays: every replay equals
     the eager result bit for bit."""
     d = W.to_device(c2)
@@ -638,7 +641,7 @@ def test_mid_batch_forward_captured_on_a_fresh_stream(c2, M):
     x = torch.from_numpy(W.make_x(M, c2.K, 2700 + M)).cuda()
     y_eager = torch.empty(M, c2.N, dtype=torch.float16, device="cuda")
     _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y_eager, 1.0, plan)
-    assert _C_ops.last_kernel() == ("mid" if M <= 16 else "skinny")
+    assert _C_ops.last_kernel() == ("mid" if M <= 16 else "quarter")
     torch.cuda.synchronize()
     y = torch.empty_like(y_eager)
     g = torch.cuda.CUDAGraph()

@@ -59,6 +59,10 @@ def test_one_launch_mid_batch_needs_no_scratch(gpu):
     compare(W.config_layer("c2"), (16, 8), 0.0, "mid", 8400)
 
 
+def test_quarter_partials_in_scratch(gpu):
+    compare(W.config_layer("c2"), (32, 20), 0.0, "quarter", 8500)
+
+
 def test_decode_needs_no_scratch(gpu):
     compare(W.config_layer("c2"), (2, 1), 1.0, "decode", 8300)
 
