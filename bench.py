@@ -68,8 +68,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--profile", action="store_true",
-                    help="eager launches for rocprofv3 --pmc: decode c2 M=1 (alpha 1 and 0), "
-                         "prefill c3 M=2048, then a plain device copy of known size")
+                    help="eager launches for rocprofv3 --pmc: decode c2 M=1 (alpha 1 and 0), the mid-batch "
+                         "kernels at c2 M=8 and M=32, prefill c3 M=2048, then a plain device copy of known size")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="six eager planned prefill forwards at c3 (M=2048, alpha=1), for counter passes "
                          "of rocprofv3 --pmc over the prefill kernel alone")
@@ -230,6 +230,10 @@ class _Hip:
                            ("hipGraphInstantiate", [P(V), V, V, ctypes.c_char_p, ctypes.c_size_t]),
                            ("hipGraphLaunch", [V, V]), ("hipGraphExecDestroy", [V]), ("hipGraphDestroy", [V]),
                            ("hipStreamSynchronize", [V]),
+                           ("hipGraphGetNodes", [V, P(V), P(ctypes.c_size_t)]),
+                           ("hipGraphNodeGetDependentNodes", [V, P(V), P(ctypes.c_size_t)]),
+                           ("hipGraphNodeGetDependencies", [V, P(V), P(ctypes.c_size_t)]),
+                           ("hipGraphAddDependencies", [V, P(V), P(V), ctypes.c_size_t]),
                            ("hipEventElapsedTime", [P(ctypes.c_float), V, V])):
             fn = getattr(h, name)
             fn.argtypes = args
@@ -252,11 +256,13 @@ _HIP = None
 
 def graph_steps_time(torch, fn, steps, pre):
     """Milliseconds per call of fn(pre + i), i < steps, timed by HIP events
-    recorded inside one HIP graph: [pre untimed calls] -> event -> [the
-    `steps` calls] -> event.  The untimed calls put graph start-up and the
+    recorded inside one HIP graph: [pre untimed calls] -> [event -> the
+    `steps` calls -> event].  The untimed calls put graph start-up and the
     clock ramp before the first event; the events bracket exactly `steps`
-    calls.  The graph is built on a stream of its own (default priority)
-    from two captured segments, replayed once untimed, then once timed."""
+    calls, and sit inside the timed segment's own graph (its first and last
+    nodes), so the start of that segment is not timed either.  The graph is
+    built on a stream of its own (default priority) from two captured
+    segments, replayed once untimed, then once timed."""
     global _HIP
     if _HIP is None:
         _HIP = _Hip()
@@ -282,12 +288,27 @@ def graph_steps_time(torch, fn, steps, pre):
         gB = capture(pre, steps)
         e0, e1 = H.new("hipEventCreate"), H.new("hipEventCreate")
         events += [e0, e1]
+        # the timed segment's roots and leaves, then an event node before the
+        # roots and one after the leaves, inside the segment's graph
+        n = c.c_size_t(0)
+        H("hipGraphGetNodes", gB, None, c.byref(n))
+        nodes = (c.c_void_p * n.value)()
+        H("hipGraphGetNodes", gB, nodes, c.byref(n))
+
+        def count(api, node):
+            k = c.c_size_t(0)
+            H(api, node, None, c.byref(k))
+            return k.value
+        roots = [x for x in nodes if count("hipGraphNodeGetDependencies", x) == 0]
+        leaves = [x for x in nodes if count("hipGraphNodeGetDependentNodes", x) == 0]
+        n0 = H.new("hipGraphAddEventRecordNode", gB, None, 0, e0)
+        for r in roots:
+            H("hipGraphAddDependencies", gB, c.byref(n0), (c.c_void_p * 1)(r), 1)
+        H.new("hipGraphAddEventRecordNode", gB, (c.c_void_p * len(leaves))(*leaves), len(leaves), e1)
         G = H.new("hipGraphCreate", 0)
         graphs.append(G)
         nA = H.new("hipGraphAddChildGraphNode", G, None, 0, gA)
-        n0 = H.new("hipGraphAddEventRecordNode", G, (c.c_void_p * 1)(nA), 1, e0)
-        nB = H.new("hipGraphAddChildGraphNode", G, (c.c_void_p * 1)(n0), 1, gB)
-        H.new("hipGraphAddEventRecordNode", G, (c.c_void_p * 1)(nB), 1, e1)
+        H.new("hipGraphAddChildGraphNode", G, (c.c_void_p * 1)(nA), 1, gB)
         ex = H.new("hipGraphInstantiate", G, None, None, 0)
         execs.append(ex)
         H("hipGraphLaunch", ex, s)
@@ -383,6 +404,8 @@ def time_dropin(torch, layer, M, alpha, calls, graph_steps=0):
     for _ in range(5):
         C.forward(*args)
     torch.cuda.synchronize()
+    import gc
+    gc.collect()  # (see time_module)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     w0 = _t.perf_counter()
@@ -467,6 +490,7 @@ def time_module(torch, calls=300):
     checks, plan-cache lookup, launch) and the GPU time per call (HIP
     events around the same loop).  The layer is loaded from a
     reference-layout state_dict of the c2 buffers."""
+    import gc
     import time as _t
     from libortho_amd import OrthoLinear, workloads as W
     lay = W.config_layer("c2")
@@ -477,6 +501,9 @@ def time_module(torch, calls=300):
                        "ortho_row_ptr": torch.from_numpy(lay.row_ptr)})
     m = m.cuda()
     x = torch.from_numpy(W.make_x(1, lay.K, 77)).cuda()
+    # the earlier sections leave a large heap: collect it now, so that the
+    # loop measures the call path and not a full collection every few calls
+    gc.collect()
     with torch.no_grad():
         for _ in range(20):
             m(x)
@@ -498,15 +525,17 @@ def time_module(torch, calls=300):
 COPY_BYTES = 512 << 20  # calibration copy: reads and writes exactly this many bytes
 PROFILE_DECODE_STEPS = 100
 PROFILE_PREFILL_STEPS = 5
-PROFILE_SKINNY_STEPS = 100
-PROFILE_SKINNY_M = 8
+PROFILE_MID_STEPS = 100
+PROFILE_MID_M = 8       # the one-launch mid-batch kernel
+PROFILE_QUARTER_M = 32  # the quarter-split kernel and its reduction
 PROFILE_COPIES = 5
 
 
 def profile_run(torch):
     """Eager launches (no graph) so that rocprofv3 --pmc sees one dispatch
-    per forward: decode c2 M=1 alpha=1, decode c2 M=1 alpha=0, mid-batch c2
-    M=8 alpha=1 (planned; its kernel and the slice reduction), prefill c3
+    per forward: decode c2 M=1 alpha=1, decode c2 M=1 alpha=0, the
+    one-launch mid-batch kernel at c2 M=8 alpha=1 and the quarter-split
+    kernel (and its reduction) at c2 M=32 alpha=1 (planned), prefill c3
     M=2048 alpha=1 (planned), then PROFILE_COPIES device-to-device copies of
     COPY_BYTES (the calibration for FETCH_SIZE / WRITE_SIZE)."""
     from libortho_amd import workloads as W
@@ -520,11 +549,12 @@ def profile_run(torch):
         torch.cuda.synchronize()
         del rot
     rot = Rotation(c2, torch, plan=True)
-    x = torch.from_numpy(W.make_x(PROFILE_SKINNY_M, c2.K, 7008)).cuda()
-    y = torch.empty(PROFILE_SKINNY_M, c2.N, dtype=torch.float16, device="cuda")
-    for i in range(PROFILE_SKINNY_STEPS):
-        rot.call(i, x, y, 1.0)
-    torch.cuda.synchronize()
+    for m in (PROFILE_MID_M, PROFILE_QUARTER_M):
+        x = torch.from_numpy(W.make_x(m, c2.K, 7000 + m)).cuda()
+        y = torch.empty(m, c2.N, dtype=torch.float16, device="cuda")
+        for i in range(PROFILE_MID_STEPS):
+            rot.call(i, x, y, 1.0)
+        torch.cuda.synchronize()
     del rot
     c3 = W.config_layer("c3")
     rot = Rotation(c3, torch, min_copies=2, min_bytes=0, plan=True)
@@ -541,7 +571,7 @@ def profile_run(torch):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"profile": "done", "decode_steps": PROFILE_DECODE_STEPS,
-                      "skinny_steps": PROFILE_SKINNY_STEPS, "prefill_steps": PROFILE_PREFILL_STEPS,
+                      "mid_steps": PROFILE_MID_STEPS, "prefill_steps": PROFILE_PREFILL_STEPS,
                       "copies": PROFILE_COPIES,
                       "copy_bytes": COPY_BYTES}), flush=True)
 
@@ -571,8 +601,8 @@ def summarize_pmc(fetch_csv, write_csv):
         factor = (sum(copies) / len(copies)) * 1024.0 / COPY_BYTES
         kern = {}
         for _, name, v in rows:
-            if name.startswith("_ZN4orth20skinny_reduce_kernel"):  # the trace keeps this name mangled
-                name = "orth::skinny_reduce_kernel"
+            if "quarter_reduce_kernel" in name:  # the trace keeps this name mangled
+                name = "orth::quarter_reduce_kernel"
             if "orth::" in name:
                 kern.setdefault(name, []).append(v)
         per[counter] = (factor, kern)
@@ -588,13 +618,16 @@ def summarize_pmc(fetch_csv, write_csv):
             key, algo = f"c2_m1_alpha{int(alpha)}", W.algorithmic_bytes(c2, 1, alpha)
         elif "orth::prefill_kernel" in name:
             key, algo = "c3_m2048_alpha1", W.algorithmic_bytes(c3, 2048, 1.0)
-        elif name.startswith("void orth::skinny_kernel"):
-            m = PROFILE_SKINNY_M
+        elif name.startswith("void orth::mid_kernel"):
+            m = PROFILE_MID_M
             key, algo = f"c2_m{m}_alpha1", W.algorithmic_bytes(c2, m, 1.0)
-        elif "orth::skinny_reduce_kernel" in name:
-            # the slice reduction of the same forwards: its bytes count
-            # against the forward's algorithmic bytes in the combined entry
-            key, algo = f"c2_m{PROFILE_SKINNY_M}_alpha1_reduce", None
+        elif name.startswith("void orth::quarter_kernel"):
+            m = PROFILE_QUARTER_M
+            key, algo = f"c2_m{m}_alpha1", W.algorithmic_bytes(c2, m, 1.0)
+        elif "orth::quarter_reduce_kernel" in name:
+            # the reduction of the same forwards: its bytes count against the
+            # forward's algorithmic bytes in the combined entry
+            key, algo = f"c2_m{PROFILE_QUARTER_M}_alpha1_reduce", None
         else:
             continue
         fk = sum(f_k[name]) / len(f_k[name])
@@ -606,7 +639,7 @@ def summarize_pmc(fetch_csv, write_csv):
                     "fetch_bytes": int(fb), "write_bytes": int(wb), "bytes": int(fb + wb),
                     "algorithmic_bytes": algo,
                     "ratio_to_algorithmic": round((fb + wb) / algo, 4) if algo else None}
-    mk, rk = f"c2_m{PROFILE_SKINNY_M}_alpha1", f"c2_m{PROFILE_SKINNY_M}_alpha1_reduce"
+    mk, rk = f"c2_m{PROFILE_QUARTER_M}_alpha1", f"c2_m{PROFILE_QUARTER_M}_alpha1_reduce"
     if mk in out and rk in out:
         tot = out[mk]["bytes"] + out[rk]["bytes"]
         out[mk + "_forward"] = {"kernels": [out[mk]["kernel"], out[rk]["kernel"]], "bytes": tot,
