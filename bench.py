@@ -523,6 +523,10 @@ def time_module(torch, calls=300):
 
 
 COPY_BYTES = 512 << 20  # calibration copy: reads and writes exactly this many bytes
+# graph launches timed per secondary line, whatever --steps is: the two
+# in-graph timing events cost a fixed ~14 us per measurement (~0.6 us a
+# step at K = 20, < 0.05 us at 300); the headline keeps the caller's K
+SECONDARY_STEPS = 300
 PROFILE_DECODE_STEPS = 100
 PROFILE_PREFILL_STEPS = 5
 PROFILE_MID_STEPS = 100
@@ -730,7 +734,7 @@ def main():
     if not args.no_secondary:
         for m in (2, 4, 8, 16):
             # with the cached ortho plan, as OrthoLinear passes it
-            rr = time_workload(torch, layer, m, alpha, args.steps, 10, plan=True)
+            rr = time_workload(torch, layer, m, alpha, SECONDARY_STEPS, 10, plan=True)
             b = W.algorithmic_bytes(layer, m, alpha)
             secondary.append({"workload": f"c2 M={m}", "kernel": rr["kernel"],
                               "us_per_step": round(rr["ms_per_step"] * 1e3, 3),
@@ -752,7 +756,7 @@ def main():
                 log(f"  {secondary[-1]}")
         for cfg, m, a in (("c1", 1, 1.0), ("c1", 1, 0.0), ("c4", 8, 1.0)):
             lay = W.config_layer(cfg)
-            rr = time_workload(torch, lay, m, a, args.steps, 10, plan=True)
+            rr = time_workload(torch, lay, m, a, SECONDARY_STEPS, 10, plan=True)
             b = W.algorithmic_bytes(lay, m, a)
             secondary.append({"workload": f"{cfg} M={m} alpha={a}", "kernel": rr["kernel"],
                               "us_per_step": round(rr["ms_per_step"] * 1e3, 3),
@@ -762,7 +766,7 @@ def main():
         for m in (1, 32):
             for grouped in (False, True):
                 # 7 launches per step: a shorter graph (the capture holds them all)
-                ms, b, f, ks = time_block(torch, m, max(20, min(args.steps, 300)), grouped)
+                ms, b, f, ks = time_block(torch, m, SECONDARY_STEPS, grouped)
                 secondary.append({"workload": f"c5 Llama-2-7B block (7 projections) M={m}"
                                   + (", q/k/v and gate/up grouped" if grouped else ""),
                                   "kernel": "+".join(ks), "us_per_step": round(ms * 1e3, 3),
@@ -770,7 +774,7 @@ def main():
                                   "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                   "TFLOP/s": round(f / (ms * 1e-3) / 1e12, 2)})
                 log(f"  {secondary[-1]}")
-        r1 = time_dropin(torch, layer, 1, 1.0, 300, graph_steps=max(20, min(args.steps, 2000)))
+        r1 = time_dropin(torch, layer, 1, 1.0, 300, graph_steps=SECONDARY_STEPS)
         b = W.algorithmic_bytes(layer, 1, 1.0)
         r1.update({"workload": "reference 8-argument _C_ops.forward, c2 M=1 alpha=1 (no plan: CSR read)",
                    "GB/s_graph": round(b / (r1["us_per_launch_graph"] * 1e-6) / 1e9, 1)})
