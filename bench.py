@@ -222,7 +222,8 @@ class _Hip:
         self.c = ctypes
         h = ctypes.CDLL("libamdhip64.so")
         V, P = ctypes.c_void_p, ctypes.POINTER
-        for name, args in (("hipEventCreate", [P(V)]), ("hipEventDestroy", [V]), ("hipStreamCreate", [P(V)]),
+        for name, args in (("hipEventCreateWithFlags", [P(V), ctypes.c_uint]), ("hipEventDestroy", [V]),
+                           ("hipStreamCreate", [P(V)]),
                            ("hipStreamDestroy", [V]), ("hipStreamBeginCapture", [V, ctypes.c_int]),
                            ("hipStreamEndCapture", [V, P(V)]), ("hipGraphCreate", [P(V), ctypes.c_uint]),
                            ("hipGraphAddChildGraphNode", [P(V), V, P(V), ctypes.c_size_t, V]),
@@ -252,6 +253,7 @@ class _Hip:
 
 
 _HIP = None
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # hip_runtime_api.h
 
 
 def graph_steps_time(torch, fn, steps, pre):
@@ -286,7 +288,13 @@ def graph_steps_time(torch, fn, steps, pre):
             return g
         gA = capture(0, pre)
         gB = capture(pre, steps)
-        e0, e1 = H.new("hipEventCreate"), H.new("hipEventCreate")
+        # timing-only events: hipEventDisableSystemFence skips the system-scope
+        # cache writeback and invalidation at each event, which HIP documents
+        # for exactly this use; it cuts the fixed cost of one measurement
+        # from ~13 to ~8 us (measured: 20 decode launches 7.2 -> 7.0 us each,
+        # 2,000 launches 6.60 us either way)
+        e0 = H.new("hipEventCreateWithFlags", HIP_EVENT_DISABLE_SYSTEM_FENCE)
+        e1 = H.new("hipEventCreateWithFlags", HIP_EVENT_DISABLE_SYSTEM_FENCE)
         events += [e0, e1]
         # the timed segment's roots and leaves, then an event node before the
         # roots and one after the leaves, inside the segment's graph
@@ -524,8 +532,8 @@ def time_module(torch, calls=300):
 
 COPY_BYTES = 512 << 20  # calibration copy: reads and writes exactly this many bytes
 # graph launches timed per secondary line, whatever --steps is: the two
-# in-graph timing events cost a fixed ~14 us per measurement (~0.6 us a
-# step at K = 20, < 0.05 us at 300); the headline keeps the caller's K
+# in-graph timing events cost a fixed ~8 us per measurement (~0.4 us a
+# step at K = 20, < 0.03 us at 300); the headline keeps the caller's K
 SECONDARY_STEPS = 300
 PROFILE_DECODE_STEPS = 100
 PROFILE_PREFILL_STEPS = 5

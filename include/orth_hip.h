@@ -106,7 +106,10 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  * term), the quarter-split kernel (17..32, the same conditions), the
  * split-K mid-batch kernel (other batches up to 64), the MFMA prefill
  * kernel (above), and a general kernel for shapes and dtypes the fast
- * kernels do not take (orth_hip_last_kernel() names the choice).  Kernels
+ * kernels do not take (orth_hip_last_kernel() names the choice).  BF16 I/O
+ * takes the one-launch mid-batch kernel for 1..16 tokens (K = 4096, a plan
+ * or no ortho term) and the prefill kernel from 17; FP32 I/O the general
+ * kernel.  Kernels
  * that need scratch memory (split-K partials, a prefill plan when none is
  * given) take it from a per-stream workspace or stream-ordered allocations.
  * Replaces orth_layer_forward_cuda, /root/reference/include/ortho.h:141-144

@@ -20,6 +20,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // Which kernel served a forward call (orth_hip_last_kernel()).
 enum KernelId {
@@ -97,6 +98,20 @@ __device__ __forceinline__ f16 out_f16(float v, const void *bias, int bias_dtype
     f16 r = (f16)v;
     if (bias) r = (f16)((float)r + load_as_f32(bias, bias_dtype, n));
     return r;
+}
+
+// The same for a BF16 output (round to nearest even): y = bf16(float(bf16(v)) + bias[n]).
+__device__ __forceinline__ uint16_t out_bf16(float v, const void *bias, int bias_dtype, int64_t n) {
+    uint16_t r = f32_to_bf16_bits(v);
+    if (bias) r = f32_to_bf16_bits(bf16_bits_to_f32(r) + load_as_f32(bias, bias_dtype, n));
+    return r;
+}
+
+// A 16-bit activation (FP16, or BF16 when XB) as float.
+template <bool XB>
+__device__ __forceinline__ float x16_to_f32(f16 h) {
+    if constexpr (XB) return bf16_bits_to_f32(__builtin_bit_cast(uint16_t, h));
+    else return (float)h;
 }
 
 // Sign-extend a 4-bit two's complement nibble.
@@ -179,6 +194,17 @@ __device__ __forceinline__ void int4x8_to_f16_biased(uint32_t w, uint32_t out[4]
     out[1] = (w & 0x00F000F0u) ^ 0x54805480u;
     out[2] = (t & 0x000F000Fu) ^ 0x64086408u;
     out[3] = (t & 0x00F000F0u) ^ 0x54805480u;
+}
+
+// BF16 words in the same interleaved order, biased: a 4-bit value u in
+// mantissa bits 0..3 of bfloat16 128.0 (0x4300, whose unit in the last
+// place is 1) reads as exactly 128 + u, so with u = n ^ 8 = q + 8 every half
+// is q + 136.  An MFMA over them yields sum_k x_k q_k + 136 * sum_k x_k.
+__device__ __forceinline__ void int4x8_to_bf16_biased(uint32_t w, uint32_t out[4]) {
+    out[0] = (w & 0x000F000Fu) ^ 0x43084308u;          // k-pair (0,4)
+    out[1] = ((w >> 4) & 0x000F000Fu) ^ 0x43084308u;   // (1,5)
+    out[2] = ((w >> 8) & 0x000F000Fu) ^ 0x43084308u;   // (2,6)
+    out[3] = ((w >> 12) & 0x000F000Fu) ^ 0x43084308u;  // (3,7)
 }
 
 // Reorder 8 consecutive fp16 (as 4 words (0,1)(2,3)(4,5)(6,7)) into the

@@ -87,8 +87,12 @@ struct MidArgs {
 // wave's quarter as one aligned 16-byte vector), 4 one scale per row.
 // SPARSE: 0 no ortho term; 3 / 4 / 5 / 6 plan records of 256 / 512 / <= 1024
 // / <= 2048 words.  DB: the partial and sum regions alternate between
-// iterations (one barrier per iteration; else two).
-template <int MT, int GMODE, int SPARSE, bool DB>
+// iterations (one barrier per iteration; else two).  XB: BF16 activations
+// and output (v_mfma_f32_16x16x32_bf16, the weights as the exact BF16
+// integers q + 136; each chunk's 136 * sum x is removed with the chunk sums
+// of the activations, formed once per launch by MFMAs against a ones
+// operand).
+template <int MT, int GMODE, int SPARSE, bool DB, bool XB>
 __global__ void __launch_bounds__(kMidNT) __attribute__((amdgpu_waves_per_eu(1, 1))) mid_kernel(MidArgs a) {
     constexpr int W = kMidW;
     constexpr int CPW = kMidCPW;
@@ -190,6 +194,21 @@ __global__ void __launch_bounds__(kMidNT) __attribute__((amdgpu_waves_per_eu(1, 
 #pragma unroll
             for (int k = 0; k < 4; k++) afr[p][k] = *reinterpret_cast<const u32x4 *>(xs_lane + (p * 128 + 8 * k));
     }
+    // XB: chunk p's activation sums, in the MFMA output layout (token
+    // 4 g + i of this lane), against a ones B operand
+    f32x4 xsum[XB ? CPW : 1];
+    if constexpr (XB) {
+        const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+#pragma unroll
+        for (int p = 0; p < CPW; p++) {
+            f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[p][k]),
+                                                            __builtin_bit_cast(bf16x8, ones), t, 0, 0, 0);
+            xsum[p] = t;
+        }
+    }
     // ---- then, over the same LDS, column by column for the ortho term: the
     //      MT tokens of column c contiguous (two 16-byte reads per entry
     //      instead of MT 2-byte ones), 16 bytes of padding after every 8
@@ -245,105 +264,138 @@ __global__ void __launch_bounds__(kMidNT) __attribute__((amdgpu_waves_per_eu(1, 
             qnext = qrow_of(b + 1);
         }
 
-        // ---- sparse sums of this quarter: 4 lanes per row, entries
-        //      start + tg + 4u in order, reduced over the quad
-        if (REC) {
-            float sacc[MT];
-#pragma unroll
-            for (int m = 0; m < MT; m++) sacc[m] = 0.f;
-            const bool ok = (er[0] == plan_cell_tag(kCellQuarter, a.N, K, a.nnz, a.qwords, b, q)) &
-                            (er[1] == 0u);  // (uniform)
-            if (ok) {
-                const uint32_t hw = er[2 + qr];
-                const int32_t lo = (int32_t)(hw & 0xffffu);
-                const int32_t hi = qr <= last_row ? (int32_t)(hw >> 16) : lo;
-                const uint32_t *ee = er + kCellHdrWords;
-                constexpr int U = 4;
-                for (int32_t j0 = lo + tg; j0 < hi; j0 += 4 * U) {
-                    uint32_t w[U];
-#pragma unroll
-                    for (int u = 0; u < U; u++) w[u] = ee[min(j0 + 4 * u, hi - 1)];
-                    // all activation reads of the batch, then the products
-                    // (else each read waits for the one before)
-                    f16x8 xh[U][MT / 8];
-                    float ve[U];
-#pragma unroll
-                    for (int u = 0; u < U; u++) {
-                        const bool ok_e = j0 + 4 * u < hi;
-                        const int cc = ok_e ? (int)(w[u] & 0xffffu) + col0 : col0;
-                        ve[u] = ok_e ? (float)__builtin_bit_cast(f16, (uint16_t)(w[u] >> 16)) : 0.f;
-                        const f16 *xc = xt_col(cc);
-#pragma unroll
-                        for (int v = 0; v < MT / 8; v++) xh[u][v] = *reinterpret_cast<const f16x8 *>(xc + 8 * v);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int u = 0; u < U; u++)
-#pragma unroll
-                        for (int m = 0; m < MT; m++)
-                            sacc[m] = __builtin_fmaf(ve[u], (float)xh[u][m >> 3][m & 7], sacc[m]);
-                }
-            } else {
-                int32_t fs = 0, fe = 0;
-                csr_row_range(a.row_ptr, n0 + min(qr, last_row), a.nnz, fs, fe);
-                if (qr > last_row) fe = fs;
-                for (int32_t j = fs + tg; j < fe; j += 4) {
-                    const int32_t c = a.col[j];
-                    const bool ok_e = c >= col0 && c < col1;
-                    const f16 *xc = xt_col(ok_e ? c : col0);
-                    const float ve = ok_e ? (float)a.vals[j] : 0.f;
-#pragma unroll
-                    for (int m = 0; m < MT; m++) sacc[m] = __builtin_fmaf(ve, (float)xc[m], sacc[m]);
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-                float v = sacc[m];
-                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
-                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
-                sacc[m] = v;
-            }
-            if (tg == 0) {
-#pragma unroll
-                for (int m = 0; m < MT; m++) sp[(q * MT + m) * 16 + qr] = sacc[m];
-            }
-        }
-
-        // ---- dense term: chunk pairs, the two MFMA chains interleaved
+        // The dense term and the ortho sums of the block, in the order that
+        // measured faster: with 16 tokens the dense pairs first (their loads of
+        // the next block's weights are issued earlier and the sums' LDS
+        // latency overlaps them; c2 13.6 -> 13.0 us), with 8 the sums first
+        // (10.8 -> 10.4 us).
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto dense_part = [&]() {
+            // ---- dense term: chunk pairs, the two MFMA chains interleaved
 #pragma unroll
-        for (int j = 0; j < CPW / 2; j++) {
-            const u32x4 w0 = wv[2 * j], w1 = wv[2 * j + 1];
-            if (MORE) {
-                load_chunk(qnext, 2 * j);
-                load_chunk(qnext, 2 * j + 1);
-            }
-            const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w};
-            const uint32_t u1[4] = {w1.x, w1.y, w1.z, w1.w};
-            f32x4 pa = f32x4{0.f, 0.f, 0.f, 0.f}, pb = pa;
+            for (int j = 0; j < CPW / 2; j++) {
+                const u32x4 w0 = wv[2 * j], w1 = wv[2 * j + 1];
+                if (MORE) {
+                    load_chunk(qnext, 2 * j);
+                    load_chunk(qnext, 2 * j + 1);
+                }
+                const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w};
+                const uint32_t u1[4] = {w1.x, w1.y, w1.z, w1.w};
+                f32x4 pa = f32x4{0.f, 0.f, 0.f, 0.f}, pb = pa;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                uint32_t b0[4], b1[4];
-                int4x8_to_f16_interleaved(u0[k], b0);
-                int4x8_to_f16_interleaved(u1[k], b1);
-                pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[2 * j][k]),
-                                                            __builtin_bit_cast(f16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
-                                                            pa, 0, 0, 0);
-                pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[2 * j + 1][k]),
-                                                            __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
-                                                            pb, 0, 0, 0);
-            }
-            float s0 = 1.0f, s1 = 1.0f;
-            if (GMODE == 1) {
-                const uint32_t s2 = sv[j];  // the scales of chunks 2j, 2j + 1 of row nl
-                s0 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 & 0xffffu));
-                s1 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 >> 16));
-            }
+                for (int k = 0; k < 4; k++) {
+                    uint32_t b0[4], b1[4];
+                    if constexpr (XB) {
+                        int4x8_to_bf16_biased(u0[k], b0);
+                        int4x8_to_bf16_biased(u1[k], b1);
+                        pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[2 * j][k]),
+                                                                     __builtin_bit_cast(bf16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
+                                                                     pa, 0, 0, 0);
+                        pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[2 * j + 1][k]),
+                                                                     __builtin_bit_cast(bf16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
+                                                                     pb, 0, 0, 0);
+                    } else {
+                        int4x8_to_f16_interleaved(u0[k], b0);
+                        int4x8_to_f16_interleaved(u1[k], b1);
+                        pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[2 * j][k]),
+                                                                    __builtin_bit_cast(f16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
+                                                                    pa, 0, 0, 0);
+                        pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[2 * j + 1][k]),
+                                                                    __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
+                                                                    pb, 0, 0, 0);
+                    }
+                }
+                if constexpr (XB) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                acc[k] += s0 * pa[k];
-                acc[k] += s1 * pb[k];
+                    for (int k = 0; k < 4; k++) {
+                        pa[k] -= 136.0f * xsum[2 * j][k];
+                        pb[k] -= 136.0f * xsum[2 * j + 1][k];
+                    }
+                }
+                float s0 = 1.0f, s1 = 1.0f;
+                if (GMODE == 1) {
+                    const uint32_t s2 = sv[j];  // the scales of chunks 2j, 2j + 1 of row nl
+                    s0 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 & 0xffffu));
+                    s1 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 >> 16));
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    acc[k] += s0 * pa[k];
+                    acc[k] += s1 * pb[k];
+                }
             }
+        };
+        auto sparse_part = [&]() {
+            // ---- sparse sums of this quarter: 4 lanes per row, entries
+            //      start + tg + 4u in order, reduced over the quad
+            if (REC) {
+                float sacc[MT];
+#pragma unroll
+                for (int m = 0; m < MT; m++) sacc[m] = 0.f;
+                const bool ok = (er[0] == plan_cell_tag(kCellQuarter, a.N, K, a.nnz, a.qwords, b, q)) &
+                                (er[1] == 0u);  // (uniform)
+                if (ok) {
+                    const uint32_t hw = er[2 + qr];
+                    const int32_t lo = (int32_t)(hw & 0xffffu);
+                    const int32_t hi = qr <= last_row ? (int32_t)(hw >> 16) : lo;
+                    const uint32_t *ee = er + kCellHdrWords;
+                    constexpr int U = 4;
+                    for (int32_t j0 = lo + tg; j0 < hi; j0 += 4 * U) {
+                        uint32_t w[U];
+#pragma unroll
+                        for (int u = 0; u < U; u++) w[u] = ee[min(j0 + 4 * u, hi - 1)];
+                        // all activation reads of the batch, then the products
+                        // (else each read waits for the one before)
+                        f16x8 xh[U][MT / 8];
+                        float ve[U];
+#pragma unroll
+                        for (int u = 0; u < U; u++) {
+                            const bool ok_e = j0 + 4 * u < hi;
+                            const int cc = ok_e ? (int)(w[u] & 0xffffu) + col0 : col0;
+                            ve[u] = ok_e ? (float)__builtin_bit_cast(f16, (uint16_t)(w[u] >> 16)) : 0.f;
+                            const f16 *xc = xt_col(cc);
+#pragma unroll
+                            for (int v = 0; v < MT / 8; v++) xh[u][v] = *reinterpret_cast<const f16x8 *>(xc + 8 * v);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int u = 0; u < U; u++)
+#pragma unroll
+                            for (int m = 0; m < MT; m++)
+                                sacc[m] = __builtin_fmaf(ve[u], x16_to_f32<XB>(xh[u][m >> 3][m & 7]), sacc[m]);
+                    }
+                } else {
+                    int32_t fs = 0, fe = 0;
+                    csr_row_range(a.row_ptr, n0 + min(qr, last_row), a.nnz, fs, fe);
+                    if (qr > last_row) fe = fs;
+                    for (int32_t j = fs + tg; j < fe; j += 4) {
+                        const int32_t c = a.col[j];
+                        const bool ok_e = c >= col0 && c < col1;
+                        const f16 *xc = xt_col(ok_e ? c : col0);
+                        const float ve = ok_e ? (float)a.vals[j] : 0.f;
+#pragma unroll
+                        for (int m = 0; m < MT; m++) sacc[m] = __builtin_fmaf(ve, x16_to_f32<XB>(xc[m]), sacc[m]);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    float v = sacc[m];
+                    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
+                    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
+                    sacc[m] = v;
+                }
+                if (tg == 0) {
+#pragma unroll
+                    for (int m = 0; m < MT; m++) sp[(q * MT + m) * 16 + qr] = sacc[m];
+                }
+            }
+        };
+        if constexpr (MT == 16) {
+            dense_part();
+            sparse_part();
+        } else {
+            sparse_part();
+            dense_part();
         }
 
         sv = sv_next;
@@ -366,7 +418,10 @@ __global__ void __launch_bounds__(kMidNT) __attribute__((amdgpu_waves_per_eu(1, 
                     for (int w = 0; w < W; w++) s += sp[(w * MT + m) * 16 + r];
                     v += a.alpha * s;
                 }
-                a.y[(int64_t)m * a.N + n] = out_f16(v, a.bias, a.bias_dtype, n);
+                if constexpr (XB)
+                    reinterpret_cast<uint16_t *>(a.y)[(int64_t)m * a.N + n] = out_bf16(v, a.bias, a.bias_dtype, n);
+                else
+                    a.y[(int64_t)m * a.N + n] = out_f16(v, a.bias, a.bias_dtype, n);
             }
         }
         if (!DB) __syncthreads();  // the regions are rewritten in the next iteration
@@ -380,11 +435,15 @@ __global__ void __launch_bounds__(kMidNT) __attribute__((amdgpu_waves_per_eu(1, 
 struct MidShape {
     int mt, gmode, sparse, lds, grid;
     bool db;  // alternating partial and sum regions
+    bool xb;  // BF16 activations and output
 };
 
 static bool mid_shape(const ForwardArgs &a, const void *plan, int cus, MidArgs *d, MidShape &sh) {
-    if (a.M < 5 || a.M > 16) return false;
-    if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
+    // FP16: 5..16 tokens (the decode kernel takes fewer); BF16: 1..16 (the
+    // decode kernel is FP16 only)
+    sh.xb = a.io_dtype == ORTH_DT_BF16;
+    if (a.M > 16 || a.M < (sh.xb ? 1 : 5)) return false;
+    if ((a.io_dtype != ORTH_DT_F16 && !sh.xb) || a.scale_dtype != ORTH_DT_F16) return false;
     if (a.K != 512 * kMidCPW) return false;
     if ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.x)) & 15) return false;
     if (a.N > ((int64_t)1 << 31) || a.N < 1) return false;
@@ -464,7 +523,7 @@ bool mid_supported(const ForwardArgs &a, const void *plan) {
     return mid_shape(a, plan, 256, nullptr, sh);
 }
 
-template <int MT, int GMODE, int SPARSE, bool DB>
+template <int MT, int GMODE, int SPARSE, bool DB, bool XB>
 static hipError_t mid_launch_t(const MidArgs &d, const MidShape &sh, hipStream_t s) {
     // more than 64 KB of dynamic LDS must be allowed once per device (the
     // attribute call is idempotent, so two threads racing to set it is harmless)
@@ -472,34 +531,40 @@ static hipError_t mid_launch_t(const MidArgs &d, const MidShape &sh, hipStream_t
     int dev = 0;
     if (sh.lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 &&
         !allowed[dev].load(std::memory_order_acquire)) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(mid_kernel<MT, GMODE, SPARSE, DB>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(mid_kernel<MT, GMODE, SPARSE, DB, XB>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMidLdsMax);
         if (e != hipSuccess) return e;
         allowed[dev].store(1, std::memory_order_release);
     }
-    hipLaunchKernelGGL((mid_kernel<MT, GMODE, SPARSE, DB>), dim3((unsigned)sh.grid), dim3(kMidNT), (uint32_t)sh.lds, s,
-                       d);
+    hipLaunchKernelGGL((mid_kernel<MT, GMODE, SPARSE, DB, XB>), dim3((unsigned)sh.grid), dim3(kMidNT), (uint32_t)sh.lds,
+                       s, d);
     return hipGetLastError();
 }
 
-template <int MT, int GMODE, bool DB>
+template <int MT, int GMODE, bool DB, bool XB>
 static hipError_t mid_launch_s(const MidArgs &d, const MidShape &sh, hipStream_t s) {
     switch (sh.sparse) {
-        case 3: return mid_launch_t<MT, GMODE, 3, DB>(d, sh, s);
-        case 4: return mid_launch_t<MT, GMODE, 4, DB>(d, sh, s);
-        case 5: return mid_launch_t<MT, GMODE, 5, DB>(d, sh, s);
+        case 3: return mid_launch_t<MT, GMODE, 3, DB, XB>(d, sh, s);
+        case 4: return mid_launch_t<MT, GMODE, 4, DB, XB>(d, sh, s);
+        case 5: return mid_launch_t<MT, GMODE, 5, DB, XB>(d, sh, s);
         case 6:
             // 16 tokens: the activations leave no LDS for records of 2048
             // words (mid_shape refuses them)
-            if constexpr (MT == 8) return mid_launch_t<MT, GMODE, 6, DB>(d, sh, s);
+            if constexpr (MT == 8) return mid_launch_t<MT, GMODE, 6, DB, XB>(d, sh, s);
             return hipErrorInvalidValue;
-        default: return mid_launch_t<MT, GMODE, 0, DB>(d, sh, s);
+        default: return mid_launch_t<MT, GMODE, 0, DB, XB>(d, sh, s);
     }
 }
 
-template <int MT, int GMODE>
+template <int MT, int GMODE, bool XB>
 static hipError_t mid_launch_b(const MidArgs &d, const MidShape &sh, hipStream_t s) {
-    return sh.db ? mid_launch_s<MT, GMODE, true>(d, sh, s) : mid_launch_s<MT, GMODE, false>(d, sh, s);
+    return sh.db ? mid_launch_s<MT, GMODE, true, XB>(d, sh, s) : mid_launch_s<MT, GMODE, false, XB>(d, sh, s);
+}
+
+template <bool XB>
+static hipError_t mid_launch_x(const MidArgs &d, const MidShape &sh, hipStream_t s) {
+    if (sh.mt == 8) return sh.gmode == 1 ? mid_launch_b<8, 1, XB>(d, sh, s) : mid_launch_b<8, 4, XB>(d, sh, s);
+    return sh.gmode == 1 ? mid_launch_b<16, 1, XB>(d, sh, s) : mid_launch_b<16, 4, XB>(d, sh, s);
 }
 
 // plan: the layer's ortho plan (required when the ortho term is on).
@@ -507,8 +572,7 @@ hipError_t launch_mid(const ForwardArgs &a, const void *plan, int cus, hipStream
     MidArgs d;
     MidShape sh;
     if (!mid_shape(a, plan, cus, &d, sh)) return hipErrorInvalidValue;
-    if (sh.mt == 8) return sh.gmode == 1 ? mid_launch_b<8, 1>(d, sh, stream) : mid_launch_b<8, 4>(d, sh, stream);
-    return sh.gmode == 1 ? mid_launch_b<16, 1>(d, sh, stream) : mid_launch_b<16, 4>(d, sh, stream);
+    return sh.xb ? mid_launch_x<true>(d, sh, stream) : mid_launch_x<false>(d, sh, stream);
 }
 
 }  // namespace orth

@@ -473,30 +473,61 @@ __device__ __forceinline__ uint32_t dq_byte(uint32_t w, f16x2 s2, int i) {
     return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p) + bias) * s2);
 }
 
+// The same pair for BF16 activations: q is exact in FP32 (the nibble under
+// 2^23 = 0x4B000000, minus 2^23 + 8), q*s is exact in FP32 (a 4-bit times
+// an 11-bit significand), and one rounding (nearest even) gives the BF16
+// weight.
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+}
+
+__device__ __forceinline__ uint32_t dq_byte_bf16(uint32_t w, float s, int i) {
+    const uint32_t b = w >> (8 * i);
+    const float q0 = __uint_as_float(((b & 0xFu) ^ 8u) | 0x4B000000u) - 8388616.0f;
+    const float q1 = __uint_as_float((((b >> 4) & 0xFu) ^ 8u) | 0x4B000000u) - 8388616.0f;
+    return pk_bf16(q0 * s, q1 * s);
+}
+
+template <bool XB>
 __device__ __forceinline__ void pf_store_b(const PfB &r, f16 *Bs) {
     const f16 sc = __builtin_bit_cast(f16, (uint16_t)r.s);
     const f16x2 s2 = {sc, sc};
+    const float sf = (float)sc;
     const int row = threadIdx.x >> 2, c0 = (threadIdx.x & 3) * 2;
     const uint32_t words[2] = {r.v.x, r.v.y};
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        const u32x4 o = {dq_byte(words[j], s2, 0), dq_byte(words[j], s2, 1), dq_byte(words[j], s2, 2),
-                         dq_byte(words[j], s2, 3)};
+        u32x4 o;
+        if constexpr (XB)
+            o = u32x4{dq_byte_bf16(words[j], sf, 0), dq_byte_bf16(words[j], sf, 1), dq_byte_bf16(words[j], sf, 2),
+                      dq_byte_bf16(words[j], sf, 3)};
+        else
+            o = u32x4{dq_byte(words[j], s2, 0), dq_byte(words[j], s2, 1), dq_byte(words[j], s2, 2),
+                      dq_byte(words[j], s2, 3)};
         *reinterpret_cast<u32x4 *>(Bs + pf_swz(row, c0 + j)) = o;
     }
 }
 
+// A staged weight (FP16, or BF16 when XB) plus alpha * v, rounded back.
+template <bool XB>
+__device__ __forceinline__ uint16_t fold_add(uint16_t cell, float add) {
+    if constexpr (XB) return __builtin_bit_cast(uint16_t, (__bf16)(bf16_bits_to_f32(cell) + add));
+    else return __builtin_bit_cast(uint16_t, (f16)((float)__builtin_bit_cast(f16, cell) + add));
+}
+
 // Adds alpha * v to the weight cell of entry e; a thread with no entry
 // updates its own trash cell instead, so the common path has no branch.
+template <bool XB>
 __device__ __forceinline__ void fold_fast(f16 *Bs, f16 *trash, uint32_t e, bool valid, float alpha) {
     const int r = (e >> 24) & (PF_BN - 1), c = (e >> 16) & (PF_BK - 1);  // always inside the tile
     const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
-    f16 *p = valid ? Bs + pf_swz(r, c >> 3) + (c & 7) : trash + threadIdx.x;
-    *p = (f16)((float)*p + alpha * v);
+    uint16_t *p = reinterpret_cast<uint16_t *>(valid ? Bs + pf_swz(r, c >> 3) + (c & 7) : trash + threadIdx.x);
+    *p = fold_add<XB>(*p, alpha * v);
 }
 
 // Duplicate (row, col) entries may share a cell: CAS on its 32-bit word
 // (index arithmetic keeps the pointer in the LDS address space).
+template <bool XB>
 __device__ __forceinline__ void fold_cas(f16 *Bs, uint32_t e, float alpha) {
     const int r = (e >> 24) & (PF_BN - 1), c = (e >> 16) & (PF_BK - 1);
     const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
@@ -506,8 +537,7 @@ __device__ __forceinline__ void fold_cas(f16 *Bs, uint32_t e, float alpha) {
     uint32_t old = *w, assumed;
     do {
         assumed = old;
-        const f16 cur = __builtin_bit_cast(f16, (uint16_t)(assumed >> sh));
-        const uint16_t nv = __builtin_bit_cast(uint16_t, (f16)((float)cur + alpha * v));
+        const uint16_t nv = fold_add<XB>((uint16_t)(assumed >> sh), alpha * v);
         const uint32_t upd = (assumed & ~(0xffffu << sh)) | ((uint32_t)nv << sh);
         old = atomicCAS(w, assumed, upd);
     } while (old != assumed);
@@ -516,6 +546,7 @@ __device__ __forceinline__ void fold_cas(f16 *Bs, uint32_t e, float alpha) {
 // Folds step u's plan entries into the weight stage Bs.  The first 512
 // entries come from the prefetched register; a step with more (dense rows,
 // skewed outliers) reads the rest here.
+template <bool XB>
 __device__ __forceinline__ void pf_fold(const PrefillArgs &a, const int32_t *offs, int u, const PfE &r,
                                         f16 *Bs, f16 *trash, bool canonical) {
     const int tid = threadIdx.x;
@@ -523,16 +554,17 @@ __device__ __forceinline__ void pf_fold(const PrefillArgs &a, const int32_t *off
     // every entry read in bounds whatever the LDS holds)
     const int32_t lo = max(offs[u], 0), hi = min(offs[u + 1], a.nnz);
     if (canonical) {
-        fold_fast(Bs, trash, r.e, lo + tid < hi, a.alpha);
+        fold_fast<XB>(Bs, trash, r.e, lo + tid < hi, a.alpha);
         // canonical entries are distinct cells: no ordering between passes
         if (hi - lo > PF_NT)
-            for (int32_t e = lo + PF_NT + tid; e < hi; e += PF_NT) fold_fast(Bs, trash, a.entries[e], true, a.alpha);
+            for (int32_t e = lo + PF_NT + tid; e < hi; e += PF_NT) fold_fast<XB>(Bs, trash, a.entries[e], true, a.alpha);
     } else {
-        if (lo + tid < hi) fold_cas(Bs, r.e, a.alpha);
-        for (int32_t e = lo + PF_NT + tid; e < hi; e += PF_NT) fold_cas(Bs, a.entries[e], a.alpha);
+        if (lo + tid < hi) fold_cas<XB>(Bs, r.e, a.alpha);
+        for (int32_t e = lo + PF_NT + tid; e < hi; e += PF_NT) fold_cas<XB>(Bs, a.entries[e], a.alpha);
     }
 }
 
+template <bool XB>
 __device__ __forceinline__ void pf_mfma(const f16 *As, const f16 *Bs, int wm, int wn,
                                         f32x16 (&acc)[2][2]) {
     const int lane = threadIdx.x & 63;
@@ -550,7 +582,12 @@ __device__ __forceinline__ void pf_mfma(const f16 *As, const f16 *Bs, int wm, in
         for (int bm = 0; bm < 2; bm++)
 #pragma unroll
             for (int bn = 0; bn < 2; bn++)
-                acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[bm], bf[bn], acc[bm][bn], 0, 0, 0);
+                if constexpr (XB)
+                    acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[bm]),
+                                                                          __builtin_bit_cast(bf16x8, bf[bn]),
+                                                                          acc[bm][bn], 0, 0, 0);
+                else
+                    acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[bm], bf[bn], acc[bm][bn], 0, 0, 0);
     }
 }
 
@@ -562,7 +599,7 @@ __device__ __forceinline__ void pf_mfma(const f16 *As, const f16 *Bs, int wm, in
 // while the wave waits for the memory queue, older loads and the fold's LDS
 // read-modify-write.  Activations use two LDS stages, weights
 // three, so no write touches a stage being read.
-template <bool FOLD, int J>
+template <bool FOLD, int J, bool XB>
 __device__ __forceinline__ void pf_step(const PrefillArgs &a, const PfLane &L, int t, int nk, int wm,
                                         int wn, f16 *As0, f16 *Bs0, const int32_t *offs, f16 *trash,
                                         bool canonical, PfA (&ra)[3], PfB (&rb)[3], PfE (&re)[3],
@@ -572,18 +609,20 @@ __device__ __forceinline__ void pf_step(const PrefillArgs &a, const PfLane &L, i
     // would wait for younger loads) above this step's barrier
     __builtin_amdgcn_sched_barrier(0);
     f16 *B_t = Bs0 + J * (PF_B_BYTES / 2), *B_1 = Bs0 + J1 * (PF_B_BYTES / 2), *B_2 = Bs0 + J2 * (PF_B_BYTES / 2);
-    pf_mfma(As0 + (t & 1) * (PF_A_BYTES / 2), B_t, wm, wn, acc);
+    pf_mfma<XB>(As0 + (t & 1) * (PF_A_BYTES / 2), B_t, wm, wn, acc);
     pf_load_a(a, L, min(t + 3, nk - 1), ra[J]);
     pf_load_b(a, L, min(t + 4, nk - 1), rb[J1]);
     if (FOLD) pf_load_e(a, offs, min(t + 3, nk - 1), re[J]);
     pf_store_a(L, ra[J1], As0 + ((t + 1) & 1) * (PF_A_BYTES / 2));
-    pf_store_b(rb[J2], B_2);
-    if (FOLD) pf_fold(a, offs, min(t + 1, nk - 1), re[J1], B_1, trash, canonical);
+    pf_store_b<XB>(rb[J2], B_2);
+    if (FOLD) pf_fold<XB>(a, offs, min(t + 1, nk - 1), re[J1], B_1, trash, canonical);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool FOLD>
+// XB: BF16 activations and output (v_mfma_f32_32x32x16_bf16, the staged
+// weights bf16(q*s), the fold in BF16).
+template <bool FOLD, bool XB>
 __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     f16 *As0 = reinterpret_cast<f16 *>(smem);
@@ -655,10 +694,10 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
     pf_load_b(a, L, min(1, nk - 1), rb[1]);
     if (FOLD) pf_load_e(a, offs, 0, re[0]);
     pf_store_a(L, ra[0], As0);
-    pf_store_b(rb[0], Bs0);
-    pf_store_b(rb[1], Bs0 + PF_B_BYTES / 2);
+    pf_store_b<XB>(rb[0], Bs0);
+    pf_store_b<XB>(rb[1], Bs0 + PF_B_BYTES / 2);
     __syncthreads();
-    if (FOLD) pf_fold(a, offs, 0, re[0], Bs0, trash, canonical);
+    if (FOLD) pf_fold<XB>(a, offs, 0, re[0], Bs0, trash, canonical);
     // (issued in the loop's own order, so the wait counts at the loop head
     // are the same from the prologue as from the back edge)
     __builtin_amdgcn_sched_barrier(0);
@@ -674,12 +713,12 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
 
     int t = 0;
     for (; t + 3 <= nk; t += 3) {
-        pf_step<FOLD, 0>(a, L, t, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
-        pf_step<FOLD, 1>(a, L, t + 1, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
-        pf_step<FOLD, 2>(a, L, t + 2, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
+        pf_step<FOLD, 0, XB>(a, L, t, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
+        pf_step<FOLD, 1, XB>(a, L, t + 1, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
+        pf_step<FOLD, 2, XB>(a, L, t + 2, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
     }
-    if (t < nk) pf_step<FOLD, 0>(a, L, t, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
-    if (t + 1 < nk) pf_step<FOLD, 1>(a, L, t + 1, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
+    if (t < nk) pf_step<FOLD, 0, XB>(a, L, t, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
+    if (t + 1 < nk) pf_step<FOLD, 1, XB>(a, L, t + 1, nk, wm, wn, As0, Bs0, offs, trash, canonical, ra, rb, re, acc);
 
     // epilogue: lane holds D[token 8(i/4) + 4(lane/32) + i%4][row lane%32]
     const int lane = tid & 63;
@@ -691,14 +730,19 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int64_t m = m0 + wm * 64 + bm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                if (m < a.M && n < a.N) a.y[m * a.N + n] = out_f16(acc[bm][bn][i], a.bias, a.bias_dtype, n);
+                if (m < a.M && n < a.N) {
+                    if constexpr (XB)
+                        reinterpret_cast<uint16_t *>(a.y)[m * a.N + n] = out_bf16(acc[bm][bn][i], a.bias, a.bias_dtype, n);
+                    else
+                        a.y[m * a.N + n] = out_f16(acc[bm][bn][i], a.bias, a.bias_dtype, n);
+                }
             }
         }
     }
 }
 
 bool prefill_supported(const ForwardArgs &a) {
-    if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
+    if ((a.io_dtype != ORTH_DT_F16 && a.io_dtype != ORTH_DT_BF16) || a.scale_dtype != ORTH_DT_F16) return false;
     if (a.K % PF_BK != 0) return false;
     if (a.ngroups != 1 && (a.G % PF_BK != 0 || ((a.G / PF_BK) & (a.G / PF_BK - 1)) != 0)) return false;
     if (a.has_ortho && !plan_supported(a)) return false;
@@ -737,8 +781,11 @@ hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t st
     p.nbn = (int)((a.N + PF_BN - 1) / PF_BN);
     const unsigned blocks = (unsigned)(p.nbm * p.nbn);
     if (p.fold && p.nnz <= 0) return hipErrorInvalidValue;
-    if (p.fold) hipLaunchKernelGGL(prefill_kernel<true>, dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
-    else hipLaunchKernelGGL(prefill_kernel<false>, dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    const bool xb = a.io_dtype == ORTH_DT_BF16;
+    if (p.fold && xb) hipLaunchKernelGGL((prefill_kernel<true, true>), dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    else if (p.fold) hipLaunchKernelGGL((prefill_kernel<true, false>), dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    else if (xb) hipLaunchKernelGGL((prefill_kernel<false, true>), dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<false, false>), dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
     return hipGetLastError();
 }
 
@@ -748,11 +795,15 @@ namespace orth {
 
 // Kernels that use more than 64 KB of dynamic LDS must say so per device.
 hipError_t prefill_prepare_device() {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(prefill_kernel<true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS_BYTES);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute(reinterpret_cast<const void *>(prefill_kernel<false>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS_BYTES);
+    const void *ks[4] = {reinterpret_cast<const void *>(prefill_kernel<true, false>),
+                         reinterpret_cast<const void *>(prefill_kernel<false, false>),
+                         reinterpret_cast<const void *>(prefill_kernel<true, true>),
+                         reinterpret_cast<const void *>(prefill_kernel<false, true>)};
+    for (const void *k : ks) {
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS_BYTES);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t plan_prepare_device() {

@@ -1,0 +1,132 @@
+"""BF16 activations and output on the fast paths: the one-launch mid-batch
+kernel (1..16 tokens, K = 4096: v_mfma_f32_16x16x32_bf16 over the exact
+BF16 integers q + 136) and the prefill kernel (17+ tokens:
+v_mfma_f32_32x32x16_bf16 over bf16(q*s) with the ortho term folded in
+BF16).  Each is checked against the FP64 oracle on the same BF16 inputs
+(the activations rounded to BF16 before both), and against the general
+kernel (FP32 arithmetic) on the identical device inputs."""
+import numpy as np
+import pytest
+import torch
+
+from libortho_amd import _C_ops, _lib
+from libortho_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2  # max |err| <= TOL * ||y||_inf (north_star bound; achieved ~4e-3, the BF16 output step)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _dev(gpu):
+    torch.cuda.set_device(0)
+    yield
+    _lib.set_kernel_policy("auto")
+
+
+def bf16_x(M, K, seed):
+    """Activations rounded to BF16, as float32 (the oracle's input) and as the
+    BF16 device tensor."""
+    xb = torch.from_numpy(W.make_x(M, K, seed).astype(np.float32)).to(torch.bfloat16)
+    return xb.float().numpy(), xb.cuda()
+
+
+def run(layer, xd, alpha, policy="auto", bias=None, plan=True):
+    d = W.to_device(layer)
+    y = torch.full((xd.shape[0], layer.N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    p = _C_ops.build_plan(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], layer.K) if plan else None
+    _lib.set_kernel_policy(policy)
+    try:
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], xd, y, alpha, p, bias)
+        kernel = _C_ops.last_kernel()
+    finally:
+        _lib.set_kernel_policy("auto")
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), kernel
+
+
+def check(oracle_mod, layer, x_np, alpha, y, what, rows=None):
+    ref = oracle_mod.forward_f64(layer.q, layer.scales, layer.row_ptr, layer.col, layer.vals, x_np, alpha)
+    if rows is not None:
+        ref, y = ref[rows], y[rows]
+    assert np.isfinite(y).all(), what
+    err = float(np.abs(y - ref).max())
+    assert err <= TOL * float(np.abs(ref).max()), f"{what}: max|err| {err} vs ||y|| {np.abs(ref).max()}"
+
+
+def agree_with_general(layer, xd, alpha, y, what):
+    """Both kernels accumulate in FP32 and round once to BF16: at most a few
+    BF16 steps apart."""
+    yg, kg = run(layer, xd, alpha, policy="general")
+    assert kg == "general"
+    scale = float(np.abs(yg).max())
+    assert float(np.abs(y - yg).max()) <= 2 ** -6 * scale, what
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 12, 16])
+@pytest.mark.parametrize("alpha", [1.0, 0.0])
+def test_mid_bf16_c2(oracle_mod, M, alpha):
+    lay = W.config_layer("c2")
+    x_np, xd = bf16_x(M, lay.K, 5000 + M)
+    y, k = run(lay, xd, alpha)
+    assert k == "mid"
+    check(oracle_mod, lay, x_np, alpha, y, f"bf16 mid c2 M={M} alpha={alpha}")
+    agree_with_general(lay, xd, alpha, y, f"bf16 mid c2 M={M}")
+
+
+@pytest.mark.parametrize("N,group,M,alpha", [(1000, None, 6, 1.0), (40, 128, 16, 0.5), (3000, 128, 2, 1.0)])
+def test_mid_bf16_shapes(oracle_mod, N, group, M, alpha):
+    lay = W.make_layer(4096, N, group, 0.01, 300 + N)
+    x_np, xd = bf16_x(M, 4096, 301 + M)
+    y, k = run(lay, xd, alpha)
+    assert k == "mid"
+    check(oracle_mod, lay, x_np, alpha, y, f"bf16 mid N={N} G={group} M={M}")
+
+
+def test_mid_bf16_bias_matches_the_unfused_add():
+    from oracle import pack_oracle as PO
+    lay = W.config_layer("c2")
+    _, xd = bf16_x(8, lay.K, 5100)
+    y0, _ = run(lay, xd, 1.0)
+    for dt in (torch.bfloat16, torch.float32):
+        b = (torch.randn(lay.N, generator=torch.Generator(device="cpu").manual_seed(4)) * 0.5).to(dt).cuda()
+        y, k = run(lay, xd, 1.0, bias=b)
+        assert k == "mid"
+        want = PO.f32_to_bf16_bits(y0.astype(np.float32) + b.float().cpu().numpy()[None, :])
+        got = torch.from_numpy(y).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got, want)
+
+
+def test_bf16_without_a_plan_leaves_the_mid_kernel():
+    lay = W.config_layer("c2")
+    _, xd = bf16_x(4, lay.K, 5200)
+    _, k = run(lay, xd, 1.0, plan=False)
+    assert k == "general"  # the mid kernel reads the ortho term from the plan
+    _, k = run(lay, xd, 0.0, plan=False)
+    assert k == "mid"  # no ortho term: no plan needed
+
+
+@pytest.mark.parametrize("alpha,plan", [(1.0, True), (0.5, False), (0.0, True)])
+def test_prefill_bf16(oracle_mod, alpha, plan):
+    lay = W.make_layer(4096, 1000, 128, 0.01, 400)
+    x_np, xd = bf16_x(300, 4096, 401)
+    y, k = run(lay, xd, alpha, plan=plan)
+    assert k == "prefill"
+    # rows in every 256-token tile, the first and the last
+    rows = np.array([0, 1, 100, 255, 256, 280, 299])
+    check(oracle_mod, lay, x_np, alpha, y, f"bf16 prefill alpha={alpha} plan={plan}", rows=rows)
+    agree_with_general(lay, xd, alpha, y, f"bf16 prefill alpha={alpha}")
+
+
+def test_prefill_bf16_per_row_scales_and_bias(oracle_mod):
+    from oracle import pack_oracle as PO
+    lay = W.make_layer(2048, 520, None, 0.02, 410)
+    x_np, xd = bf16_x(64, 2048, 411)
+    y, k = run(lay, xd, 1.0)
+    assert k == "prefill"
+    check(oracle_mod, lay, x_np, 1.0, y, "bf16 prefill per-row scales")
+    b = (torch.randn(lay.N, generator=torch.Generator(device="cpu").manual_seed(5)) * 0.5).to(torch.bfloat16).cuda()
+    yb, _ = run(lay, xd, 1.0, bias=b)
+    want = PO.f32_to_bf16_bits(y.astype(np.float32) + b.float().cpu().numpy()[None, :])
+    got = torch.from_numpy(yb).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
