@@ -37,6 +37,7 @@ hipError_t launch_decode(const ForwardArgs &a, const void *plan, int cus, hipStr
 bool decode_group_ok(const ForwardArgs *as, const void *const *plans, int n);
 hipError_t launch_decode_group(const ForwardArgs *as, const void *const *plans, int n, int cus, hipStream_t stream);
 bool prefill_supported(const ForwardArgs &a);
+bool decode_bf16_supported(const ForwardArgs &a, const void *plan);
 bool plan_supported(const ForwardArgs &a);
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz);
 hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t stream);
@@ -283,7 +284,7 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part,
 
 // The kernel a forward call takes under `policy` (orth_hip_set_kernel_policy).
 int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel) {
-    const bool dec_ok = decode_supported(a);
+    const bool dec_ok = decode_supported(a) || decode_bf16_supported(a, a.has_ortho ? plan : nullptr);
     const bool pre_ok = prefill_supported(a);
     // the mid-batch kernel reads each row's ortho entries through the plan;
     // without one it filters whole rows by column, which still beats the

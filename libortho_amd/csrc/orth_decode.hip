@@ -136,11 +136,15 @@ constexpr bool decode_wt(int mt, bool xlds) { return xlds && mt <= 2; }
 // block's four K quarters (256 / 512 / <= 1024 / <= 2048 words), one per
 // wave, staged through LDS and summed before the main loop (XLDS only).
 //
+// XB: BF16 activations and output (staged activations only): the weights
+// become the exact BF16 integers q + 136 (every half biased alike, the
+// chunk's bias 136 * sum x) and feed v_mfma_f32_16x16x32_bf16.
+//
 // Every global load below is unconditional with a clamped, always valid
 // address: a load under a branch makes the compiler's wait-count insertion
 // fall back to waiting for all outstanding loads, which serialises the
 // kernel behind its own weight stream.
-template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, int PD>
+template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, int PD, bool XB>
 __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     // a group launch: this workgroup's layer and its block within the layer.
     // Constant indices only: an index computed at run time into the
@@ -190,6 +194,26 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
     constexpr bool REC = SPARSE >= 3;
     constexpr int ER = 1 << (SPARSE >= 3 ? SPARSE - 3 : 0);  // record: 16-byte loads per lane
     static_assert(!REC || XLDS, "the record kernels gather staged activations");
+    static_assert(!XB || XLDS, "BF16 activations are staged");
+    // one chunk-word of weights as MFMA B operand halves, and the MFMA
+    auto wconv = [](uint32_t w, uint32_t out[4]) {
+        if constexpr (XB) int4x8_to_bf16_biased(w, out);
+        else int4x8_to_f16_biased(w, out);
+    };
+    auto mfma = [](u32x4 av, const uint32_t b[4], f32x4 c) -> f32x4 {
+        if constexpr (XB)
+            return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                           __builtin_bit_cast(bf16x8, u32x4{b[0], b[1], b[2], b[3]}),
+                                                           c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
+                                                          __builtin_bit_cast(f16x8, u32x4{b[0], b[1], b[2], b[3]}),
+                                                          c, 0, 0, 0);
+    };
+    auto store_y = [&](int64_t i, float v, int64_t n) {
+        if constexpr (XB) reinterpret_cast<uint16_t *>(a.y)[i] = out_bf16(v, a.bias, a.bias_dtype, n);
+        else a.y[i] = out_f16(v, a.bias, a.bias_dtype, n);
+    };
 
     extern __shared__ __align__(16) unsigned char smem[];
     // WT: wave w's region holds its weights during the main loop, then its
@@ -355,10 +379,13 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                     u32x4 v = xreg[m * XIT + it];
                     if (m >= a.M) v = u32x4{0, 0, 0, 0};
                     const f16x8 h = __builtin_bit_cast(f16x8, v);
-                    // even k weigh 1032, odd k weigh 72 (see int4x8_to_f16_biased)
-                    const float e = ((float)h[0] + (float)h[2]) + ((float)h[4] + (float)h[6]);
-                    const float o = ((float)h[1] + (float)h[3]) + ((float)h[5] + (float)h[7]);
-                    const float b = group_sum<16>(1032.0f * e + 72.0f * o);  // 16 pieces of a chunk
+                    // even k weigh 1032, odd k weigh 72 (see int4x8_to_f16_biased);
+                    // BF16: every k weighs 136 (int4x8_to_bf16_biased)
+                    const float e = (x16_to_f32<XB>(h[0]) + x16_to_f32<XB>(h[2])) +
+                                    (x16_to_f32<XB>(h[4]) + x16_to_f32<XB>(h[6]));
+                    const float o = (x16_to_f32<XB>(h[1]) + x16_to_f32<XB>(h[3])) +
+                                    (x16_to_f32<XB>(h[5]) + x16_to_f32<XB>(h[7]));
+                    const float b = group_sum<16>(XB ? 136.0f * (e + o) : 1032.0f * e + 72.0f * o);  // 16 pieces of a chunk
                     if (SGB) bsum[m][it] = b;
                     if (pc < wpieces) {
                         *reinterpret_cast<u32x4 *>(xs + (m * a.xstride + c_lo * 128 + pc * 8)) = permute_x8(v);
@@ -419,7 +446,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
             const int cc = ok_e ? c : 0;
 #pragma unroll
             for (int m = 0; m < MT; m++) {
-                const float xv = (float)xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))];
+                const float xv = x16_to_f32<XB>(xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))]);
                 sacc[m] = __builtin_fmaf(ok_e ? vv : 0.f, ok_e ? xv : 0.f, sacc[m]);
             }
         };
@@ -509,15 +536,13 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
             uint32_t b[4];
             u32x4 av;
             if (XLDS) {
-                int4x8_to_f16_biased(words[j], b);
+                wconv(words[j], b);
                 av = *reinterpret_cast<const u32x4 *>(xs_lane + (p * 128 + 8 * j));
             } else {
                 int4x8_to_f16_interleaved(words[j], b);
                 av = permute_x8(ag[p][j]);
             }
-            part = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
-                                                          __builtin_bit_cast(f16x8, u32x4{b[0], b[1], b[2], b[3]}),
-                                                          part, 0, 0, 0);
+            part = mfma(av, b, part);
         }
         return part;
     };
@@ -573,8 +598,8 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                     uint32_t b0[4], b1[4];
                     u32x4 a0, a1;
                     if (XLDS) {
-                        int4x8_to_f16_biased(u0[k], b0);
-                        int4x8_to_f16_biased(u1[k], b1);
+                        wconv(u0[k], b0);
+                        wconv(u1[k], b1);
                         a0 = *reinterpret_cast<const u32x4 *>(xs_lane + ((2 * j) * 128 + 8 * k));
                         a1 = *reinterpret_cast<const u32x4 *>(xs_lane + ((2 * j + 1) * 128 + 8 * k));
                     } else {
@@ -583,12 +608,8 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                         a0 = permute_x8(ag[2 * j][k]);
                         a1 = permute_x8(ag[2 * j + 1][k]);
                     }
-                    pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a0),
-                                                                __builtin_bit_cast(f16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
-                                                                pa, 0, 0, 0);
-                    pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a1),
-                                                                __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
-                                                                pb, 0, 0, 0);
+                    pa = mfma(a0, b0, pa);
+                    pb = mfma(a1, b1, pb);
                 }
                 if (WT && j + PDM < CPW / 2) load_pair(j + PDM);
                 chunk_done(pa, 2 * j);
@@ -679,8 +700,8 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int m = 0; m < MT; m++) {
                     float xv;
-                    if (XLDS) xv = (float)xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))];
-                    else xv = (float)a.x[(int64_t)min(m, a.M - 1) * K + cc];
+                    if (XLDS) xv = x16_to_f32<XB>(xs[m * a.xstride + ((cc & ~7) | interleaved_pos(cc & 7))]);
+                    else xv = x16_to_f32<XB>(a.x[(int64_t)min(m, a.M - 1) * K + cc]);
                     sacc[m] = __builtin_fmaf(vv, ok ? xv : 0.f, sacc[m]);
                 }
             }
@@ -694,8 +715,8 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int m = 0; m < MT; m++) {
                     float xv;
-                    if (XLDS) xv = (float)xs[m * a.xstride + ((c & ~7) | interleaved_pos(c & 7))];
-                    else xv = (float)a.x[(int64_t)min(m, a.M - 1) * K + c];
+                    if (XLDS) xv = x16_to_f32<XB>(xs[m * a.xstride + ((c & ~7) | interleaved_pos(c & 7))]);
+                    else xv = x16_to_f32<XB>(a.x[(int64_t)min(m, a.M - 1) * K + c]);
                     sacc[m] = __builtin_fmaf(v, xv, sacc[m]);
                 }
             }
@@ -712,7 +733,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 for (int w = 0; w < W; w++) v += red(w)[m * 16 + rl];
                 if (!GROUPED) v *= (float)srow;
                 v += a.alpha * s;
-                a.y[(int64_t)m * a.N + n] = out_f16(v, a.bias, a.bias_dtype, n);
+                store_y((int64_t)m * a.N + n, v, n);
             }
         }
         return;
@@ -734,7 +755,7 @@ __global__ void __launch_bounds__(kDecodeNT) decode_kernel(DecodeArgs a) {
                 for (int w = 0; w < W; w++) sp += (reinterpret_cast<const float *>(smem + a.lds_e) + w * a.qwords)[m * 16 + r];
                 v += a.alpha * sp;
             }
-            a.y[(int64_t)m * a.N + n] = out_f16(v, a.bias, a.bias_dtype, n);
+            store_y((int64_t)m * a.N + n, v, n);
         }
     }
 }
@@ -762,7 +783,7 @@ static int64_t decode_lds_layout(DecodeArgs &d, int mt, bool xlds, int cpw_bound
     return off;
 }
 
-template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, int PD>
+template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, int PD, bool XB>
 static hipError_t launch_decode_kp(const DecodeArgs &d, int64_t lds, hipStream_t stream) {
     // more than 64 KB of dynamic LDS must be allowed once per device (the
     // attribute call is idempotent, so two threads racing to set it is harmless)
@@ -770,29 +791,31 @@ static hipError_t launch_decode_kp(const DecodeArgs &d, int64_t lds, hipStream_t
     int dev = 0;
     if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 &&
         !allowed[dev].load(std::memory_order_acquire)) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD, XB>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecodeLdsMax);
         if (e != hipSuccess) return e;
         allowed[dev].store(1, std::memory_order_release);
     }
     const unsigned blocks = d.nextra > 0 ? (unsigned)d.blk0[d.nextra + 1] : (unsigned)((d.N + 15) / 16);
-    hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD>), dim3(blocks), dim3(kDecodeNT),
+    hipLaunchKernelGGL((decode_kernel<MT, GMODE, XLDS, CPW, SPARSE, PD, XB>), dim3(blocks), dim3(kDecodeNT),
                        (uint32_t)lds, stream, d);
     return hipGetLastError();
 }
 
 // Prefetch depth: full-width kernels (GMODE 1 and 4) by CU occupancy, the
 // others issue everything at entry past the first pairs anyway.
-template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE>
+template <int MT, int GMODE, bool XLDS, int CPW, int SPARSE, bool XB>
 static hipError_t launch_decode_k(const DecodeArgs &d, int64_t lds, hipStream_t stream) {
     if constexpr (GMODE == 1 || GMODE == 4)
-        return d.deep ? launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 3>(d, lds, stream)
-                      : launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 1>(d, lds, stream);
+        return d.deep ? launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 3, XB>(d, lds, stream)
+                      : launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 1, XB>(d, lds, stream);
     else
-        return launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 2>(d, lds, stream);
+        return launch_decode_kp<MT, GMODE, XLDS, CPW, SPARSE, 2, XB>(d, lds, stream);
 }
 
-template <int MT, int GMODE, bool XLDS, int CPW>
+// XB: the BF16 instantiations take the plan records or no ortho term only
+// (decode_bf16_supported).
+template <int MT, int GMODE, bool XLDS, int CPW, bool XB = false>
 static hipError_t launch_decode_t(const DecodeArgs &d0, hipStream_t stream) {
     DecodeArgs d = d0;
     // GMODE 1 and 4 kernels take exactly CPW chunks in every wave
@@ -802,18 +825,23 @@ static hipError_t launch_decode_t(const DecodeArgs &d0, hipStream_t stream) {
         if (d.has_ortho && d.qwords > 0) {
             const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW, kDecodeW * d.qwords);
             if (lds <= kDecodeLdsMax) {
-                if (d.qwords == 256) return launch_decode_k<MT, GMODE, XLDS, CPW, 3>(d, lds, stream);
-                if (d.qwords == 512) return launch_decode_k<MT, GMODE, XLDS, CPW, 4>(d, lds, stream);
-                if (d.qwords <= 1024) return launch_decode_k<MT, GMODE, XLDS, CPW, 5>(d, lds, stream);
-                return launch_decode_k<MT, GMODE, XLDS, CPW, 6>(d, lds, stream);
+                if (d.qwords == 256) return launch_decode_k<MT, GMODE, XLDS, CPW, 3, XB>(d, lds, stream);
+                if (d.qwords == 512) return launch_decode_k<MT, GMODE, XLDS, CPW, 4, XB>(d, lds, stream);
+                if (d.qwords <= 1024) return launch_decode_k<MT, GMODE, XLDS, CPW, 5, XB>(d, lds, stream);
+                if constexpr (!XB) return launch_decode_k<MT, GMODE, XLDS, CPW, 6, XB>(d, lds, stream);
+                return hipErrorInvalidValue;
             }
         }
     }
     const int64_t lds = decode_lds_layout(d, MT, XLDS, CPW, 0);
     if (lds > kDecodeLdsMax) return hipErrorInvalidValue;
-    if (d.has_ortho && d.csr_vec) return launch_decode_k<MT, GMODE, XLDS, CPW, 1>(d, lds, stream);
-    if (d.has_ortho) return launch_decode_k<MT, GMODE, XLDS, CPW, 2>(d, lds, stream);
-    return launch_decode_k<MT, GMODE, XLDS, CPW, 0>(d, lds, stream);
+    if constexpr (XB) {
+        if (d.has_ortho) return hipErrorInvalidValue;
+    } else {
+        if (d.has_ortho && d.csr_vec) return launch_decode_k<MT, GMODE, XLDS, CPW, 1, XB>(d, lds, stream);
+        if (d.has_ortho) return launch_decode_k<MT, GMODE, XLDS, CPW, 2, XB>(d, lds, stream);
+    }
+    return launch_decode_k<MT, GMODE, XLDS, CPW, 0, XB>(d, lds, stream);
 }
 
 // Chunk-count bounds that can occur: the staged activation block is at most
@@ -854,6 +882,24 @@ static bool decode_xlds(int64_t M, int64_t K) {
     return mt * (K + 8) * 2 <= kDecodeXLdsMax;
 }
 
+int plan_qrec_words(int64_t N, int64_t K, int64_t nnz);  // orth_prefill.hip
+
+// BF16 activations (this plan or none): 1..4 tokens, K = 4096, group-128
+// scales as 16-byte vectors or per-row scales, and the ortho term (if on)
+// from plan records of at most 1024 words.
+bool decode_bf16_supported(const ForwardArgs &a, const void *plan) {
+    if (a.io_dtype != ORTH_DT_BF16 || a.scale_dtype != ORTH_DT_F16) return false;
+    if (a.M < 1 || a.M > 4 || a.K != 4096 || a.N > ((int64_t)1 << 31)) return false;
+    if ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.x)) & 15) return false;
+    if (a.ngroups != 1 && !(a.G == 128 && (reinterpret_cast<uintptr_t>(a.scales) & 15) == 0)) return false;
+    if (a.has_ortho) {
+        if (!plan || a.val_dtype != ORTH_DT_F16) return false;
+        const int qw = plan_qrec_words(a.N, a.K, a.nnz);
+        if (qw <= 0 || qw > 1024) return false;
+    }
+    return decode_xlds(a.M, a.K);
+}
+
 bool decode_supported(const ForwardArgs &a) {
     if (a.M < 1 || a.M > 16) return false;
     if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
@@ -868,8 +914,7 @@ bool decode_supported(const ForwardArgs &a) {
     return true;
 }
 
-int plan_qrec_words(int64_t N, int64_t K, int64_t nnz);  // orth_prefill.hip
-int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz);
+int64_t plan_rec_at(int64_t N, int64_t K, int64_t nnz);  // orth_prefill.hip
 
 // The per-layer fields of a decode launch for layer a (with its plan or null).
 static DecodeLayerArgs decode_layer_args(const ForwardArgs &a, const void *plan) {
@@ -897,12 +942,12 @@ static DecodeLayerArgs decode_layer_args(const ForwardArgs &a, const void *plan)
 // layers of one group launch must agree on all of it.
 struct DecodeClass {
     int mt, gmode;
-    bool xlds;
+    bool xlds, xb;
     int qwords, has_ortho, csr_vec;
     int64_t M, K, ngroups;
     bool operator==(const DecodeClass &o) const {
-        return mt == o.mt && gmode == o.gmode && xlds == o.xlds && qwords == o.qwords && has_ortho == o.has_ortho &&
-               csr_vec == o.csr_vec && M == o.M && K == o.K && ngroups == o.ngroups;
+        return mt == o.mt && gmode == o.gmode && xlds == o.xlds && xb == o.xb && qwords == o.qwords &&
+               has_ortho == o.has_ortho && csr_vec == o.csr_vec && M == o.M && K == o.K && ngroups == o.ngroups;
     }
 };
 
@@ -948,6 +993,7 @@ static DecodeClass decode_class(const ForwardArgs &a, const void *plan, DecodeAr
     // every wave takes exactly the chunk bound (8, 16 or 24 chunks)
     const bool full = d.nchunks == 4 * d.cpw && (d.cpw == 8 || d.cpw == 16 || d.cpw == 24);
     c.gmode = !grouped ? (full ? 4 : 0) : (d.gshift != 0 ? 2 : (scale_vec && full ? 1 : (d.scale_pairs ? 3 : 2)));
+    c.xb = a.io_dtype == ORTH_DT_BF16;
     c.qwords = d.qwords;
     c.has_ortho = d.has_ortho;
     c.csr_vec = d.csr_vec;
@@ -957,7 +1003,25 @@ static DecodeClass decode_class(const ForwardArgs &a, const void *plan, DecodeAr
     return c;
 }
 
+// BF16: staged activations, 1..4 tokens, K = 4096 with group-128 scale
+// vectors or per-row scales (decode_bf16_supported).
+static hipError_t decode_dispatch_bf16(const DecodeClass &c, const DecodeArgs &d, hipStream_t stream) {
+    if (!c.xlds || c.mt > 4 || d.cpw != 8) return hipErrorInvalidValue;
+    if (c.gmode == 1) {
+        if (c.mt == 1) return launch_decode_t<1, 1, true, 8, true>(d, stream);
+        if (c.mt == 2) return launch_decode_t<2, 1, true, 8, true>(d, stream);
+        return launch_decode_t<4, 1, true, 8, true>(d, stream);
+    }
+    if (c.gmode == 4) {
+        if (c.mt == 1) return launch_decode_t<1, 4, true, 8, true>(d, stream);
+        if (c.mt == 2) return launch_decode_t<2, 4, true, 8, true>(d, stream);
+        return launch_decode_t<4, 4, true, 8, true>(d, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
 static hipError_t decode_dispatch(const DecodeClass &c, const DecodeArgs &d, hipStream_t stream) {
+    if (c.xb) return decode_dispatch_bf16(c, d, stream);
     const int mt = c.mt;
     if (c.gmode == 1) return c.xlds ? launch_decode_mt<1, true>(mt, d, stream) : launch_decode_mt<1, false>(mt, d, stream);
     if (c.gmode == 3) return c.xlds ? launch_decode_mt<3, true>(mt, d, stream) : launch_decode_mt<3, false>(mt, d, stream);

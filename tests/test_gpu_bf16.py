@@ -1,6 +1,7 @@
-"""BF16 activations and output on the fast paths: the one-launch mid-batch
-kernel (1..16 tokens, K = 4096: v_mfma_f32_16x16x32_bf16 over the exact
-BF16 integers q + 136) and the prefill kernel (17+ tokens:
+"""BF16 activations and output on the fast paths: the decode kernel (1..4
+tokens) and the one-launch mid-batch kernel (5..16 tokens), both at
+K = 4096 with v_mfma_f32_16x16x32_bf16 over the exact BF16 integers
+q + 136, and the prefill kernel (17+ tokens:
 v_mfma_f32_32x32x16_bf16 over bf16(q*s) with the ortho term folded in
 BF16).  Each is checked against the FP64 oracle on the same BF16 inputs
 (the activations rounded to BF16 before both), and against the general
@@ -63,24 +64,59 @@ def agree_with_general(layer, xd, alpha, y, what):
     assert float(np.abs(y - yg).max()) <= 2 ** -6 * scale, what
 
 
-@pytest.mark.parametrize("M", [1, 3, 8, 12, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 12, 16])
 @pytest.mark.parametrize("alpha", [1.0, 0.0])
-def test_mid_bf16_c2(oracle_mod, M, alpha):
+def test_bf16_c2(oracle_mod, M, alpha):
     lay = W.config_layer("c2")
     x_np, xd = bf16_x(M, lay.K, 5000 + M)
     y, k = run(lay, xd, alpha)
-    assert k == "mid"
-    check(oracle_mod, lay, x_np, alpha, y, f"bf16 mid c2 M={M} alpha={alpha}")
-    agree_with_general(lay, xd, alpha, y, f"bf16 mid c2 M={M}")
+    assert k == ("decode" if M <= 4 else "mid")
+    check(oracle_mod, lay, x_np, alpha, y, f"bf16 {k} c2 M={M} alpha={alpha}")
+    agree_with_general(lay, xd, alpha, y, f"bf16 {k} c2 M={M}")
+    if M <= 4:
+        # the mid-batch kernel takes the same call when forced: same sums in
+        # another order
+        ym, km = run(lay, xd, alpha, policy="mid")
+        assert km == "mid"
+        assert float(np.abs(y - ym).max()) <= 2 ** -6 * float(np.abs(ym).max())
 
 
-@pytest.mark.parametrize("N,group,M,alpha", [(1000, None, 6, 1.0), (40, 128, 16, 0.5), (3000, 128, 2, 1.0)])
-def test_mid_bf16_shapes(oracle_mod, N, group, M, alpha):
+@pytest.mark.parametrize("N,group,M,alpha", [(1000, None, 6, 1.0), (40, 128, 16, 0.5), (3000, 128, 2, 1.0),
+                                             (1000, None, 1, 1.0), (40, 128, 4, 0.5), (4096, 128, 3, 0.0)])
+def test_bf16_shapes(oracle_mod, N, group, M, alpha):
     lay = W.make_layer(4096, N, group, 0.01, 300 + N)
     x_np, xd = bf16_x(M, 4096, 301 + M)
     y, k = run(lay, xd, alpha)
-    assert k == "mid"
-    check(oracle_mod, lay, x_np, alpha, y, f"bf16 mid N={N} G={group} M={M}")
+    assert k == ("decode" if M <= 4 else "mid")
+    check(oracle_mod, lay, x_np, alpha, y, f"bf16 {k} N={N} G={group} M={M}")
+
+
+def test_bf16_decode_c5_group(oracle_mod):
+    """q/k/v of the c5 block in one BF16 decode launch: the bits of the
+    separate calls, and the oracle's values."""
+    layers = {l.name: l for l in W.llama_block(case=1)}
+    names = ("q_proj", "k_proj", "v_proj")
+    x_np, xd = bf16_x(2, 4096, 5300)
+    ds, descs, plans, outs, singles = [], [], [], [], []
+    for n in names:
+        l = layers[n]
+        d = W.to_device(l)
+        p = _C_ops.build_plan(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], l.K)
+        descs.append(_C_ops.make_layer(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], l.K, l.N, 1.0,
+                                       torch.device("cuda:0")))
+        plans.append(p)
+        outs.append(torch.full((2, l.N), float("nan"), dtype=torch.bfloat16, device="cuda"))
+        ys = torch.full((2, l.N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], xd, ys, 1.0, p)
+        assert _C_ops.last_kernel() == "decode"
+        singles.append(ys)
+        ds.append(d)
+    _C_ops.forward_group(descs, xd, outs, plans, None)
+    assert _C_ops.last_kernel() == "decode_group"
+    torch.cuda.synchronize()
+    for n, yo, ys in zip(names, outs, singles):
+        assert torch.equal(yo.view(torch.int16), ys.view(torch.int16)), n
+        check(oracle_mod, layers[n], x_np, 1.0, yo.float().cpu().numpy(), f"bf16 group {n}")
 
 
 def test_mid_bf16_bias_matches_the_unfused_add():
@@ -97,13 +133,14 @@ def test_mid_bf16_bias_matches_the_unfused_add():
         assert np.array_equal(got, want)
 
 
-def test_bf16_without_a_plan_leaves_the_mid_kernel():
+def test_bf16_without_a_plan_takes_the_general_kernel():
     lay = W.config_layer("c2")
-    _, xd = bf16_x(4, lay.K, 5200)
-    _, k = run(lay, xd, 1.0, plan=False)
-    assert k == "general"  # the mid kernel reads the ortho term from the plan
-    _, k = run(lay, xd, 0.0, plan=False)
-    assert k == "mid"  # no ortho term: no plan needed
+    for M in (4, 8):
+        _, xd = bf16_x(M, lay.K, 5200 + M)
+        _, k = run(lay, xd, 1.0, plan=False)
+        assert k == "general"  # the BF16 decode and mid kernels read the ortho term from the plan
+        _, k = run(lay, xd, 0.0, plan=False)
+        assert k == ("decode" if M <= 4 else "mid")  # no ortho term: no plan needed
 
 
 @pytest.mark.parametrize("alpha,plan", [(1.0, True), (0.5, False), (0.0, True)])
