@@ -175,15 +175,17 @@ class Rotation:
                                self.plans[i % self.n])
 
 
-def time_workload(torch, layer, M, alpha, steps, warmup, plan=False, steady=False):
+def time_workload(torch, layer, M, alpha, steps, warmup, plan=False, steady=False, dtype=None):
     """Returns dict(ms_per_step, kernel, copies) for `steps` forwards timed
     by graph_steps_time, so ms_per_step is the average launch duration, the
     gaps between launches included; with ``steady``, also
-    ms_per_step_steady from a graph of STEADY_STEPS launches."""
+    ms_per_step_steady from a graph of STEADY_STEPS launches.  ``dtype``:
+    the activations' and output's dtype (FP16 unless given)."""
     from libortho_amd import _C_ops, workloads as W
+    dtype = dtype or torch.float16
     rot = Rotation(layer, torch, plan=plan)
-    x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda()
-    y = torch.empty(M, layer.N, dtype=torch.float16, device="cuda")
+    x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda().to(dtype)
+    y = torch.empty(M, layer.N, dtype=dtype, device="cuda")
     for i in range(warmup):
         rot.call(i, x, y, alpha)
     torch.cuda.synchronize()
@@ -771,6 +773,22 @@ def main():
                               "GB/s": round(b / (rr["ms_per_step"] * 1e-3) / 1e9, 1),
                               "frac_hbm": round(b / (rr["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
             log(f"  {secondary[-1]}")
+        # BF16 activations and output: the same weights and the same
+        # algorithmic bytes (2 per activation and output element either way)
+        for m in (1, 8):
+            rr = time_workload(torch, layer, m, alpha, SECONDARY_STEPS, 10, plan=True, dtype=torch.bfloat16)
+            b = W.algorithmic_bytes(layer, m, alpha)
+            secondary.append({"workload": f"c2 M={m} alpha={alpha}, BF16 activations", "kernel": rr["kernel"],
+                              "us_per_step": round(rr["ms_per_step"] * 1e3, 3),
+                              "GB/s": round(b / (rr["ms_per_step"] * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(b / (rr["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+            log(f"  {secondary[-1]}")
+        rr = time_workload(torch, layer, 2048, 1.0, 80, 3, plan=True, dtype=torch.bfloat16)
+        tf = W.algorithmic_flops(layer, 2048, 1.0) / (rr["ms_per_step"] * 1e-3) / 1e12
+        secondary.append({"workload": "prefill 4096->11008 M=2048 alpha=1.0, BF16 activations", "kernel": rr["kernel"],
+                          "us_per_step": round(rr["ms_per_step"] * 1e3, 2), "TFLOP/s": round(tf, 1),
+                          "frac_bf16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
+        log(f"  {secondary[-1]}")
         for m in (1, 32):
             for grouped in (False, True):
                 # 7 launches per step: a shorter graph (the capture holds them all)

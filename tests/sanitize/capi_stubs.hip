@@ -19,6 +19,7 @@ hipError_t launch_csr_rows(const void *, int, int64_t, int64_t, int32_t *, void 
 hipError_t launch_csr_fill(const void *, int, int64_t, int64_t, const int32_t *, const void *, int32_t *, void *, int,
                            hipStream_t) { return hipErrorInvalidValue; }
 bool decode_supported(const ForwardArgs &) { return false; }
+bool decode_bf16_supported(const ForwardArgs &, const void *) { return false; }
 hipError_t launch_decode(const ForwardArgs &, const void *, int, hipStream_t) { return hipErrorInvalidValue; }
 bool decode_group_ok(const ForwardArgs *, const void *const *, int) { return false; }
 bool mid_supported(const ForwardArgs &, const void *) { return false; }
