@@ -264,138 +264,170 @@ __global__ void __launch_bounds__(kMidNT) __attribute__((amdgpu_waves_per_eu(1, 
             qnext = qrow_of(b + 1);
         }
 
-        // The dense term and the ortho sums of the block, in the order that
-        // measured faster: with 16 tokens the dense pairs first (their loads of
-        // the next block's weights are issued earlier and the sums' LDS
-        // latency overlaps them; c2 13.6 -> 13.0 us), with 8 the sums first
-        // (10.8 -> 10.4 us).
+        // ---- dense term, one chunk pair (the two MFMA chains interleaved),
+        //      issuing the next block's weights of the pair as it goes
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto dense_part = [&]() {
-            // ---- dense term: chunk pairs, the two MFMA chains interleaved
+        auto dense_pair = [&](int j) {
+            const u32x4 w0 = wv[2 * j], w1 = wv[2 * j + 1];
+            if (MORE) {
+                load_chunk(qnext, 2 * j);
+                load_chunk(qnext, 2 * j + 1);
+            }
+            const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w};
+            const uint32_t u1[4] = {w1.x, w1.y, w1.z, w1.w};
+            f32x4 pa = f32x4{0.f, 0.f, 0.f, 0.f}, pb = pa;
 #pragma unroll
-            for (int j = 0; j < CPW / 2; j++) {
-                const u32x4 w0 = wv[2 * j], w1 = wv[2 * j + 1];
-                if (MORE) {
-                    load_chunk(qnext, 2 * j);
-                    load_chunk(qnext, 2 * j + 1);
-                }
-                const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w};
-                const uint32_t u1[4] = {w1.x, w1.y, w1.z, w1.w};
-                f32x4 pa = f32x4{0.f, 0.f, 0.f, 0.f}, pb = pa;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    uint32_t b0[4], b1[4];
-                    if constexpr (XB) {
-                        int4x8_to_bf16_biased(u0[k], b0);
-                        int4x8_to_bf16_biased(u1[k], b1);
-                        pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[2 * j][k]),
-                                                                     __builtin_bit_cast(bf16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
-                                                                     pa, 0, 0, 0);
-                        pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[2 * j + 1][k]),
-                                                                     __builtin_bit_cast(bf16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
-                                                                     pb, 0, 0, 0);
-                    } else {
-                        int4x8_to_f16_interleaved(u0[k], b0);
-                        int4x8_to_f16_interleaved(u1[k], b1);
-                        pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[2 * j][k]),
-                                                                    __builtin_bit_cast(f16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
-                                                                    pa, 0, 0, 0);
-                        pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[2 * j + 1][k]),
-                                                                    __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
-                                                                    pb, 0, 0, 0);
-                    }
-                }
+            for (int k = 0; k < 4; k++) {
+                uint32_t b0[4], b1[4];
                 if constexpr (XB) {
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        pa[k] -= 136.0f * xsum[2 * j][k];
-                        pb[k] -= 136.0f * xsum[2 * j + 1][k];
-                    }
+                    int4x8_to_bf16_biased(u0[k], b0);
+                    int4x8_to_bf16_biased(u1[k], b1);
+                    pa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[2 * j][k]),
+                                                                 __builtin_bit_cast(bf16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
+                                                                 pa, 0, 0, 0);
+                    pb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[2 * j + 1][k]),
+                                                                 __builtin_bit_cast(bf16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
+                                                                 pb, 0, 0, 0);
+                } else {
+                    int4x8_to_f16_interleaved(u0[k], b0);
+                    int4x8_to_f16_interleaved(u1[k], b1);
+                    pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[2 * j][k]),
+                                                                __builtin_bit_cast(f16x8, u32x4{b0[0], b0[1], b0[2], b0[3]}),
+                                                                pa, 0, 0, 0);
+                    pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[2 * j + 1][k]),
+                                                                __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]}),
+                                                                pb, 0, 0, 0);
                 }
-                float s0 = 1.0f, s1 = 1.0f;
-                if (GMODE == 1) {
-                    const uint32_t s2 = sv[j];  // the scales of chunks 2j, 2j + 1 of row nl
-                    s0 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 & 0xffffu));
-                    s1 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 >> 16));
-                }
+            }
+            if constexpr (XB) {
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    acc[k] += s0 * pa[k];
-                    acc[k] += s1 * pb[k];
+                    pa[k] -= 136.0f * xsum[2 * j][k];
+                    pb[k] -= 136.0f * xsum[2 * j + 1][k];
                 }
             }
-        };
-        auto sparse_part = [&]() {
-            // ---- sparse sums of this quarter: 4 lanes per row, entries
-            //      start + tg + 4u in order, reduced over the quad
-            if (REC) {
-                float sacc[MT];
+            float s0 = 1.0f, s1 = 1.0f;
+            if (GMODE == 1) {
+                const uint32_t s2 = sv[j];  // the scales of chunks 2j, 2j + 1 of row nl
+                s0 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 & 0xffffu));
+                s1 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 >> 16));
+            }
 #pragma unroll
-                for (int m = 0; m < MT; m++) sacc[m] = 0.f;
-                const bool ok = (er[0] == plan_cell_tag(kCellQuarter, a.N, K, a.nnz, a.qwords, b, q)) &
-                                (er[1] == 0u);  // (uniform)
-                if (ok) {
-                    const uint32_t hw = er[2 + qr];
-                    const int32_t lo = (int32_t)(hw & 0xffffu);
-                    const int32_t hi = qr <= last_row ? (int32_t)(hw >> 16) : lo;
-                    const uint32_t *ee = er + kCellHdrWords;
-                    constexpr int U = 4;
-                    for (int32_t j0 = lo + tg; j0 < hi; j0 += 4 * U) {
-                        uint32_t w[U];
-#pragma unroll
-                        for (int u = 0; u < U; u++) w[u] = ee[min(j0 + 4 * u, hi - 1)];
-                        // all activation reads of the batch, then the products
-                        // (else each read waits for the one before)
-                        f16x8 xh[U][MT / 8];
-                        float ve[U];
-#pragma unroll
-                        for (int u = 0; u < U; u++) {
-                            const bool ok_e = j0 + 4 * u < hi;
-                            const int cc = ok_e ? (int)(w[u] & 0xffffu) + col0 : col0;
-                            ve[u] = ok_e ? (float)__builtin_bit_cast(f16, (uint16_t)(w[u] >> 16)) : 0.f;
-                            const f16 *xc = xt_col(cc);
-#pragma unroll
-                            for (int v = 0; v < MT / 8; v++) xh[u][v] = *reinterpret_cast<const f16x8 *>(xc + 8 * v);
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                        for (int u = 0; u < U; u++)
-#pragma unroll
-                            for (int m = 0; m < MT; m++)
-                                sacc[m] = __builtin_fmaf(ve[u], x16_to_f32<XB>(xh[u][m >> 3][m & 7]), sacc[m]);
-                    }
-                } else {
-                    int32_t fs = 0, fe = 0;
-                    csr_row_range(a.row_ptr, n0 + min(qr, last_row), a.nnz, fs, fe);
-                    if (qr > last_row) fe = fs;
-                    for (int32_t j = fs + tg; j < fe; j += 4) {
-                        const int32_t c = a.col[j];
-                        const bool ok_e = c >= col0 && c < col1;
-                        const f16 *xc = xt_col(ok_e ? c : col0);
-                        const float ve = ok_e ? (float)a.vals[j] : 0.f;
-#pragma unroll
-                        for (int m = 0; m < MT; m++) sacc[m] = __builtin_fmaf(ve, x16_to_f32<XB>(xc[m]), sacc[m]);
-                    }
-                }
-#pragma unroll
-                for (int m = 0; m < MT; m++) {
-                    float v = sacc[m];
-                    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
-                    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
-                    sacc[m] = v;
-                }
-                if (tg == 0) {
-#pragma unroll
-                    for (int m = 0; m < MT; m++) sp[(q * MT + m) * 16 + qr] = sacc[m];
-                }
+            for (int k = 0; k < 4; k++) {
+                acc[k] += s0 * pa[k];
+                acc[k] += s1 * pb[k];
             }
         };
-        if constexpr (MT == 16) {
-            dense_part();
-            sparse_part();
+        static_assert(CPW == 8, "four chunk pairs per block");
+        if constexpr (!REC) {
+#pragma unroll
+            for (int j = 0; j < CPW / 2; j++) dense_pair(j);
         } else {
-            sparse_part();
-            dense_part();
+            // ---- ortho sums of this quarter, 4 lanes per row (entries
+            //      start + tg + 4u in order), reduced over the quad.  The
+            //      first two batches of 4 entries per lane are interleaved
+            //      with the dense pairs, so that their LDS round trips (the
+            //      record words, then the activations they address) overlap
+            //      the matrix work: the wave is alone on its SIMD and would
+            //      otherwise wait for each round trip.  The dense pairs stay
+            //      outside any branch (their weight loads too); a record that
+            //      does not hold all the block's entries (ok false) leaves
+            //      the batches empty and the rows are read from the CSR after.
+            float sacc[MT];
+#pragma unroll
+            for (int m = 0; m < MT; m++) sacc[m] = 0.f;
+            const bool ok = (er[0] == plan_cell_tag(kCellQuarter, a.N, K, a.nnz, a.qwords, b, q)) &
+                            (er[1] == 0u);  // (uniform)
+            const uint32_t hw = er[2 + qr];
+            const int32_t lo = ok ? (int32_t)(hw & 0xffffu) : 0;
+            const int32_t hi = ok && qr <= last_row ? (int32_t)(hw >> 16) : lo;
+            const uint32_t *ee = er + kCellHdrWords;
+            constexpr int U = 4;
+            uint32_t w[2][U];
+            f16x8 xh[U][MT / 8];
+            float ve[U];
+            auto rec_reads = [&](int k) {
+#pragma unroll
+                for (int u = 0; u < U; u++) w[k][u] = ee[max(min(lo + tg + 16 * k + 4 * u, hi - 1), 0)];
+            };
+            auto x_reads = [&](int k) {
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const bool ok_e = lo + tg + 16 * k + 4 * u < hi;
+                    const int cc = ok_e ? (int)(w[k][u] & 0xffffu) + col0 : col0;
+                    ve[u] = ok_e ? (float)__builtin_bit_cast(f16, (uint16_t)(w[k][u] >> 16)) : 0.f;
+                    const f16 *xc = xt_col(cc);
+#pragma unroll
+                    for (int v = 0; v < MT / 8; v++) xh[u][v] = *reinterpret_cast<const f16x8 *>(xc + 8 * v);
+                }
+            };
+            auto fmas = [&]() {
+#pragma unroll
+                for (int u = 0; u < U; u++)
+#pragma unroll
+                    for (int m = 0; m < MT; m++)
+                        sacc[m] = __builtin_fmaf(ve[u], x16_to_f32<XB>(xh[u][m >> 3][m & 7]), sacc[m]);
+            };
+            rec_reads(0);
+            rec_reads(1);
+            __builtin_amdgcn_sched_barrier(0);
+            dense_pair(0);
+            __builtin_amdgcn_sched_barrier(0);
+            x_reads(0);
+            __builtin_amdgcn_sched_barrier(0);
+            dense_pair(1);
+            __builtin_amdgcn_sched_barrier(0);
+            fmas();
+            x_reads(1);
+            __builtin_amdgcn_sched_barrier(0);
+            dense_pair(2);
+            __builtin_amdgcn_sched_barrier(0);
+            fmas();
+            __builtin_amdgcn_sched_barrier(0);
+            dense_pair(3);
+            if (ok) {
+                // entries past the first two batches (rows with more than 8
+                // entries in the quarter per lane of the quad)
+                for (int32_t j0 = lo + tg + 32; j0 < hi; j0 += 4 * U) {
+                    uint32_t wr[U];
+#pragma unroll
+                    for (int u = 0; u < U; u++) wr[u] = ee[min(j0 + 4 * u, hi - 1)];
+#pragma unroll
+                    for (int u = 0; u < U; u++) {
+                        const bool ok_e = j0 + 4 * u < hi;
+                        const int cc = ok_e ? (int)(wr[u] & 0xffffu) + col0 : col0;
+                        ve[u] = ok_e ? (float)__builtin_bit_cast(f16, (uint16_t)(wr[u] >> 16)) : 0.f;
+                        const f16 *xc = xt_col(cc);
+#pragma unroll
+                        for (int v = 0; v < MT / 8; v++) xh[u][v] = *reinterpret_cast<const f16x8 *>(xc + 8 * v);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    fmas();
+                }
+            } else {
+                int32_t fs = 0, fe = 0;
+                csr_row_range(a.row_ptr, n0 + min(qr, last_row), a.nnz, fs, fe);
+                if (qr > last_row) fe = fs;
+                for (int32_t j = fs + tg; j < fe; j += 4) {
+                    const int32_t c = a.col[j];
+                    const bool ok_e = c >= col0 && c < col1;
+                    const f16 *xc = xt_col(ok_e ? c : col0);
+                    const float vv = ok_e ? (float)a.vals[j] : 0.f;
+#pragma unroll
+                    for (int m = 0; m < MT; m++) sacc[m] = __builtin_fmaf(vv, x16_to_f32<XB>(xc[m]), sacc[m]);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                float v = sacc[m];
+                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
+                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
+                sacc[m] = v;
+            }
+            if (tg == 0) {
+#pragma unroll
+                for (int m = 0; m < MT; m++) sp[(q * MT + m) * 16 + qr] = sacc[m];
+            }
         }
 
         sv = sv_next;
