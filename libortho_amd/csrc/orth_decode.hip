@@ -828,8 +828,7 @@ static hipError_t launch_decode_t(const DecodeArgs &d0, hipStream_t stream) {
                 if (d.qwords == 256) return launch_decode_k<MT, GMODE, XLDS, CPW, 3, XB>(d, lds, stream);
                 if (d.qwords == 512) return launch_decode_k<MT, GMODE, XLDS, CPW, 4, XB>(d, lds, stream);
                 if (d.qwords <= 1024) return launch_decode_k<MT, GMODE, XLDS, CPW, 5, XB>(d, lds, stream);
-                if constexpr (!XB) return launch_decode_k<MT, GMODE, XLDS, CPW, 6, XB>(d, lds, stream);
-                return hipErrorInvalidValue;
+                return launch_decode_k<MT, GMODE, XLDS, CPW, 6, XB>(d, lds, stream);
             }
         }
     }
@@ -883,22 +882,6 @@ static bool decode_xlds(int64_t M, int64_t K) {
 }
 
 int plan_qrec_words(int64_t N, int64_t K, int64_t nnz);  // orth_prefill.hip
-
-// BF16 activations (this plan or none): 1..4 tokens, K = 4096, group-128
-// scales as 16-byte vectors or per-row scales, and the ortho term (if on)
-// from plan records of at most 1024 words.
-bool decode_bf16_supported(const ForwardArgs &a, const void *plan) {
-    if (a.io_dtype != ORTH_DT_BF16 || a.scale_dtype != ORTH_DT_F16) return false;
-    if (a.M < 1 || a.M > 4 || a.K != 4096 || a.N > ((int64_t)1 << 31)) return false;
-    if ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.x)) & 15) return false;
-    if (a.ngroups != 1 && !(a.G == 128 && (reinterpret_cast<uintptr_t>(a.scales) & 15) == 0)) return false;
-    if (a.has_ortho) {
-        if (!plan || a.val_dtype != ORTH_DT_F16) return false;
-        const int qw = plan_qrec_words(a.N, a.K, a.nnz);
-        if (qw <= 0 || qw > 1024) return false;
-    }
-    return decode_xlds(a.M, a.K);
-}
 
 bool decode_supported(const ForwardArgs &a) {
     if (a.M < 1 || a.M > 16) return false;
@@ -1003,10 +986,20 @@ static DecodeClass decode_class(const ForwardArgs &a, const void *plan, DecodeAr
     return c;
 }
 
-// BF16: staged activations, 1..4 tokens, K = 4096 with group-128 scale
-// vectors or per-row scales (decode_bf16_supported).
+// The BF16 instantiations: staged activations and 1..4 tokens with K = 4096
+// (group-128 scale vectors or per-row scales), or 1..2 tokens with 17..24
+// chunks per wave and paired group-128 scales (K = 11008).
+static bool decode_bf16_class_ok(const DecodeClass &c, const DecodeArgs &d) {
+    if (!c.xlds || c.mt > 4) return false;
+    if (d.cpw == 8) return c.gmode == 1 || c.gmode == 4;
+    if (d.cpw > 16 && d.cpw <= 24) return c.gmode == 3 && c.mt <= 2;
+    return false;
+}
+
 static hipError_t decode_dispatch_bf16(const DecodeClass &c, const DecodeArgs &d, hipStream_t stream) {
-    if (!c.xlds || c.mt > 4 || d.cpw != 8) return hipErrorInvalidValue;
+    if (!decode_bf16_class_ok(c, d)) return hipErrorInvalidValue;
+    if (d.cpw > 8) return c.mt == 1 ? launch_decode_t<1, 3, true, 24, true>(d, stream)
+                                     : launch_decode_t<2, 3, true, 24, true>(d, stream);
     if (c.gmode == 1) {
         if (c.mt == 1) return launch_decode_t<1, 1, true, 8, true>(d, stream);
         if (c.mt == 2) return launch_decode_t<2, 1, true, 8, true>(d, stream);
@@ -1071,6 +1064,27 @@ hipError_t launch_decode_group(const ForwardArgs *as, const void *const *plans, 
     for (int l = n; l <= kDecodeMaxGroup; l++) d.blk0[l] = (int)blk;
     d.deep = blk < 2 * (int64_t)cus;
     return decode_dispatch(c, d, stream);
+}
+
+// BF16 activations (this plan or none): a shape class with a BF16
+// instantiation (decode_bf16_class_ok), and the ortho term (if on) from
+// plan records that the LDS takes beside the staged activations.
+bool decode_bf16_supported(const ForwardArgs &a, const void *plan) {
+    if (a.io_dtype != ORTH_DT_BF16 || a.scale_dtype != ORTH_DT_F16) return false;
+    if (a.M < 1 || a.M > 4 || a.K % 128 != 0 || decode_cpw(a.K) > kDecodeMaxCPW || a.N > ((int64_t)1 << 31))
+        return false;
+    if ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.x)) & 15) return false;
+    if (a.ngroups != 1 && a.G != 128) return false;
+    if (a.has_ortho && a.val_dtype != ORTH_DT_F16) return false;
+    DecodeArgs d;
+    const DecodeClass c = decode_class(a, a.has_ortho ? plan : nullptr, d);
+    if (!decode_bf16_class_ok(c, d)) return false;
+    if (a.has_ortho) {
+        if (d.qwords <= 0 || d.qwords > 2048) return false;  // (no plan: no records)
+        const int cpw_bound = d.cpw <= 8 ? 8 : 24;
+        if (decode_lds_layout(d, c.mt, true, cpw_bound, kDecodeW * d.qwords) > kDecodeLdsMax) return false;
+    }
+    return true;
 }
 
 }  // namespace orth

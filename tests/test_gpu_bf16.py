@@ -119,6 +119,35 @@ def test_bf16_decode_c5_group(oracle_mod):
         check(oracle_mod, layers[n], x_np, 1.0, yo.float().cpu().numpy(), f"bf16 group {n}")
 
 
+def test_bf16_decode_down_proj(oracle_mod):
+    """c5's down projection (K = 11008: 22-chunk quarters, paired group-128
+    scales, 2 % ortho in records of more than 1024 words) in the BF16 decode
+    kernel at one token; two tokens of K = 11008 exceed the staged
+    activation block (as for FP16, which then takes the split-K kernel) and
+    take the general kernel."""
+    lay = {l.name: l for l in W.llama_block(case=1)}["down_proj"]
+    x_np, xd = bf16_x(1, lay.K, 5401)
+    for alpha in (1.0, 0.0):
+        y, k = run(lay, xd, alpha)
+        assert k == "decode"
+        check(oracle_mod, lay, x_np, alpha, y, f"bf16 down_proj M=1 alpha={alpha}")
+        agree_with_general(lay, xd, alpha, y, "bf16 down_proj M=1")
+    _, xd2 = bf16_x(2, lay.K, 5402)
+    _, k2 = run(lay, xd2, 1.0)
+    assert k2 == "general"
+
+
+def test_bf16_c5_block_takes_no_general_kernel(oracle_mod):
+    """Every projection of the c5 block at one BF16 token on a fast kernel."""
+    x_np, xd = bf16_x(1, 4096, 5500)
+    acts = {}
+    for l in W.llama_block(case=1):
+        xin_np, xin = (x_np, xd) if l.K == 4096 else bf16_x(1, l.K, 5501)
+        y, k = run(l, xin, 1.0)
+        assert k == "decode", (l.name, k)
+        check(oracle_mod, l, xin_np, 1.0, y, f"bf16 c5 {l.name}")
+
+
 def test_mid_bf16_bias_matches_the_unfused_add():
     from oracle import pack_oracle as PO
     lay = W.config_layer("c2")
