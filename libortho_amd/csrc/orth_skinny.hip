@@ -553,56 +553,70 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
 
 // y = sum of the S partials, in slice order.  Thread t takes 4 consecutive
 // outputs of one token (N % 4 == 0) or one output (otherwise).
+// Row block blk's outputs (its 128 rows x M tokens) are dealt to R
+// workgroups, one output group per thread; workgroup id b takes block
+// (b & 7) + 8 ((b >> 3) / R), part (b >> 3) % R, so every workgroup of
+// block blk runs on XCD blk % 8 like the slices that wrote its partials.
+// The loads of all S slices (up to 16 per round) are issued before the
+// first add (addresses clamped to the last slice, the extra ones not
+// added); sums in slice order.
+constexpr int kSkRedU = 16;
+
+static int skinny_reduce_parts(int M, int vec4) {
+    const int items = M * (vec4 ? kSkRows / 4 : kSkRows);
+    return (items + 255) / 256;
+}
+
 __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f16 *y, int M, int64_t N, int S,
-                                                            int vec4, const void *bias, int bias_dtype) {
-    // workgroup blk (on XCD blk % 8, like the slices of row block blk) adds
-    // the S partials of rows [128 blk, 128 blk + 128) for every token.  The
-    // loads of a group of 8 slices are issued before the first add (addresses
-    // clamped to the last slice, the extra ones not added); sums in slice order.
-    constexpr int U = 8;
-    const int64_t n0 = (int64_t)blockIdx.x * kSkRows;
+                                                            int vec4, int nblocks, int R, const void *bias,
+                                                            int bias_dtype) {
+    constexpr int U = kSkRedU;
+    const int q = (int)(blockIdx.x >> 3);
+    const int blk = (int)(blockIdx.x & 7) + 8 * (q / R);
+    const int r = q - (q / R) * R;
+    if (blk >= nblocks) return;
+    const int64_t n0 = (int64_t)blk * kSkRows;
     const int64_t MN = (int64_t)M * N;
+    const int idx = r * 256 + (int)threadIdx.x;
     if (vec4) {
-        for (int idx = threadIdx.x; idx < M * (kSkRows / 4); idx += 256) {
-            const int m = idx / (kSkRows / 4);
-            const int64_t n = n0 + 4 * (idx - m * (kSkRows / 4));
-            if (n >= N) continue;
-            const int64_t o = (int64_t)m * N + n;
-            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-            for (int s0 = 0; s0 < S; s0 += U) {
-                f32x4 w[U];
+        if (idx >= M * (kSkRows / 4)) return;
+        const int m = idx / (kSkRows / 4);
+        const int64_t n = n0 + 4 * (idx - m * (kSkRows / 4));
+        if (n >= N) return;
+        const int64_t o = (int64_t)m * N + n;
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < S; s0 += U) {
+            f32x4 w[U];
 #pragma unroll
-                for (int u = 0; u < U; u++)
-                    w[u] = *reinterpret_cast<const f32x4 *>(part + (int64_t)min(s0 + u, S - 1) * MN + o);
+            for (int u = 0; u < U; u++)
+                w[u] = *reinterpret_cast<const f32x4 *>(part + (int64_t)min(s0 + u, S - 1) * MN + o);
 #pragma unroll
-                for (int u = 0; u < U; u++) {
-                    if (s0 + u == 0) v = w[u];
-                    else if (s0 + u < S) v += w[u];
-                }
+            for (int u = 0; u < U; u++) {
+                if (s0 + u == 0) v = w[u];
+                else if (s0 + u < S) v += w[u];
             }
-            const f16x2 lo = {out_f16(v[0], bias, bias_dtype, n), out_f16(v[1], bias, bias_dtype, n + 1)};
-            const f16x2 hi = {out_f16(v[2], bias, bias_dtype, n + 2), out_f16(v[3], bias, bias_dtype, n + 3)};
-            *reinterpret_cast<uint2 *>(y + o) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
         }
+        const f16x2 lo = {out_f16(v[0], bias, bias_dtype, n), out_f16(v[1], bias, bias_dtype, n + 1)};
+        const f16x2 hi = {out_f16(v[2], bias, bias_dtype, n + 2), out_f16(v[3], bias, bias_dtype, n + 3)};
+        *reinterpret_cast<uint2 *>(y + o) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
     } else {
-        for (int idx = threadIdx.x; idx < M * kSkRows; idx += 256) {
-            const int m = idx / kSkRows;
-            const int64_t n = n0 + (idx - m * kSkRows);
-            if (n >= N) continue;
-            const int64_t o = (int64_t)m * N + n;
-            float v = 0.f;
-            for (int s0 = 0; s0 < S; s0 += U) {
-                float w[U];
+        if (idx >= M * kSkRows) return;
+        const int m = idx / kSkRows;
+        const int64_t n = n0 + (idx - m * kSkRows);
+        if (n >= N) return;
+        const int64_t o = (int64_t)m * N + n;
+        float v = 0.f;
+        for (int s0 = 0; s0 < S; s0 += U) {
+            float w[U];
 #pragma unroll
-                for (int u = 0; u < U; u++) w[u] = part[(int64_t)min(s0 + u, S - 1) * MN + o];
+            for (int u = 0; u < U; u++) w[u] = part[(int64_t)min(s0 + u, S - 1) * MN + o];
 #pragma unroll
-                for (int u = 0; u < U; u++) {
-                    if (s0 + u == 0) v = w[u];
-                    else if (s0 + u < S) v += w[u];
-                }
+            for (int u = 0; u < U; u++) {
+                if (s0 + u == 0) v = w[u];
+                else if (s0 + u < S) v += w[u];
             }
-            y[o] = out_f16(v, bias, bias_dtype, n);
         }
+        y[o] = out_f16(v, bias, bias_dtype, n);
     }
 }
 
@@ -781,8 +795,10 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
     }
     if (e != hipSuccess || sh.S == 1) return e;
     const int vec4 = (a.N % 4 == 0) ? 1 : 0;
-    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)sh.nblocks), dim3(256), 0, stream, part,
-                       static_cast<f16 *>(a.y), (int)a.M, a.N, sh.S, vec4, a.bias, a.bias_dtype);
+    const int R = skinny_reduce_parts((int)a.M, vec4);
+    const unsigned rblocks = (unsigned)(((sh.nblocks + 7) / 8) * 8 * R);
+    hipLaunchKernelGGL(skinny_reduce_kernel, dim3(rblocks), dim3(256), 0, stream, part, static_cast<f16 *>(a.y),
+                       (int)a.M, a.N, sh.S, vec4, sh.nblocks, R, a.bias, a.bias_dtype);
     return hipGetLastError();
 }
 

@@ -148,15 +148,16 @@ def test_bf16_c5_block_takes_no_general_kernel(oracle_mod):
         check(oracle_mod, l, xin_np, 1.0, y, f"bf16 c5 {l.name}")
 
 
-def test_mid_bf16_bias_matches_the_unfused_add():
+@pytest.mark.parametrize("M,kernel", [(8, "mid"), (1, "decode"), (3, "decode")])
+def test_bf16_bias_matches_the_unfused_add(M, kernel):
     from oracle import pack_oracle as PO
     lay = W.config_layer("c2")
-    _, xd = bf16_x(8, lay.K, 5100)
+    _, xd = bf16_x(M, lay.K, 5100 + M)
     y0, _ = run(lay, xd, 1.0)
     for dt in (torch.bfloat16, torch.float32):
         b = (torch.randn(lay.N, generator=torch.Generator(device="cpu").manual_seed(4)) * 0.5).to(dt).cuda()
         y, k = run(lay, xd, 1.0, bias=b)
-        assert k == "mid"
+        assert k == kernel
         want = PO.f32_to_bf16_bits(y0.astype(np.float32) + b.float().cpu().numpy()[None, :])
         got = torch.from_numpy(y).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
         assert np.array_equal(got, want)
