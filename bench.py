@@ -258,7 +258,7 @@ _HIP = None
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # hip_runtime_api.h
 
 
-def graph_steps_time(torch, fn, steps, pre, warm=1):
+def graph_steps_time(torch, fn, steps, pre):
     """Milliseconds per call of fn(pre + i), i < steps, timed by HIP events
     recorded inside one HIP graph: [pre untimed calls] -> [event -> the
     `steps` calls -> event].  The untimed calls put graph start-up and the
@@ -276,8 +276,7 @@ def graph_steps_time(torch, fn, steps, pre, warm=1):
     graphs, execs, events = [], [], []
     try:
         with torch.cuda.stream(ts):
-            for i in range(warm):
-                fn(i)  # any per-stream set-up outside capture (calls 0 .. warm - 1)
+            fn(0)  # any per-stream set-up outside capture
         torch.cuda.synchronize()
 
         def capture(lo, n):
@@ -358,11 +357,10 @@ def replay_timed(torch, g):
     return t0.elapsed_time(t1)
 
 
-def graph_time(torch, fn, steps, warm=1):
+def graph_time(torch, fn, steps):
     """Average duration of fn(i) for i < steps, by graph_steps_time with
-    min(steps, 50) untimed calls first (and ``warm`` eager ones before the
-    capture)."""
-    return graph_steps_time(torch, lambda i: fn(i), steps, min(steps, 50), warm)
+    min(steps, 50) untimed calls first."""
+    return graph_steps_time(torch, lambda i: fn(i), steps, min(steps, 50))
 
 
 def time_block(torch, M, steps, grouped=False):
@@ -406,8 +404,8 @@ def time_dropin(torch, layer, M, alpha, calls, graph_steps=0):
     from Python: wall and GPU time per call (the entry keeps each weight
     set's ortho plan from its first call, so the timed calls are planned);
     with graph_steps, also the per-launch time of that many calls captured in
-    a graph (weights rotated as in time_workload, each copy called once
-    eagerly on the capture stream first, as a graph's warm-up would)."""
+    a graph (weights rotated as in time_workload; captured calls take no
+    plan, so this is the CSR-reading path)."""
     import time as _t
     import libortho._C_ops as C
     from libortho_amd import workloads as W
@@ -434,7 +432,7 @@ def time_dropin(torch, layer, M, alpha, calls, graph_steps=0):
         rot = Rotation(layer, torch, plan=False)
         ms = graph_time(torch, lambda i: C.forward(*(lambda c: (c["q"], c["scales"], c["vals"], c["col"],
                                                                    c["row_ptr"]))(rot.copies[i % rot.n]),
-                                                   x, y, alpha), graph_steps, warm=rot.n)
+                                                   x, y, alpha), graph_steps)
         out["us_per_launch_graph"] = round(ms * 1e3, 3)
     return out
 
@@ -806,7 +804,8 @@ def main():
                 log(f"  {secondary[-1]}")
         r1 = time_dropin(torch, layer, 1, 1.0, 300, graph_steps=SECONDARY_STEPS)
         b = W.algorithmic_bytes(layer, 1, 1.0)
-        r1.update({"workload": "reference 8-argument _C_ops.forward, c2 M=1 alpha=1 (the entry's cached plan)",
+        r1.update({"workload": "reference 8-argument _C_ops.forward, c2 M=1 alpha=1 (eager: the entry's cached "
+                               "plan; graph: CSR read)",
                    "GB/s_graph": round(b / (r1["us_per_launch_graph"] * 1e-6) / 1e9, 1)})
         secondary.append(r1)
         log(f"  {secondary[-1]}")

@@ -135,8 +135,9 @@ def forward(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, 
     The reference's operator carries no plan, so with alpha > 0 this entry
     keeps one per weight set (:class:`_PlanCache`): the first call on a set
     builds it, later calls take the planned kernels (at 2,048 tokens of c3
-    88 instead of ~163 µs a call, which otherwise builds a temporary plan
-    each time). Results are those of ``forward_planned`` with that plan."""
+    ~100 instead of ~163 µs an eager call, which otherwise builds a
+    temporary plan each time). Results are those of ``forward_planned`` with
+    that plan; calls under graph capture take none."""
     plan = _PLANS.lookup((q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr), input,
                          alpha)
     forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input,
@@ -151,9 +152,10 @@ class _PlanCache:
     pointers and shapes (an in-place write bumps ``_version``; a freed tensor
     drops its entries).  Bounded, least recently used first out.  A plan
     built on one stream is used on another only after that stream has waited
-    on the build (once, in an eager call); under graph capture nothing is
-    built and no event is touched, so a capture uses a plan only on a stream
-    an eager call has already ordered after the build."""
+    on the build, and its memory is recorded on that stream, so freeing it
+    waits for the stream's work.  Under graph capture no plan is handed out
+    (a graph would keep the pointer of a plan this cache may free): captured
+    calls read the CSR as the reference's operator does."""
 
     MAX = 64
 
@@ -185,6 +187,8 @@ class _PlanCache:
             key = (id(ts[0]), id(ts[1]), id(ts[2]), id(ts[3]), id(ts[4]), int(input.shape[1]), dev)
         except (AttributeError, TypeError, ValueError):
             return None
+        if torch.cuda.is_current_stream_capturing():
+            return None  # a graph would keep the pointer of a plan this cache may free
         e = self._d.get(key)
         if e is not None:
             r = e["refs"]
@@ -192,16 +196,13 @@ class _PlanCache:
                     and e["sig"] == self._sig(ts)):
                 self._d.move_to_end(key)
                 cur = self._raw_stream(dev)
-                if cur in e["streams"]:
-                    return e["plan"]
-                if torch.cuda.is_current_stream_capturing():
-                    return None  # no event calls under capture: this call reads the CSR itself
-                torch.cuda.current_stream(dev).wait_event(e["event"])  # once per stream
-                e["streams"].add(cur)
+                if cur not in e["streams"]:  # first use on this stream: order it after the build,
+                    st = torch.cuda.current_stream(dev)  # and keep the plan's memory from reuse
+                    st.wait_event(e["event"])              # until this stream's work on it is done
+                    e["plan"].record_stream(st)
+                    e["streams"].add(cur)
                 return e["plan"]
             del self._d[key]
-        if torch.cuda.is_current_stream_capturing():
-            return None
         if not all(isinstance(t, torch.Tensor) and t.is_cuda and t.get_device() == dev for t in ts):
             return None  # forward_planned raises the reason
         try:

@@ -130,28 +130,32 @@ def test_plan_built_on_one_stream_used_on_another():
         assert torch.equal(yy.view(torch.int16), want.view(torch.int16))
 
 
-def test_graph_capture_uses_a_cached_plan_and_builds_none():
+def test_graph_capture_reads_the_csr_and_builds_no_plan():
+    """A captured graph would keep the pointer of a plan the cache may free,
+    so captured calls take no plan (cached or new) and read the CSR."""
     lay = W.config_layer("c2")
     d = W.to_device(lay)
     fresh = W.to_device(W.make_layer(4096, 1040, 128, 0.02, 6700))
     x = torch.from_numpy(W.make_x(1, lay.K, 6701)).cuda()
-    want, _ = planned(d, x, 1.0, lay.K)
     ref_forward(d, x, 1.0)  # cached eagerly
     assert len(_C_ops._PLANS) == 1
+    want = torch.empty(1, lay.N, dtype=torch.float16, device="cuda")
+    _C_ops.forward_planned(*args(d), x, want, 1.0, None)
+    want2 = torch.empty(1, 1040, dtype=torch.float16, device="cuda")
+    _C_ops.forward_planned(*args(fresh), x, want2, 1.0, None)
     y = torch.full((1, lay.N), float("nan"), dtype=torch.float16, device="cuda")
     y2 = torch.full((1, 1040), float("nan"), dtype=torch.float16, device="cuda")
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        _C_ops.forward(*args(d), x, y, 1.0)  # the usual eager warm-up: orders s after the build
+        _C_ops.forward(*args(d), x, y, 1.0)  # eager warm-up on the capture stream
     torch.cuda.current_stream().wait_stream(s)
     with torch.cuda.graph(g, stream=s):
         _C_ops.forward(*args(d), x, y, 1.0)
-        _C_ops.forward(*args(fresh), x, y2, 1.0)  # not cached: no plan built under capture
+        _C_ops.forward(*args(fresh), x, y2, 1.0)
     assert len(_C_ops._PLANS) == 1
-    want2 = torch.empty_like(y2)
-    _C_ops.forward_planned(*args(fresh), x, want2, 1.0, None)
+    _C_ops._PLANS.clear()  # the graph holds no plan pointer: replays are unaffected
     for _ in range(3):
         y.fill_(float("nan"))
         y2.fill_(float("nan"))
