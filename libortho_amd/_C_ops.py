@@ -128,6 +128,13 @@ def _stream(device: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def _raw_stream(dev_index: int) -> int:
+    """The current stream of device ``dev_index`` as its raw handle (cheap:
+    no Stream object)."""
+    get = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    return get(dev_index) if get is not None else torch.cuda.current_stream(dev_index).cuda_stream
+
+
 def forward(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input, output,
             alpha) -> None:
     """y = Base(x) + alpha * Ortho(x), written into ``output`` in place.
@@ -172,11 +179,6 @@ class _PlanCache:
     def _sig(ts):
         return tuple((t._version, t.data_ptr(), t.shape, t.dtype) for t in ts)
 
-    @staticmethod
-    def _raw_stream(dev_index):
-        get = getattr(torch._C, "_cuda_getCurrentRawStream", None)
-        return get(dev_index) if get is not None else torch.cuda.current_stream(dev_index).cuda_stream
-
     def lookup(self, ts, input, alpha):
         """The plan for weight tensors ``ts`` (q, scales, values, columns,
         row pointers) and ``input``, or None."""
@@ -195,7 +197,7 @@ class _PlanCache:
             if (r[0]() is ts[0] and r[1]() is ts[1] and r[2]() is ts[2] and r[3]() is ts[3] and r[4]() is ts[4]
                     and e["sig"] == self._sig(ts)):
                 self._d.move_to_end(key)
-                cur = self._raw_stream(dev)
+                cur = _raw_stream(dev)
                 if cur not in e["streams"]:  # first use on this stream: order it after the build,
                     st = torch.cuda.current_stream(dev)  # and keep the plan's memory from reuse
                     st.wait_event(e["event"])              # until this stream's work on it is done
@@ -218,7 +220,7 @@ class _PlanCache:
         def drop(_r, key=key, d=d):
             d.pop(key, None)
         self._d[key] = {"refs": tuple(weakref.ref(t, drop) for t in ts), "sig": self._sig(ts), "plan": plan,
-                        "event": ev, "streams": {self._raw_stream(dev)}}
+                        "event": ev, "streams": {_raw_stream(dev)}}
         while len(self._d) > self.MAX:
             self._d.popitem(last=False)
         return plan

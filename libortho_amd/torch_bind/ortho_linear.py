@@ -158,14 +158,32 @@ class OrthoLinear(nn.Module):
         return all(a is b for a, b in zip(ts0, ts1)) and v0 == v1
 
     def _ortho_plan(self):
-        """The cached ortho plan, rebuilt when the CSR buffers change."""
+        """The cached ortho plan, rebuilt when the CSR buffers change.  A
+        stream other than the one that built it waits on the build once, and
+        the plan's memory is recorded on it (so a rebuilt plan's old memory
+        is not reused before that stream's work is done).  Under graph
+        capture the plan is used as is (torch.cuda.graph synchronises the
+        device before capturing)."""
         if self.ortho_values.numel() == 0 or not self.ortho_values.is_cuda:
             return None
         key = self._csr_key()
+        dev = self.ortho_values.get_device()
         if not self._plan_valid(key):
             self._plan = _C.build_plan(self.base_weight, self.base_scales, self.ortho_values,
                                        self.ortho_col_indices, self.ortho_row_ptr, self.in_features)
             self._plan_key = key
+            self._plan_streams = set()
+            if self._plan is not None:
+                self._plan_event = torch.cuda.Event()
+                self._plan_event.record(torch.cuda.current_stream(dev))
+                self._plan_streams.add(_C._raw_stream(dev))
+        if self._plan is not None:
+            cur = _C._raw_stream(dev)
+            if cur not in self._plan_streams and not torch.cuda.is_current_stream_capturing():
+                st = torch.cuda.current_stream(dev)
+                st.wait_event(self._plan_event)
+                self._plan.record_stream(st)
+                self._plan_streams.add(cur)
         return self._plan
 
     def _layer_desc(self, device):
@@ -185,6 +203,18 @@ class OrthoLinear(nn.Module):
         self._plan_key = None
         self._desc_key = None
         return super()._apply(fn, *args, **kwargs)
+
+    def __getstate__(self):
+        """Copies and pickles carry the parameters and buffers, not the
+        derived caches (the C descriptor holds raw pointers, and the plan
+        and its build event belong to this module's buffers); the next
+        forward rebuilds them."""
+        state = dict(super().__getstate__())
+        for k in ("_desc", "_desc_key", "_plan_event", "_plan_streams"):
+            state.pop(k, None)
+        state["_plan"] = None
+        state["_plan_key"] = None
+        return state
 
     # --------------------------------------------------------------- forward
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -123,3 +123,26 @@ def test_a_refused_checkpoint_leaves_the_module_unchanged():
     assert m.group_size is None
     for k, v in m.state_dict().items():
         assert torch.equal(v, before[k]), k
+
+
+def test_copies_carry_the_weights_not_the_derived_caches():
+    """A module that has run a forward holds a C descriptor (raw pointers),
+    an ortho plan and its build event: ``copy.deepcopy`` and pickling drop
+    them (the copy rebuilds its own on its first forward) and keep every
+    parameter and buffer."""
+    import copy
+    import pickle
+
+    from libortho_amd import _lib
+    m = OrthoLinear(256, 64, bias=True, group_size=128)
+    with torch.no_grad():
+        m.bias.copy_(torch.arange(64, dtype=torch.float32))
+    m._desc, m._desc_key = _lib.OrthHipLayer(), ("key",)
+    m._plan, m._plan_key = torch.zeros(8, dtype=torch.uint8), ("key",)
+    m._plan_streams = {0}
+    for c in (copy.deepcopy(m), pickle.loads(pickle.dumps(m))):
+        assert c._plan is None and c._plan_key is None
+        assert not hasattr(c, "_desc") and not hasattr(c, "_plan_streams")
+        for (k, a), (k2, b) in zip(m.state_dict().items(), c.state_dict().items()):
+            assert k == k2 and torch.equal(a, b)
+    assert m._desc_key == ("key",)  # the original keeps its caches

@@ -163,3 +163,38 @@ def test_graph_capture_reads_the_csr_and_builds_no_plan():
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), want.view(torch.int16))
         assert torch.equal(y2.view(torch.int16), want2.view(torch.int16))
+
+
+def _ortholinear(K, N, seed):
+    from libortho_amd import OrthoLinear
+    rng = np.random.default_rng(seed)
+    m = OrthoLinear(K, N, group_size=128).cuda()
+    m.load_from_weights(torch.from_numpy((rng.standard_normal((N, K)) * 0.02).astype(np.float32)).cuda(),
+                        torch.from_numpy(np.where(rng.random((N, K)) < 0.02, rng.standard_normal((N, K)), 0.0)
+                                         .astype(np.float32)).cuda())
+    return m
+
+
+@torch.no_grad()
+def test_ortholinear_plan_used_on_another_stream_and_by_a_copy():
+    """OrthoLinear's own plan: a second stream waits on its build before the
+    first use there; a deep copy of a module that has run a forward rebuilds
+    its own descriptor and plan, with the same outputs."""
+    import copy
+    m = _ortholinear(4096, 1040, 6800)
+    x = torch.from_numpy(W.make_x(8, 4096, 6801)).cuda()
+    want = m(x)
+    assert _C_ops.last_kernel() == "mid"  # planned
+    torch.cuda.synchronize()
+    m.ortho_values.mul_(1.0)  # new version: the next call rebuilds the plan
+    first = m(x)  # rebuilt on the default stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):  # no wait on the default stream: only the plan's build event orders s
+        x.record_stream(s)
+        got = m(x)
+    torch.cuda.current_stream().wait_stream(s)
+    c = copy.deepcopy(m)
+    got2 = c(x)
+    torch.cuda.synchronize()
+    for y in (first, got, got2):
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
