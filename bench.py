@@ -791,6 +791,20 @@ def main():
                           "us_per_step": round(rr["ms_per_step"] * 1e3, 2), "TFLOP/s": round(tf, 1),
                           "frac_bf16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
         log(f"  {secondary[-1]}")
+        # the general kernel (one wave per output): FP32 activations and
+        # output (4 bytes each in the traffic), and an FP16 layer whose K is
+        # not a multiple of 128 (per-row scales), which no fast kernel takes
+        odd = W.make_layer(4000, 11008, None, 0.01, 4000)
+        for lay, m, dt, label in ((layer, 1, torch.float32, "c2 M=1 alpha=1.0, FP32 activations"),
+                                  (layer, 8, torch.float32, "c2 M=8 alpha=1.0, FP32 activations"),
+                                  (odd, 1, None, "4000->11008 per-row scales M=1 alpha=1.0 (K % 128 != 0)")):
+            rr = time_workload(torch, lay, m, 1.0, SECONDARY_STEPS, 10, plan=True, dtype=dt)
+            b = W.algorithmic_bytes(lay, m, 1.0) + (2 * m * (lay.K + lay.N) if dt == torch.float32 else 0)
+            secondary.append({"workload": label, "kernel": rr["kernel"],
+                              "us_per_step": round(rr["ms_per_step"] * 1e3, 3),
+                              "GB/s": round(b / (rr["ms_per_step"] * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(b / (rr["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+            log(f"  {secondary[-1]}")
         for m in (1, 32):
             for grouped in (False, True):
                 # 7 launches per step: a shorter graph (the capture holds them all)
