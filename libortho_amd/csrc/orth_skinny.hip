@@ -11,7 +11,8 @@
 //    nontemporal load per 128-wide chunk of its row at entry (all loads
 //    straight-line, addresses clamped).  The weights become biased exact FP16
 //    integers (five bit operations per 8 nibbles) and feed
-//    v_mfma_f32_16x16x32_f16 as the B operand; the activations of each
+//    v_mfma_f32_16x16x32_f16 as the B operand (BF16 activations: exact BF16
+//    integers q + 136 into v_mfma_f32_16x16x32_bf16); the activations of each
 //    16-token tile are the A operand, read from LDS (interleaved k order).
 //    The bias is removed per chunk with the activation sums computed while
 //    staging; group scales multiply each chunk's FP32 partial.
@@ -113,8 +114,11 @@ struct SkinnyArgs {
 // of a row gather two tokens each, not four); 3 .. 6 (one tile, GMODE 3) the
 // same from the plan's slice records instead of the CSR: 3 / 4 records of
 // 256 words (4: at most 8 tokens), 5 / 6 of 512 words.
-template <int NTT, int GMODE, int CPS, int SPK>
-__global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT <= 2 ? 4 : 2))) skinny_kernel(SkinnyArgs a) {
+// (4 waves per SIMD up to two token tiles; BF16 with two tiles needs the
+// registers of 2: at 4 one instantiation spilled 8 bytes)
+template <int NTT, int GMODE, int CPS, int SPK, bool XB>
+__global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT == 1 || (NTT == 2 && !XB) ? 4 : 2)))
+skinny_kernel(SkinnyArgs a) {
     constexpr bool SPARSE = SPK != 0;
     constexpr bool SREC = SPK >= 3;                  // slice records: each wave reads its 16 rows' record
     constexpr bool HALF = SPK == 2 || SPK == 4 || SPK == 6;
@@ -129,6 +133,22 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
     constexpr int PDC = FULL ? 4 : CPS;  // weight loads issued at entry
     // QUAD: four consecutive lanes per row in the sparse term (one token tile)
     constexpr bool QUAD = NTT == 1;
+    // XB: BF16 activations and output.  The weights become the exact BF16
+    // integers q + 136 (every k weighs 136 in the chunk's bias sum) and feed
+    // v_mfma_f32_16x16x32_bf16; FP16: q + 1032 (even k) / q + 72 (odd k).
+    auto wconv = [](uint32_t w, uint32_t out[4]) {
+        if constexpr (XB) int4x8_to_bf16_biased(w, out);
+        else int4x8_to_f16_biased(w, out);
+    };
+    auto mfma = [](const f16x8 &av, const uint32_t b[4], f32x4 c) -> f32x4 {
+        if constexpr (XB)
+            return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                           __builtin_bit_cast(bf16x8, u32x4{b[0], b[1], b[2], b[3]}),
+                                                           c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(f16x8, u32x4{b[0], b[1], b[2], b[3]}),
+                                                          c, 0, 0, 0);
+    };
     constexpr int EL = QUAD ? kSkEB / 4 : kSkEB;  // entries a lane loads per batch
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -234,10 +254,11 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
         u32x4 v = xreg[i];
         if (m >= a.M) v = u32x4{0, 0, 0, 0};
         const f16x8 h = __builtin_bit_cast(f16x8, v);
-        // even k weigh 1032, odd k weigh 72 (see int4x8_to_f16_biased)
-        const float e = ((float)h[0] + (float)h[2]) + ((float)h[4] + (float)h[6]);
-        const float o = ((float)h[1] + (float)h[3]) + ((float)h[5] + (float)h[7]);
-        const float b = group_sum<16>(1032.0f * e + 72.0f * o);  // the 16 pieces of (m, c)
+        // even k weigh 1032, odd k weigh 72 (see int4x8_to_f16_biased); BF16:
+        // every k weighs 136 (int4x8_to_bf16_biased)
+        const float e = (x16_to_f32<XB>(h[0]) + x16_to_f32<XB>(h[2])) + (x16_to_f32<XB>(h[4]) + x16_to_f32<XB>(h[6]));
+        const float o = (x16_to_f32<XB>(h[1]) + x16_to_f32<XB>(h[3])) + (x16_to_f32<XB>(h[5]) + x16_to_f32<XB>(h[7]));
+        const float b = group_sum<16>(XB ? 136.0f * (e + o) : 1032.0f * e + 72.0f * o);  // the 16 pieces of (m, c)
         if (m < MP && c < a.cps) {  // the LDS tile holds the host's cps chunks
             *reinterpret_cast<u32x4 *>(xs + (m * a.xstride + c * 128 + (p & 15) * 8)) = permute_x8(v);
             if ((p & 15) == 0) cr[c * MP + m] = b;
@@ -325,7 +346,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
 #pragma unroll
                 for (int t = 0; t < TQ; t++) {
                     const int m = QUAD ? tg + 4 * t : 16 * (t >> 2) + 4 * g + (t & 3);
-                    const float pr = val * (float)xs[m * xstride + xi];
+                    const float pr = val * x16_to_f32<XB>(xs[m * xstride + xi]);
                     sacc_e[t] += ok ? pr : 0.f;
                 }
             }
@@ -386,8 +407,8 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
                 const uint32_t w1[4] = {wv[p + 1].x, wv[p + 1].y, wv[p + 1].z, wv[p + 1].w};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    int4x8_to_f16_biased(w0[j], bq0[j]);
-                    int4x8_to_f16_biased(w1[j], bq1[j]);
+                    wconv(w0[j], bq0[j]);
+                    wconv(w1[j], bq1[j]);
                 }
             }
             if (!SREC && p + PDC < CPS) load_chunk(p + PDC);
@@ -403,10 +424,8 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
                 for (int j = 0; j < 4; j++) {
                     const f16x8 a0 = *reinterpret_cast<const f16x8 *>(xl + 8 * j);
                     const f16x8 a1 = *reinterpret_cast<const f16x8 *>(xl + 128 + 8 * j);
-                    pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        a0, __builtin_bit_cast(f16x8, u32x4{bq0[j][0], bq0[j][1], bq0[j][2], bq0[j][3]}), pa, 0, 0, 0);
-                    pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        a1, __builtin_bit_cast(f16x8, u32x4{bq1[j][0], bq1[j][1], bq1[j][2], bq1[j][3]}), pb, 0, 0, 0);
+                    pa = mfma(a0, bq0[j], pa);
+                    pb = mfma(a1, bq1[j], pb);
                 }
                 // D[token 4g + i][row nl]
                 const f32x4 cra = *reinterpret_cast<const f32x4 *>(cr + p * MP + tt * 16 + 4 * g);
@@ -425,7 +444,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
                 const uint32_t words[4] = {wv[p].x, wv[p].y, wv[p].z, wv[p].w};
                 uint32_t bq[4][4];
     #pragma unroll
-                for (int j = 0; j < 4; j++) int4x8_to_f16_biased(words[j], bq[j]);
+                for (int j = 0; j < 4; j++) wconv(words[j], bq[j]);
                 float s = 1.0f;
                 if (GMODE == 1) {
                     // scales of chunks kc0 + 8i + 2g', +1 sit in lane 16g' + nl
@@ -441,8 +460,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
     #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const f16x8 afr = *reinterpret_cast<const f16x8 *>(xl + 8 * j);
-                        const f16x8 bfr = __builtin_bit_cast(f16x8, u32x4{bq[j][0], bq[j][1], bq[j][2], bq[j][3]});
-                        part = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr, bfr, part, 0, 0, 0);
+                        part = mfma(afr, bq[j], part);
                     }
                     // D[token 4g + i][row nl]
                     const f32x4 crv = *reinterpret_cast<const f32x4 *>(cr + p * MP + tt * 16 + 4 * g);
@@ -494,7 +512,7 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
 #pragma unroll
                 for (int t = 0; t < TQ; t++) {
                     const int m = QUAD ? tg + 4 * t : 16 * (t >> 2) + 4 * g + (t & 3);
-                    const float pr = val * (float)xs[m * xstride + xi];
+                    const float pr = val * x16_to_f32<XB>(xs[m * xstride + xi]);
                     sacc[t] += ok ? pr : 0.f;
                 }
             }
@@ -535,7 +553,12 @@ __global__ void __launch_bounds__(kSkNT) __attribute__((amdgpu_waves_per_eu(NTT 
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = tt * 16 + 4 * g + i;
-                if (m < a.M && n < a.N) a.y[(int64_t)m * a.N + n] = out_f16(val[tt][i], a.bias, a.bias_dtype, n);
+                if (m < a.M && n < a.N) {
+                    if constexpr (XB)
+                        reinterpret_cast<uint16_t *>(a.y)[(int64_t)m * a.N + n] = out_bf16(val[tt][i], a.bias, a.bias_dtype, n);
+                    else
+                        a.y[(int64_t)m * a.N + n] = out_f16(val[tt][i], a.bias, a.bias_dtype, n);
+                }
             }
         return;
     }
@@ -569,7 +592,7 @@ static int skinny_reduce_parts(int M, int vec4) {
 
 __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f16 *y, int M, int64_t N, int S,
                                                             int vec4, int nblocks, int R, const void *bias,
-                                                            int bias_dtype) {
+                                                            int bias_dtype, int xb) {
     constexpr int U = kSkRedU;
     const int q = (int)(blockIdx.x >> 3);
     const int blk = (int)(blockIdx.x & 7) + 8 * (q / R);
@@ -596,9 +619,12 @@ __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f
                 else if (s0 + u < S) v += w[u];
             }
         }
-        const f16x2 lo = {out_f16(v[0], bias, bias_dtype, n), out_f16(v[1], bias, bias_dtype, n + 1)};
-        const f16x2 hi = {out_f16(v[2], bias, bias_dtype, n + 2), out_f16(v[3], bias, bias_dtype, n + 3)};
-        *reinterpret_cast<uint2 *>(y + o) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            h[e] = xb ? (uint32_t)out_bf16(v[e], bias, bias_dtype, n + e)
+                      : (uint32_t)__builtin_bit_cast(uint16_t, out_f16(v[e], bias, bias_dtype, n + e));
+        *reinterpret_cast<uint2 *>(y + o) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     } else {
         if (idx >= M * kSkRows) return;
         const int m = idx / kSkRows;
@@ -616,7 +642,8 @@ __global__ void __launch_bounds__(256) skinny_reduce_kernel(const float *part, f
                 else if (s0 + u < S) v += w[u];
             }
         }
-        y[o] = out_f16(v, bias, bias_dtype, n);
+        if (xb) reinterpret_cast<uint16_t *>(y)[o] = out_bf16(v, bias, bias_dtype, n);
+        else y[o] = out_f16(v, bias, bias_dtype, n);
     }
 }
 
@@ -655,7 +682,7 @@ static bool skinny_shape(const ForwardArgs &a, int cus, SkinnyShape &sh) {
 
 bool skinny_supported(const ForwardArgs &a) {
     if (a.M < 1 || a.M > 64) return false;
-    if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
+    if ((a.io_dtype != ORTH_DT_F16 && a.io_dtype != ORTH_DT_BF16) || a.scale_dtype != ORTH_DT_F16) return false;
     if (a.has_ortho && a.val_dtype != ORTH_DT_F16) return false;  // values read from the CSR as FP16
     if (a.K % 128 != 0) return false;
     if (a.ngroups != 1) {
@@ -669,7 +696,7 @@ bool skinny_supported(const ForwardArgs &a) {
     return skinny_shape(a, 256, sh);
 }
 
-template <int NTT, int GMODE, int CPS, int SPARSE>
+template <int NTT, int GMODE, int CPS, int SPARSE, bool XB>
 static hipError_t skinny_launch_t(const SkinnyArgs &d, int blocks, int lds, hipStream_t s) {
     // more than 64 KB of dynamic LDS must be allowed once per device (the
     // attribute call is idempotent, so two threads racing to set it is harmless)
@@ -677,16 +704,16 @@ static hipError_t skinny_launch_t(const SkinnyArgs &d, int blocks, int lds, hipS
     int dev = 0;
     if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 &&
         !allowed[dev].load(std::memory_order_acquire)) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(skinny_kernel<NTT, GMODE, CPS, SPARSE>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(skinny_kernel<NTT, GMODE, CPS, SPARSE, XB>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
         if (e != hipSuccess) return e;
         allowed[dev].store(1, std::memory_order_release);
     }
-    hipLaunchKernelGGL((skinny_kernel<NTT, GMODE, CPS, SPARSE>), dim3(blocks), dim3(kSkNT), (uint32_t)lds, s, d);
+    hipLaunchKernelGGL((skinny_kernel<NTT, GMODE, CPS, SPARSE, XB>), dim3(blocks), dim3(kSkNT), (uint32_t)lds, s, d);
     return hipGetLastError();
 }
 
-template <int NTT, int GMODE>
+template <int NTT, int GMODE, bool XB>
 static hipError_t skinny_launch_g(const SkinnyArgs &d, bool sparse, int blocks, int lds, hipStream_t s) {
     constexpr int C = sk_cps_bound(NTT);
     if (d.cps > C) return hipErrorInvalidValue;  // the kernel handles at most C chunks per slice
@@ -694,27 +721,38 @@ static hipError_t skinny_launch_g(const SkinnyArgs &d, bool sparse, int blocks, 
         if constexpr (NTT == 1 && GMODE == 3) {
             if (d.swords > 0) {  // slice records (launch_skinny checked the shape)
                 const bool half = d.M <= 8;
-                if (d.swords == 256) return half ? skinny_launch_t<NTT, GMODE, C, 4>(d, blocks, lds, s)
-                                                 : skinny_launch_t<NTT, GMODE, C, 3>(d, blocks, lds, s);
-                return half ? skinny_launch_t<NTT, GMODE, C, 6>(d, blocks, lds, s)
-                            : skinny_launch_t<NTT, GMODE, C, 5>(d, blocks, lds, s);
+                if (d.swords == 256) return half ? skinny_launch_t<NTT, GMODE, C, 4, XB>(d, blocks, lds, s)
+                                                 : skinny_launch_t<NTT, GMODE, C, 3, XB>(d, blocks, lds, s);
+                return half ? skinny_launch_t<NTT, GMODE, C, 6, XB>(d, blocks, lds, s)
+                            : skinny_launch_t<NTT, GMODE, C, 5, XB>(d, blocks, lds, s);
             }
         }
-        if (NTT == 1 && d.M <= 8) return skinny_launch_t<NTT, GMODE, C, (NTT == 1 ? 2 : 1)>(d, blocks, lds, s);
-        return skinny_launch_t<NTT, GMODE, C, 1>(d, blocks, lds, s);
+        if (NTT == 1 && d.M <= 8) return skinny_launch_t<NTT, GMODE, C, (NTT == 1 ? 2 : 1), XB>(d, blocks, lds, s);
+        return skinny_launch_t<NTT, GMODE, C, 1, XB>(d, blocks, lds, s);
     }
-    return skinny_launch_t<NTT, GMODE, C, 0>(d, blocks, lds, s);
+    return skinny_launch_t<NTT, GMODE, C, 0, XB>(d, blocks, lds, s);
 }
 
-template <int NTT>
+template <int NTT, bool XB>
 static hipError_t skinny_launch_n(const SkinnyArgs &d, int gmode, bool sparse, int blocks, int lds, hipStream_t s) {
     switch (gmode) {
-        case 0: return skinny_launch_g<NTT, 0>(d, sparse, blocks, lds, s);
-        case 1: return skinny_launch_g<NTT, 1>(d, sparse, blocks, lds, s);
+        case 0: return skinny_launch_g<NTT, 0, XB>(d, sparse, blocks, lds, s);
+        case 1: return skinny_launch_g<NTT, 1, XB>(d, sparse, blocks, lds, s);
         case 3:
-            if constexpr (NTT == 1) return skinny_launch_g<NTT, 3>(d, sparse, blocks, lds, s);
+            if constexpr (NTT == 1) return skinny_launch_g<NTT, 3, XB>(d, sparse, blocks, lds, s);
             return hipErrorInvalidValue;
-        default: return skinny_launch_g<NTT, 2>(d, sparse, blocks, lds, s);
+        default: return skinny_launch_g<NTT, 2, XB>(d, sparse, blocks, lds, s);
+    }
+}
+
+template <bool XB>
+static hipError_t skinny_launch_x(const SkinnyArgs &d, int ntt, int gmode, bool sparse, int blocks, int lds,
+                                  hipStream_t s) {
+    switch (ntt) {
+        case 1: return skinny_launch_n<1, XB>(d, gmode, sparse, blocks, lds, s);
+        case 2: return skinny_launch_n<2, XB>(d, gmode, sparse, blocks, lds, s);
+        case 3: return skinny_launch_n<3, XB>(d, gmode, sparse, blocks, lds, s);
+        default: return skinny_launch_n<4, XB>(d, gmode, sparse, blocks, lds, s);
     }
 }
 
@@ -786,19 +824,15 @@ hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float 
         lds += 8 * sw * 4;
     }
     const int blocks = ((sh.nblocks + 7) / 8) * 8 * sh.S;  // padded: see skinny_kernel
-    hipError_t e;
-    switch (sh.ntt) {
-        case 1: e = skinny_launch_n<1>(d, gmode, sparse, blocks, lds, stream); break;
-        case 2: e = skinny_launch_n<2>(d, gmode, sparse, blocks, lds, stream); break;
-        case 3: e = skinny_launch_n<3>(d, gmode, sparse, blocks, lds, stream); break;
-        default: e = skinny_launch_n<4>(d, gmode, sparse, blocks, lds, stream); break;
-    }
+    const bool xb = a.io_dtype == ORTH_DT_BF16;
+    const hipError_t e = xb ? skinny_launch_x<true>(d, sh.ntt, gmode, sparse, blocks, lds, stream)
+                            : skinny_launch_x<false>(d, sh.ntt, gmode, sparse, blocks, lds, stream);
     if (e != hipSuccess || sh.S == 1) return e;
     const int vec4 = (a.N % 4 == 0) ? 1 : 0;
     const int R = skinny_reduce_parts((int)a.M, vec4);
     const unsigned rblocks = (unsigned)(((sh.nblocks + 7) / 8) * 8 * R);
     hipLaunchKernelGGL(skinny_reduce_kernel, dim3(rblocks), dim3(256), 0, stream, part, static_cast<f16 *>(a.y),
-                       (int)a.M, a.N, sh.S, vec4, sh.nblocks, R, a.bias, a.bias_dtype);
+                       (int)a.M, a.N, sh.S, vec4, sh.nblocks, R, a.bias, a.bias_dtype, xb ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -123,8 +123,7 @@ def test_bf16_decode_down_proj(oracle_mod):
     """c5's down projection (K = 11008: 22-chunk quarters, paired group-128
     scales, 2 % ortho in records of more than 1024 words) in the BF16 decode
     kernel at one token; two tokens of K = 11008 exceed the staged
-    activation block (as for FP16, which then takes the split-K kernel) and
-    take the general kernel."""
+    activation block and take the split-K kernel, as FP16 does."""
     lay = {l.name: l for l in W.llama_block(case=1)}["down_proj"]
     x_np, xd = bf16_x(1, lay.K, 5401)
     for alpha in (1.0, 0.0):
@@ -134,7 +133,7 @@ def test_bf16_decode_down_proj(oracle_mod):
         agree_with_general(lay, xd, alpha, y, "bf16 down_proj M=1")
     _, xd2 = bf16_x(2, lay.K, 5402)
     _, k2 = run(lay, xd2, 1.0)
-    assert k2 == "general"
+    assert k2 == "skinny"
 
 
 def test_bf16_c5_block_takes_no_general_kernel(oracle_mod):
@@ -163,12 +162,13 @@ def test_bf16_bias_matches_the_unfused_add(M, kernel):
         assert np.array_equal(got, want)
 
 
-def test_bf16_without_a_plan_takes_the_general_kernel():
+def test_bf16_without_a_plan_takes_the_split_k_kernel(oracle_mod):
     lay = W.config_layer("c2")
     for M in (4, 8):
-        _, xd = bf16_x(M, lay.K, 5200 + M)
-        _, k = run(lay, xd, 1.0, plan=False)
-        assert k == "general"  # the BF16 decode and mid kernels read the ortho term from the plan
+        x_np, xd = bf16_x(M, lay.K, 5200 + M)
+        y, k = run(lay, xd, 1.0, plan=False)
+        assert k == "skinny"  # the BF16 decode and mid kernels read the ortho term from the plan
+        check(oracle_mod, lay, x_np, 1.0, y, f"bf16 unplanned skinny M={M}")
         _, k = run(lay, xd, 0.0, plan=False)
         assert k == ("decode" if M <= 4 else "mid")  # no ortho term: no plan needed
 
@@ -188,7 +188,7 @@ def test_prefill_bf16(oracle_mod, alpha, plan):
 def test_prefill_bf16_per_row_scales_and_bias(oracle_mod):
     from oracle import pack_oracle as PO
     lay = W.make_layer(2048, 520, None, 0.02, 410)
-    x_np, xd = bf16_x(64, 2048, 411)
+    x_np, xd = bf16_x(80, 2048, 411)  # (up to 64 tokens take the split-K kernel)
     y, k = run(lay, xd, 1.0)
     assert k == "prefill"
     check(oracle_mod, lay, x_np, 1.0, y, "bf16 prefill per-row scales")
@@ -197,3 +197,37 @@ def test_prefill_bf16_per_row_scales_and_bias(oracle_mod):
     want = PO.f32_to_bf16_bits(y.astype(np.float32) + b.float().cpu().numpy()[None, :])
     got = torch.from_numpy(yb).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("M", [2, 8, 16, 32])
+@pytest.mark.parametrize("alpha", [1.0, 0.0])
+def test_bf16_split_k_down_proj(oracle_mod, M, alpha):
+    """c5's down projection (K = 11008, group-128, 2 % ortho) with BF16
+    activations at 2..32 tokens: the split-K kernel (bf16 MFMA over q + 136,
+    FP32 partials, a BF16 reduction)."""
+    lay = {l.name: l for l in W.llama_block(case=1)}["down_proj"]
+    x_np, xd = bf16_x(M, lay.K, 5600 + M)
+    y, k = run(lay, xd, alpha)
+    assert k == "skinny"
+    check(oracle_mod, lay, x_np, alpha, y, f"bf16 skinny down_proj M={M} alpha={alpha}")
+    agree_with_general(lay, xd, alpha, y, f"bf16 skinny down_proj M={M}")
+
+
+@pytest.mark.parametrize("K,N,M", [(11008, 4096, 8), (4096, 1001, 24), (4096, 1040, 40)])
+def test_bf16_split_k_bias_matches_the_unfused_add(oracle_mod, K, N, M):
+    """The fused bias in the split-K path: the reduction's BF16 store (4
+    outputs per thread when N % 4 == 0, one otherwise) has the bits of the
+    FP32 add after the unfused call."""
+    from oracle import pack_oracle as PO
+    lay = W.make_layer(K, N, 128, 0.01, 5700 + N)
+    x_np, xd = bf16_x(M, K, 5701 + M)
+    y0, k = run(lay, xd, 1.0)
+    assert k == "skinny"
+    check(oracle_mod, lay, x_np, 1.0, y0, f"bf16 skinny K={K} N={N} M={M}")
+    for dt in (torch.bfloat16, torch.float32):
+        b = (torch.randn(N, generator=torch.Generator(device="cpu").manual_seed(6)) * 0.5).to(dt).cuda()
+        y, kb = run(lay, xd, 1.0, bias=b)
+        assert kb == "skinny"
+        want = PO.f32_to_bf16_bits(y0.astype(np.float32) + b.float().cpu().numpy()[None, :])
+        got = torch.from_numpy(y).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got, want)

@@ -521,14 +521,18 @@ def test_malformed_row_ptr_is_contained(oracle_mod):
         assert y.shape == (M, N)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_other_activation_dtypes(oracle_mod, dtype):
-    L = W.make_layer(1024, 200, 128, 0.02, seed=101)
+@pytest.mark.parametrize("dtype,K,G,kernel", [(torch.bfloat16, 1024, 128, "skinny"),
+                                               (torch.bfloat16, 1000, 40, "general"),
+                                               (torch.float32, 1024, 128, "general")])
+def test_other_activation_dtypes(oracle_mod, dtype, K, G, kernel):
+    """BF16 activations on a shape the split-K kernel takes (K % 128 == 0,
+    group 128) and on one it does not; FP32 activations on the general kernel."""
+    L = W.make_layer(K, 200, G, 0.02, seed=101)
     x = W.make_x(5, L.K, 102).astype(np.float32)
     if dtype == torch.bfloat16:
         x = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     y, k = run(L, x, 1.0, dtype=dtype)
-    assert k == "general"
+    assert k == kernel
     assert_close(y, oracle_y(oracle_mod, L, x, 1.0))
 
 
