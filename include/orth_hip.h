@@ -109,8 +109,9 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  * kernels do not take (orth_hip_last_kernel() names the choice).  BF16 I/O
  * takes the decode kernel for 1..4 tokens and the one-launch mid-batch
  * kernel for 5..16 (both K = 4096 with a plan or no ortho term), the
- * split-K mid-batch kernel for the other batches up to 64 (K % 128 == 0),
- * the prefill kernel above; FP32 I/O the general kernel.  Kernels
+ * quarter-split kernel for 17..32 (K = 4096, 256-word plan records or no
+ * ortho term), the split-K mid-batch kernel for the other batches up to 64
+ * (K % 128 == 0), the prefill kernel above; FP32 I/O the general kernel.  Kernels
  * that need scratch memory (split-K partials, a prefill plan when none is
  * given) take it from a per-stream workspace or stream-ordered allocations.
  * Replaces orth_layer_forward_cuda, /root/reference/include/ortho.h:141-144

@@ -17,7 +17,9 @@
 //    r = lane % 16, g = lane / 16) loads 16 bytes of row r per chunk
 //    (nontemporal), converts each word to 8 exact FP16 integers and feeds
 //    v_mfma_f32_16x16x32_f16 for both token tiles; each chunk's FP32 partial
-//    is multiplied by its group scale.  Loads run one block ahead (record,
+//    is multiplied by its group scale.  (BF16 activations: the exact BF16
+//    integers q + 136 into v_mfma_f32_16x16x32_bf16, less 136 times the
+//    chunk's activation sum per token, formed once at staging.)  Loads run one block ahead (record,
 //    scales, then weights, issued as the previous block's are consumed).
 //  * Ortho term (alpha > 0): the plan record of (block, quarter) is staged in
 //    the wave's own LDS region and v*x summed over its entries, 4 lanes per
@@ -63,6 +65,7 @@ struct QuarterArgs {
     int nblk;          // 16-row blocks
     int gq;            // workgroups per quarter
     int lds_xt, lds_e, lds_ex;  // byte offsets of the LDS regions (activations at 0)
+    int lds_xsum;               // BF16: [CPW chunks][MT tokens] 136 * sum of the chunk's activations
     float alpha;
     const uint32_t *rec;  // plan quarter records: qwords words per (block, quarter)
     int qwords;
@@ -70,8 +73,10 @@ struct QuarterArgs {
 
 // GMODE: 1 G = 128 (a row's 8 scales of the quarter as one aligned 16-byte
 // vector), 4 one scale per row.  SPARSE: 0 no ortho term; 3 / 4 / 5 plan
-// records of 256 / 512 / <= 1024 words.
-template <int GMODE, int SPARSE>
+// records of 256 / 512 / <= 1024 words.  XB: BF16 activations and output:
+// the weights become the exact BF16 integers q + 136, and each chunk's
+// partial loses 136 * (the chunk's activation sum), formed once at staging.
+template <int GMODE, int SPARSE, bool XB>
 __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1))) quarter_kernel(QuarterArgs a) {
     constexpr int MT = kQuMT;
     constexpr int CPW = kQuCPW;
@@ -157,6 +162,21 @@ __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1
     for (int t = 0; t < 16; t++) {
         if (th + t >= a.M) xreg[t] = u32x4{0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4 *>(xs + ((th + t) * XS + cl0)) = permute_x8(xreg[t]);
+    }
+    if constexpr (XB) {
+        // 136 * sum over the 128 columns of chunk cl0 / 128 (16 lanes of 8),
+        // per token: the bias the q + 136 weights add to every output row
+        float *xsum = reinterpret_cast<float *>(smem + a.lds_xsum);
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const uint32_t w[4] = {xreg[t].x, xreg[t].y, xreg[t].z, xreg[t].w};
+            float v = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                v += bf16_bits_to_f32((uint16_t)(w[e] & 0xffffu)) + bf16_bits_to_f32((uint16_t)(w[e] >> 16));
+            v = group_sum<16>(v);
+            if ((cg & 15) == 0) xsum[(cl0 >> 7) * MT + th + t] = 136.0f * v;
+        }
     }
     if (REC) {
 #pragma unroll
@@ -248,7 +268,7 @@ __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1
                     for (int u = 0; u < U; u++)
 #pragma unroll
                         for (int m = 0; m < MT; m++)
-                            sacc[m] = __builtin_fmaf(ve[u], (float)xh[u][m >> 3][m & 7], sacc[m]);
+                            sacc[m] = __builtin_fmaf(ve[u], x16_to_f32<XB>(xh[u][m >> 3][m & 7]), sacc[m]);
                 }
             } else {
                 int32_t fs = 0, fe = 0;
@@ -260,7 +280,7 @@ __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1
                     const f16 *xc = xt_col(ok_e ? c : 0);
                     const float ve = ok_e ? (float)a.vals[j] : 0.f;
 #pragma unroll
-                    for (int m = 0; m < MT; m++) sacc[m] = __builtin_fmaf(ve, (float)xc[m], sacc[m]);
+                    for (int m = 0; m < MT; m++) sacc[m] = __builtin_fmaf(ve, x16_to_f32<XB>(xc[m]), sacc[m]);
                 }
             }
 #pragma unroll
@@ -296,16 +316,30 @@ __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
                 uint32_t b0[4], b1[4];
-                int4x8_to_f16_interleaved(u0[kk], b0);
-                int4x8_to_f16_interleaved(u1[kk], b1);
-                const f16x8 bf0 = __builtin_bit_cast(f16x8, u32x4{b0[0], b0[1], b0[2], b0[3]});
-                const f16x8 bf1 = __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]});
+                if constexpr (XB) {
+                    int4x8_to_bf16_biased(u0[kk], b0);
+                    int4x8_to_bf16_biased(u1[kk], b1);
+                    const bf16x8 bf0 = __builtin_bit_cast(bf16x8, u32x4{b0[0], b0[1], b0[2], b0[3]});
+                    const bf16x8 bf1 = __builtin_bit_cast(bf16x8, u32x4{b1[0], b1[1], b1[2], b1[3]});
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    pa[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[t][2 * j][kk]), bf0,
-                                                                   pa[t], 0, 0, 0);
-                    pb[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[t][2 * j + 1][kk]), bf1,
-                                                                   pb[t], 0, 0, 0);
+                    for (int t = 0; t < 2; t++) {
+                        pa[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[t][2 * j][kk]),
+                                                                        bf0, pa[t], 0, 0, 0);
+                        pb[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, afr[t][2 * j + 1][kk]),
+                                                                        bf1, pb[t], 0, 0, 0);
+                    }
+                } else {
+                    int4x8_to_f16_interleaved(u0[kk], b0);
+                    int4x8_to_f16_interleaved(u1[kk], b1);
+                    const f16x8 bf0 = __builtin_bit_cast(f16x8, u32x4{b0[0], b0[1], b0[2], b0[3]});
+                    const f16x8 bf1 = __builtin_bit_cast(f16x8, u32x4{b1[0], b1[1], b1[2], b1[3]});
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        pa[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[t][2 * j][kk]),
+                                                                       bf0, pa[t], 0, 0, 0);
+                        pb[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, afr[t][2 * j + 1][kk]),
+                                                                       bf1, pb[t], 0, 0, 0);
+                    }
                 }
             }
             float s0 = 1.0f, s1 = 1.0f;
@@ -313,6 +347,20 @@ __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1
                 const uint32_t s2 = sv[j];  // the scales of chunks 2j, 2j + 1 of row nl
                 s0 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 & 0xffffu));
                 s1 = (float)__builtin_bit_cast(f16, (uint16_t)(s2 >> 16));
+            }
+            if constexpr (XB) {
+                // D[token 16 t + 4 g + k]: remove 136 * (the chunk's activation sum)
+                const float *xsum = reinterpret_cast<const float *>(smem + a.lds_xsum);
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const f32x4 ca = *reinterpret_cast<const f32x4 *>(xsum + (2 * j) * MT + 16 * t + 4 * g);
+                    const f32x4 cb = *reinterpret_cast<const f32x4 *>(xsum + (2 * j + 1) * MT + 16 * t + 4 * g);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        pa[t][k] -= ca[k];
+                        pb[t][k] -= cb[k];
+                    }
+                }
             }
 #pragma unroll
             for (int t = 0; t < 2; t++)
@@ -348,7 +396,7 @@ __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1
 // FP16 (+ bias): thread t takes 4 consecutive outputs of one token (N % 4
 // == 0; else one output), all four quarters' loads issued together.
 __global__ void __launch_bounds__(256) quarter_reduce_kernel(const float *part, f16 *y, int M, int64_t N, int vec4,
-                                                             const void *bias, int bias_dtype) {
+                                                             const void *bias, int bias_dtype, int xb) {
     const int64_t MN = (int64_t)M * N;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (vec4) {
@@ -359,15 +407,20 @@ __global__ void __launch_bounds__(256) quarter_reduce_kernel(const float *part, 
         for (int s = 0; s < 4; s++) v[s] = *reinterpret_cast<const f32x4 *>(part + s * MN + o);
         const f32x4 r = ((v[0] + v[1]) + v[2]) + v[3];
         const int64_t n = o % N;
-        const f16x2 lo = {out_f16(r[0], bias, bias_dtype, n), out_f16(r[1], bias, bias_dtype, n + 1)};
-        const f16x2 hi = {out_f16(r[2], bias, bias_dtype, n + 2), out_f16(r[3], bias, bias_dtype, n + 3)};
-        *reinterpret_cast<uint2 *>(y + o) = uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            h[e] = xb ? (uint32_t)out_bf16(r[e], bias, bias_dtype, n + e)
+                      : (uint32_t)__builtin_bit_cast(uint16_t, out_f16(r[e], bias, bias_dtype, n + e));
+        *reinterpret_cast<uint2 *>(y + o) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     } else {
         if (t >= MN) return;
         float v[4];
 #pragma unroll
         for (int s = 0; s < 4; s++) v[s] = part[s * MN + t];
-        y[t] = out_f16(((v[0] + v[1]) + v[2]) + v[3], bias, bias_dtype, t % N);
+        const float r = ((v[0] + v[1]) + v[2]) + v[3];
+        if (xb) reinterpret_cast<uint16_t *>(y)[t] = out_bf16(r, bias, bias_dtype, t % N);
+        else y[t] = out_f16(r, bias, bias_dtype, t % N);
     }
 }
 
@@ -375,11 +428,13 @@ __global__ void __launch_bounds__(256) quarter_reduce_kernel(const float *part, 
 
 struct QuarterShape {
     int gmode, sparse, lds, grid;
+    bool xb;
 };
 
 static bool quarter_shape(const ForwardArgs &a, const void *plan, QuarterArgs *d, QuarterShape &sh) {
     if (a.M < 17 || a.M > kQuMT) return false;
-    if (a.io_dtype != ORTH_DT_F16 || a.scale_dtype != ORTH_DT_F16) return false;
+    if ((a.io_dtype != ORTH_DT_F16 && a.io_dtype != ORTH_DT_BF16) || a.scale_dtype != ORTH_DT_F16) return false;
+    sh.xb = a.io_dtype == ORTH_DT_BF16;
     if (a.K != 512 * kQuCPW) return false;
     if ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.x)) & 15) return false;
     if (a.N > ((int64_t)1 << 31) || a.N < 1) return false;
@@ -394,6 +449,9 @@ static bool quarter_shape(const ForwardArgs &a, const void *plan, QuarterArgs *d
         qwords = plan_qrec_words(a.N, a.K, a.nnz);
         if (qwords <= 0 || qwords > 1024 || decode_chunks_per_wave(a.K) != kQuCPW) return false;
         sh.sparse = qwords == 256 ? 3 : qwords == 512 ? 4 : 5;
+        // BF16: 256-word records only (with 512 or more the registers of the
+        // chunk-sum correction spill; those calls take the split-K kernel)
+        if (sh.xb && sh.sparse > 3) return false;
     }
     auto al = [](int64_t v) { return (v + 15) & ~int64_t(15); };
     const int64_t cols = 128 * kQuCPW;
@@ -404,6 +462,8 @@ static bool quarter_shape(const ForwardArgs &a, const void *plan, QuarterArgs *d
     off += (int64_t)kQuW * qwords * 4;
     const int64_t lds_ex = off;
     if (sh.sparse) off += (int64_t)kQuW * 16 * kQuMT * 4;
+    const int64_t lds_xsum = off;
+    if (sh.xb) off += (int64_t)kQuCPW * kQuMT * 4;
     if (off > kQuLdsMax) return false;
     sh.lds = (int)off;
     const int64_t nblk = (a.N + 15) / 16;
@@ -427,6 +487,7 @@ static bool quarter_shape(const ForwardArgs &a, const void *plan, QuarterArgs *d
         d->lds_xt = (int)lds_xt;
         d->lds_e = (int)lds_e;
         d->lds_ex = (int)lds_ex;
+        d->lds_xsum = (int)lds_xsum;
         d->alpha = a.alpha;
         d->rec = sh.sparse ? reinterpret_cast<const uint32_t *>(static_cast<const char *>(plan) +
                                                                 plan_rec_at(a.N, a.K, a.nnz))
@@ -445,7 +506,7 @@ bool quarter_supported(const ForwardArgs &a, const void *plan) {
 // Workspace bytes of a call: the four quarters' FP32 partials.
 int64_t quarter_workspace_bytes(const ForwardArgs &a) { return 4 * a.M * a.N * 4; }
 
-template <int GMODE, int SPARSE>
+template <int GMODE, int SPARSE, bool XB>
 static hipError_t quarter_launch_t(const QuarterArgs &d, const QuarterShape &sh, hipStream_t s) {
     // more than 64 KB of dynamic LDS must be allowed once per device (the
     // attribute call is idempotent, so two threads racing to set it is harmless)
@@ -453,22 +514,24 @@ static hipError_t quarter_launch_t(const QuarterArgs &d, const QuarterShape &sh,
     int dev = 0;
     if (sh.lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 &&
         !allowed[dev].load(std::memory_order_acquire)) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(quarter_kernel<GMODE, SPARSE>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(quarter_kernel<GMODE, SPARSE, XB>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQuLdsMax);
         if (e != hipSuccess) return e;
         allowed[dev].store(1, std::memory_order_release);
     }
-    hipLaunchKernelGGL((quarter_kernel<GMODE, SPARSE>), dim3((unsigned)sh.grid), dim3(kQuNT), (uint32_t)sh.lds, s, d);
+    hipLaunchKernelGGL((quarter_kernel<GMODE, SPARSE, XB>), dim3((unsigned)sh.grid), dim3(kQuNT), (uint32_t)sh.lds, s, d);
     return hipGetLastError();
 }
 
-template <int GMODE>
+template <int GMODE, bool XB>
 static hipError_t quarter_launch_s(const QuarterArgs &d, const QuarterShape &sh, hipStream_t s) {
     switch (sh.sparse) {
-        case 3: return quarter_launch_t<GMODE, 3>(d, sh, s);
-        case 4: return quarter_launch_t<GMODE, 4>(d, sh, s);
-        case 5: return quarter_launch_t<GMODE, 5>(d, sh, s);
-        default: return quarter_launch_t<GMODE, 0>(d, sh, s);
+        case 3: return quarter_launch_t<GMODE, 3, XB>(d, sh, s);
+        case 4:
+        case 5:
+            if constexpr (XB) return hipErrorInvalidValue;  // excluded by quarter_shape
+            else return sh.sparse == 4 ? quarter_launch_t<GMODE, 4, XB>(d, sh, s) : quarter_launch_t<GMODE, 5, XB>(d, sh, s);
+        default: return quarter_launch_t<GMODE, 0, XB>(d, sh, s);
     }
 }
 
@@ -479,12 +542,13 @@ hipError_t launch_quarter(const ForwardArgs &a, const void *plan, float *part, h
     QuarterShape sh;
     if (!quarter_shape(a, plan, &d, sh) || !part) return hipErrorInvalidValue;
     d.part = part;
-    hipError_t e = sh.gmode == 1 ? quarter_launch_s<1>(d, sh, stream) : quarter_launch_s<4>(d, sh, stream);
+    hipError_t e = sh.xb ? (sh.gmode == 1 ? quarter_launch_s<1, true>(d, sh, stream) : quarter_launch_s<4, true>(d, sh, stream))
+                         : (sh.gmode == 1 ? quarter_launch_s<1, false>(d, sh, stream) : quarter_launch_s<4, false>(d, sh, stream));
     if (e != hipSuccess) return e;
     const int vec4 = a.N % 4 == 0 ? 1 : 0;
     const int64_t threads = vec4 ? a.M * a.N / 4 : a.M * a.N;
     hipLaunchKernelGGL(quarter_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, part,
-                       static_cast<f16 *>(a.y), (int)a.M, a.N, vec4, a.bias, a.bias_dtype);
+                       static_cast<f16 *>(a.y), (int)a.M, a.N, vec4, a.bias, a.bias_dtype, sh.xb ? 1 : 0);
     return hipGetLastError();
 }
 

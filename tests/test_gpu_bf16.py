@@ -213,7 +213,7 @@ def test_bf16_split_k_down_proj(oracle_mod, M, alpha):
     agree_with_general(lay, xd, alpha, y, f"bf16 skinny down_proj M={M}")
 
 
-@pytest.mark.parametrize("K,N,M", [(11008, 4096, 8), (4096, 1001, 24), (4096, 1040, 40)])
+@pytest.mark.parametrize("K,N,M", [(11008, 4096, 8), (11008, 1001, 24), (4096, 1040, 40)])
 def test_bf16_split_k_bias_matches_the_unfused_add(oracle_mod, K, N, M):
     """The fused bias in the split-K path: the reduction's BF16 store (4
     outputs per thread when N % 4 == 0, one otherwise) has the bits of the
@@ -231,3 +231,46 @@ def test_bf16_split_k_bias_matches_the_unfused_add(oracle_mod, K, N, M):
         want = PO.f32_to_bf16_bits(y0.astype(np.float32) + b.float().cpu().numpy()[None, :])
         got = torch.from_numpy(y).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
         assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("M", [17, 24, 32])
+@pytest.mark.parametrize("alpha", [1.0, 0.0])
+def test_bf16_quarter_c2(oracle_mod, M, alpha):
+    """17..32 BF16 tokens at K = 4096 with 256-word plan records: the
+    quarter-split kernel (q + 136 weights, 136 * sum(x) per chunk and token
+    formed once at staging, BF16 stores in the reduction)."""
+    lay = W.config_layer("c2")
+    x_np, xd = bf16_x(M, lay.K, 5800 + M)
+    y, k = run(lay, xd, alpha)
+    assert k == "quarter"
+    check(oracle_mod, lay, x_np, alpha, y, f"bf16 quarter c2 M={M} alpha={alpha}")
+    agree_with_general(lay, xd, alpha, y, f"bf16 quarter c2 M={M}")
+
+
+@pytest.mark.parametrize("N,group,M", [(1040, 128, 24), (1001, 128, 20), (520, None, 17)])
+def test_bf16_quarter_shapes_and_bias(oracle_mod, N, group, M):
+    """Ragged N (the reduction's one-output path when N % 4 != 0), per-row
+    scales, and the fused BF16 / FP32 bias with the bits of the unfused add."""
+    from oracle import pack_oracle as PO
+    lay = W.make_layer(4096, N, group, 0.01, 5900 + N)
+    x_np, xd = bf16_x(M, 4096, 5901 + M)
+    y0, k = run(lay, xd, 1.0)
+    assert k == "quarter"
+    check(oracle_mod, lay, x_np, 1.0, y0, f"bf16 quarter N={N} G={group} M={M}")
+    for dt in (torch.bfloat16, torch.float32):
+        b = (torch.randn(N, generator=torch.Generator(device="cpu").manual_seed(7)) * 0.5).to(dt).cuda()
+        y, kb = run(lay, xd, 1.0, bias=b)
+        assert kb == "quarter"
+        want = PO.f32_to_bf16_bits(y0.astype(np.float32) + b.float().cpu().numpy()[None, :])
+        got = torch.from_numpy(y).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got, want)
+
+
+def test_bf16_quarter_leaves_larger_records_to_split_k(oracle_mod):
+    """c5's q_proj (2 % ortho: 512-word records) at 32 BF16 tokens takes the
+    split-K kernel (the quarter kernel takes BF16 with 256-word records only)."""
+    lay = {l.name: l for l in W.llama_block(case=1)}["q_proj"]
+    x_np, xd = bf16_x(32, lay.K, 6000)
+    y, k = run(lay, xd, 1.0)
+    assert k == "skinny"
+    check(oracle_mod, lay, x_np, 1.0, y, "bf16 c5 q_proj M=32")
