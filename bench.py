@@ -777,10 +777,11 @@ def main():
             log(f"  {secondary[-1]}")
         # BF16 activations and output: the same weights and the same
         # algorithmic bytes (2 per activation and output element either way)
-        for m in (1, 8):
-            rr = time_workload(torch, layer, m, alpha, SECONDARY_STEPS, 10, plan=True, dtype=torch.bfloat16)
-            b = W.algorithmic_bytes(layer, m, alpha)
-            secondary.append({"workload": f"c2 M={m} alpha={alpha}, BF16 activations", "kernel": rr["kernel"],
+        down = {l.name: l for l in W.llama_block()}["down_proj"]
+        for lay, m, label in ((layer, 1, "c2"), (layer, 8, "c2"), (layer, 32, "c2"), (down, 8, "c5 down_proj")):
+            rr = time_workload(torch, lay, m, alpha, SECONDARY_STEPS, 10, plan=True, dtype=torch.bfloat16)
+            b = W.algorithmic_bytes(lay, m, alpha)
+            secondary.append({"workload": f"{label} M={m} alpha={alpha}, BF16 activations", "kernel": rr["kernel"],
                               "us_per_step": round(rr["ms_per_step"] * 1e3, 3),
                               "GB/s": round(b / (rr["ms_per_step"] * 1e-3) / 1e9, 1),
                               "frac_hbm": round(b / (rr["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
