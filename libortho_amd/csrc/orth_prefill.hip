@@ -473,19 +473,13 @@ __device__ __forceinline__ uint32_t dq_byte(uint32_t w, f16x2 s2, int i) {
     return __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p) + bias) * s2);
 }
 
-// The same pair for BF16 activations: q is exact in FP32 (the nibble under
-// 2^23 = 0x4B000000, minus 2^23 + 8), q*s is exact in FP32 (a 4-bit times
-// an 11-bit significand), and one rounding (nearest even) gives the BF16
-// weight.
+// Two FP32 values rounded (nearest even) to BF16 and packed, lo first.  For
+// BF16 activations the staged weights are bf16(q * s) with q * s exact in
+// FP32 (a 4-bit times an 11-bit significand): one rounding (pf_store_b).
 __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
-}
-
-__device__ __forceinline__ uint32_t dq_byte_bf16(uint32_t w, float s, int i) {
-    const uint32_t b = w >> (8 * i);
-    const float q0 = __uint_as_float(((b & 0xFu) ^ 8u) | 0x4B000000u) - 8388616.0f;
-    const float q1 = __uint_as_float((((b >> 4) & 0xFu) ^ 8u) | 0x4B000000u) - 8388616.0f;
-    return pk_bf16(q0 * s, q1 * s);
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));  // one v_cvt_pk_bf16_f32
 }
 
 template <bool XB>
@@ -498,10 +492,19 @@ __device__ __forceinline__ void pf_store_b(const PfB &r, f16 *Bs) {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         u32x4 o;
-        if constexpr (XB)
-            o = u32x4{dq_byte_bf16(words[j], sf, 0), dq_byte_bf16(words[j], sf, 1), dq_byte_bf16(words[j], sf, 2),
-                      dq_byte_bf16(words[j], sf, 3)};
-        else
+        if constexpr (XB) {
+            // the word's even-k nibbles (lo) and odd-k nibbles (hi) as bytes
+            // u = q + 8; q * s = fma(u, s, -8 s) exactly (-8 s is exact, and
+            // q * s fits in the FP32 significand), then one rounding to BF16
+            const uint32_t lo = (words[j] & 0x0F0F0F0Fu) ^ 0x08080808u;
+            const uint32_t hi = ((words[j] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+            const float s8 = -8.0f * sf;
+            auto pair = [&](int i) {
+                return pk_bf16(__builtin_fmaf((float)((lo >> (8 * i)) & 0xFFu), sf, s8),
+                               __builtin_fmaf((float)((hi >> (8 * i)) & 0xFFu), sf, s8));
+            };
+            o = u32x4{pair(0), pair(1), pair(2), pair(3)};
+        } else
             o = u32x4{dq_byte(words[j], s2, 0), dq_byte(words[j], s2, 1), dq_byte(words[j], s2, 2),
                       dq_byte(words[j], s2, 3)};
         *reinterpret_cast<u32x4 *>(Bs + pf_swz(row, c0 + j)) = o;
