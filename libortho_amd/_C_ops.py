@@ -157,23 +157,33 @@ class _PlanCache:
     An entry holds weak references to its five tensors and is valid only
     while the same tensor objects are alive with unchanged versions, data
     pointers and shapes (an in-place write bumps ``_version``; a freed tensor
-    drops its entries).  Bounded, least recently used first out.  A plan
+    drops its entries).  Bounded by MAX entries and MAX_BYTES of plans (a
+    model's every layer fits: a plan is ~12 % of its INT4 weights), least
+    recently used first out.  A plan
     built on one stream is used on another only after that stream has waited
     on the build, and its memory is recorded on that stream, so freeing it
     waits for the stream's work.  Under graph capture no plan is handed out
     (a graph would keep the pointer of a plan this cache may free): captured
     calls read the CSR as the reference's operator does."""
 
-    MAX = 64
+    MAX = 4096
+    MAX_BYTES = 8 << 30
 
     def __init__(self):
         self._d = collections.OrderedDict()
+        self._bytes = 0
 
     def __len__(self):
         return len(self._d)
 
     def clear(self):
         self._d.clear()
+        self._bytes = 0
+
+    def _drop(self, key):
+        e = self._d.pop(key, None)
+        if e is not None:
+            self._bytes -= e["plan"].numel()
 
     @staticmethod
     def _sig(ts):
@@ -204,7 +214,7 @@ class _PlanCache:
                     e["plan"].record_stream(st)
                     e["streams"].add(cur)
                 return e["plan"]
-            del self._d[key]
+            self._drop(key)
         if not all(isinstance(t, torch.Tensor) and t.is_cuda and t.get_device() == dev for t in ts):
             return None  # forward_planned raises the reason
         try:
@@ -215,14 +225,17 @@ class _PlanCache:
             return None
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(dev))
-        d = self._d
+        owner = weakref.ref(self)
 
-        def drop(_r, key=key, d=d):
-            d.pop(key, None)
+        def drop(_r, key=key, owner=owner):
+            c = owner()
+            if c is not None:
+                c._drop(key)
         self._d[key] = {"refs": tuple(weakref.ref(t, drop) for t in ts), "sig": self._sig(ts), "plan": plan,
                         "event": ev, "streams": {_raw_stream(dev)}}
-        while len(self._d) > self.MAX:
-            self._d.popitem(last=False)
+        self._bytes += plan.numel()
+        while len(self._d) > 1 and (len(self._d) > self.MAX or self._bytes > self.MAX_BYTES):
+            self._drop(next(iter(self._d)))
         return plan
 
 

@@ -198,3 +198,26 @@ def test_ortholinear_plan_used_on_another_stream_and_by_a_copy():
     torch.cuda.synchronize()
     for y in (first, got, got2):
         assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+
+
+def test_bounds_evict_the_least_recently_used_plans(monkeypatch):
+    """At most MAX entries and MAX_BYTES of plans (here shrunk to 2 entries,
+    then to one plan's bytes); the byte count follows every drop."""
+    sets = [W.to_device(W.make_layer(4096, 520, 128, 0.02, 6900 + i)) for i in range(3)]
+    x = torch.from_numpy(W.make_x(1, 4096, 6910)).cuda()
+    monkeypatch.setattr(_C_ops._PlanCache, "MAX", 2)
+    for d in sets:
+        ref_forward(d, x, 1.0)
+    assert len(_C_ops._PLANS) == 2
+    plans = [e["plan"] for e in _C_ops._PLANS._d.values()]
+    assert _C_ops._PLANS._bytes == sum(p.numel() for p in plans)
+    ref_forward(sets[1], x, 1.0)  # most recent: sets 2, 1
+    ref_forward(sets[0], x, 1.0)  # rebuilt; evicts set 2
+    keys = [k[2] for k in _C_ops._PLANS._d]
+    assert keys == [id(sets[1]["vals"]), id(sets[0]["vals"])]
+    monkeypatch.setattr(_C_ops._PlanCache, "MAX_BYTES", plans[0].numel())
+    ref_forward(sets[2], x, 1.0)  # over the byte bound: only the newest stays
+    assert len(_C_ops._PLANS) == 1 and [k[2] for k in _C_ops._PLANS._d] == [id(sets[2]["vals"])]
+    del sets, d  # (the loop variable holds the last set too)
+    gc.collect()
+    assert len(_C_ops._PLANS) == 0 and _C_ops._PLANS._bytes == 0
