@@ -376,13 +376,21 @@ __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1
         // ---- this quarter's partials: lane (row nl, tokens 16 t + 4 g + k)
         const int64_t n = n0 + nl;
         if (i < nit && nl <= last_row) {
+            // the lane's 8 sparse sums as two vector reads ahead of the stores
+            // (read inside each store's token test, they took one LDS round
+            // trip per store)
+            f32x4 es[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+            if (REC) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) es[t] = *reinterpret_cast<const f32x4 *>(ex + nl * MT + 16 * t + 4 * g);
+            }
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const int m = 16 * t + 4 * g + k;
                     float v = acc[t][k] * srow;
-                    if (REC) v += a.alpha * ex[nl * MT + m];
+                    if (REC) v += a.alpha * es[t][k];
                     if (m < a.M) a.part[((int64_t)qq * a.M + m) * a.N + n] = v;
                 }
         }
