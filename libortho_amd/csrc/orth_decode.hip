@@ -1,4 +1,5 @@
-// Decode dual GEMM (batch M <= 16) for gfx950.
+// Decode dual GEMM for gfx950: up to 16 tokens; the dispatcher gives it 1..4
+// (and up to 8 where no mid-batch kernel applies).
 //
 // Computes what /root/reference/src/dual_gemm.cu:176-225 computes (the
 // reference launches one 32-thread block per 32 output rows and walks K

@@ -1,4 +1,5 @@
-// Prefill dual GEMM (batch M > 16) for gfx950, and the ortho plan builder.
+// Prefill dual GEMM for gfx950 (batches above 64 tokens, and 17..64 where
+// the mid-batch kernels do not apply), and the ortho plan builder.
 //
 // Design intent of /root/reference/src/dual_gemm_tensor_core.cu:215-337
 // (matrix-core base GEMM with the ortho term fused), built for CDNA4:
