@@ -376,23 +376,22 @@ __global__ void __launch_bounds__(kQuNT) __attribute__((amdgpu_waves_per_eu(1, 1
         // ---- this quarter's partials: lane (row nl, tokens 16 t + 4 g + k)
         const int64_t n = n0 + nl;
         if (i < nit && nl <= last_row) {
-            // the lane's 8 sparse sums as two vector reads ahead of the stores
-            // (read inside each store's token test, they took one LDS round
-            // trip per store)
-            f32x4 es[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-            if (REC) {
 #pragma unroll
-                for (int t = 0; t < 2; t++) es[t] = *reinterpret_cast<const f32x4 *>(ex + nl * MT + 16 * t + 4 * g);
-            }
-#pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int t = 0; t < 2; t++) {
+                // FP16: the tile's 4 sparse sums as one vector read ahead of
+                // its stores (read inside each store's token test, they took
+                // one LDS round trip per store); BF16 reads them per store
+                // (the vector spills registers there)
+                f32x4 es = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (REC && !XB) es = *reinterpret_cast<const f32x4 *>(ex + nl * MT + 16 * t + 4 * g);
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const int m = 16 * t + 4 * g + k;
                     float v = acc[t][k] * srow;
-                    if (REC) v += a.alpha * es[t][k];
+                    if (REC) v += a.alpha * (XB ? ex[nl * MT + m] : es[k]);
                     if (m < a.M) a.part[((int64_t)qq * a.M + m) * a.N + n] = v;
                 }
+            }
         }
     };
     const int its = nit > 0 ? nit : 1;
