@@ -152,10 +152,11 @@ __global__ void __launch_bounds__(256) general_kernel(ForwardArgs a) {
 template <int IO>
 static hipError_t launch_general_io(const ForwardArgs &a, hipStream_t stream) {
     // (tiles of 8 tokens, or the word loop unrolled 4 deep, measured slower)
-    const int64_t mt = a.M == 1 ? 1 : 4;
+    const int64_t mt = a.M <= 1 ? 1 : a.M == 2 ? 2 : 4;
     const int64_t tiles = (a.M + mt - 1) / mt;
     const dim3 grid((unsigned)((a.N + 3) / 4), (unsigned)(tiles < 65535 ? tiles : 65535));
     if (mt == 1) hipLaunchKernelGGL((general_kernel<IO, 1>), grid, dim3(256), 0, stream, a);
+    else if (mt == 2) hipLaunchKernelGGL((general_kernel<IO, 2>), grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((general_kernel<IO, 4>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }

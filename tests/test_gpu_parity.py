@@ -536,6 +536,20 @@ def test_other_activation_dtypes(oracle_mod, dtype, K, G, kernel):
     assert_close(y, oracle_y(oracle_mod, L, x, 1.0))
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6])
+@pytest.mark.parametrize("dtype,K,G", [(torch.float32, 1024, 128), (torch.bfloat16, 1000, 40)])
+def test_general_kernel_token_tiles(oracle_mod, dtype, K, G, M):
+    """The general kernel's tiles of 1, 2 and 4 tokens, with a ragged last
+    tile at 3 and 6 tokens."""
+    L = W.make_layer(K, 136, G, 0.02, seed=105 + M)
+    x = W.make_x(M, L.K, 106 + M).astype(np.float32)
+    if dtype == torch.bfloat16:
+        x = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    y, k = run(L, x, 1.0, dtype=dtype)
+    assert k == "general"
+    assert_close(y, oracle_y(oracle_mod, L, x, 1.0), what=f"general {dtype} M={M}")
+
+
 def test_fp32_scales_and_values(oracle_mod):
     L = W.make_layer(1024, 200, 128, 0.02, seed=103)
     x = W.make_x(3, L.K, 104)
