@@ -247,13 +247,17 @@ int orth_pack_csr_fill_hip(const void *w, int32_t w_dtype, int64_t out_features,
  * packing; all pointers device memory, calls asynchronous on `stream`).
  * Each replaces torch ops of /root/reference/tools/sieve.py with the same
  * arithmetic on a GPU tensor (every intermediate rounded to the dtype the
- * torch op returns).
+ * torch op returns).  `flags`: 0, or ORTH_SIEVE_IEEE_DIV to divide by the
+ * host scalars (7 and the row count) as torch does on a CPU tensor (IEEE
+ * division) instead of as on a GPU tensor (a product with the FP32
+ * reciprocal); any other bit is an error.
  *
  * orth_sieve_quantize_hip: w_base [out_features, in_features] (w's dtype) =
  * quantize_int4(w), /root/reference/tools/sieve.py:13-23: per-row scale
  * clamp(max|w|, 1e-8) / 7, clamp(round(w / s), -8, 7) * s, non-finite -> 0. */
+#define ORTH_SIEVE_IEEE_DIV 1
 int orth_sieve_quantize_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
-                            void *w_base, void *stream);
+                            void *w_base, int32_t flags, void *stream);
 
 /* orth_sieve_split_hip: hessian_sieve, /root/reference/tools/sieve.py:25-76.
  * Writes w_base as above and w_ortho = residual * (score > t) (w's dtype),
@@ -268,7 +272,7 @@ int64_t orth_sieve_select_bytes(void);
 int orth_sieve_split_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
                          const void *h_inv, int32_t h_dtype, int64_t h_stride, int32_t score_dtype,
                          int32_t use_rank, int64_t rank, float threshold, void *w_base, void *w_ortho,
-                         float *score, void *select_state, void *stream);
+                         float *score, void *select_state, int32_t flags, void *stream);
 
 /* orth_sieve_hdiag_hip: out [in_features] (x's dtype) = diag(x^T x) / rows +
  * 1e-6 for x [rows, in_features], /root/reference/tools/sieve.py:79-95 (the
@@ -277,7 +281,7 @@ int orth_sieve_split_hip(const void *w, int32_t w_dtype, int64_t out_features, i
  * orth_sieve_hdiag_workspace(rows, in_features) elements. */
 int64_t orth_sieve_hdiag_workspace(int64_t rows, int64_t in_features);
 int orth_sieve_hdiag_hip(const void *x, int32_t x_dtype, int64_t rows, int64_t in_features, float *workspace,
-                         int64_t workspace_floats, void *out, void *stream);
+                         int64_t workspace_floats, void *out, int32_t flags, void *stream);
 
 /* Device facts.  Replaces check_tensor_core_support,
  * /root/reference/src/dual_gemm_tensor_core.cu:342-350. */

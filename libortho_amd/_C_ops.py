@@ -457,9 +457,19 @@ def pack_csr(ortho_weight: torch.Tensor, values_dtype=None, use_mask: bool = Tru
     return row_ptr, col, vals
 
 
-def sieve_quantize(weight: torch.Tensor) -> torch.Tensor:
+SIEVE_IEEE_DIV = 1  # ORTH_SIEVE_IEEE_DIV: divide by host scalars as torch does on a CPU tensor
+
+
+def _sieve_flags(ieee_div: bool) -> int:
+    return SIEVE_IEEE_DIV if ieee_div else 0
+
+
+def sieve_quantize(weight: torch.Tensor, ieee_div: bool = False) -> torch.Tensor:
     """quantize_int4 (/root/reference/tools/sieve.py:13-23) of a 2-D GPU
-    tensor with the library's kernel: same dtype and shape as ``weight``."""
+    tensor with the library's kernel: same dtype and shape as ``weight``.
+    ``ieee_div`` divides by the host scalar 7 as torch does on a CPU tensor
+    (IEEE division) rather than as on a GPU tensor (a product with the FP32
+    reciprocal)."""
     _req(weight.is_cuda and weight.dim() == 2 and weight.dtype in _DT,
          "sieve_quantize needs a 2-D float16, bfloat16 or float32 tensor on a ROCm GPU")
     w = weight.contiguous()
@@ -468,14 +478,15 @@ def sieve_quantize(weight: torch.Tensor) -> torch.Tensor:
         return out
     with torch.cuda.device(w.device):
         _lib.check(_lib.lib().orth_sieve_quantize_hip(_ptr(w), _DT[w.dtype], int(w.shape[0]), int(w.shape[1]),
-                                                      _ptr(out), _stream(w.device)))
+                                                      _ptr(out), _sieve_flags(ieee_div), _stream(w.device)))
     return out
 
 
 def sieve_split(weight: torch.Tensor, H_inv: torch.Tensor, curvature_thresh: float = 10.0,
-                sparsity_target=None):
+                sparsity_target=None, ieee_div: bool = False):
     """hessian_sieve (/root/reference/tools/sieve.py:25-76) with the
-    library's kernels: (w_base, w_ortho), both of ``weight``'s dtype."""
+    library's kernels: (w_base, w_ortho), both of ``weight``'s dtype
+    (``ieee_div`` as in :func:`sieve_quantize`)."""
     _req(weight.is_cuda and weight.dim() == 2 and weight.dtype in _DT,
          "sieve_split needs a 2-D float16, bfloat16 or float32 weight on a ROCm GPU")
     _req(H_inv.device == weight.device and H_inv.dtype in _DT and H_inv.dim() in (1, 2),
@@ -502,13 +513,15 @@ def sieve_split(weight: torch.Tensor, H_inv: torch.Tensor, curvature_thresh: flo
         _lib.check(L.orth_sieve_split_hip(_ptr(w), _DT[w.dtype], N, K, ctypes.c_void_p(h.data_ptr()), _DT[h.dtype],
                                           h_stride, _DT[score_dt], 1 if use_rank else 0, rank,
                                           float(curvature_thresh) if not use_rank else 0.0, _ptr(w_base),
-                                          _ptr(w_ortho), _ptr(score), _ptr(sel), _stream(w.device)))
+                                          _ptr(w_ortho), _ptr(score), _ptr(sel), _sieve_flags(ieee_div),
+                                          _stream(w.device)))
     return w_base, w_ortho
 
 
-def sieve_hdiag(inputs: torch.Tensor) -> torch.Tensor:
+def sieve_hdiag(inputs: torch.Tensor, ieee_div: bool = False) -> torch.Tensor:
     """compute_hessian_diag_approx (/root/reference/tools/sieve.py:79-95),
-    diag(X^T X) / n + 1e-6, of a 2-D GPU tensor with the library's kernels."""
+    diag(X^T X) / n + 1e-6, of a 2-D GPU tensor with the library's kernels
+    (``ieee_div``: the division by n as on a CPU tensor)."""
     _req(inputs.is_cuda and inputs.dim() == 2 and inputs.dtype in _DT,
          "sieve_hdiag needs a 2-D float16, bfloat16 or float32 tensor on a ROCm GPU")
     x = inputs.contiguous()
@@ -519,7 +532,8 @@ def sieve_hdiag(inputs: torch.Tensor) -> torch.Tensor:
     ws = torch.empty(ws_n, dtype=torch.float32, device=x.device)
     out = torch.empty(K, dtype=x.dtype, device=x.device)
     with torch.cuda.device(x.device):
-        _lib.check(L.orth_sieve_hdiag_hip(_ptr(x), _DT[x.dtype], n, K, _ptr(ws), ws_n, _ptr(out), _stream(x.device)))
+        _lib.check(L.orth_sieve_hdiag_hip(_ptr(x), _DT[x.dtype], n, K, _ptr(ws), ws_n, _ptr(out),
+                                          _sieve_flags(ieee_div), _stream(x.device)))
     return out
 
 

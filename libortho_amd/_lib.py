@@ -71,12 +71,12 @@ SIGNATURES = {
     "orth_pack_csr_mask_bytes": (_I64, [_P, _I32, _I64, _I64]),
     "orth_pack_csr_rows_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _I64, _P]),
     "orth_pack_csr_fill_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P, _I64, _P, _P, _I32, _P]),
-    "orth_sieve_quantize_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _P]),
+    "orth_sieve_quantize_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _P]),
     "orth_sieve_select_bytes": (_I64, []),
     "orth_sieve_split_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _I64, _I32, _I32, _I64, _F32,
-                                            _P, _P, _P, _P, _P]),
+                                            _P, _P, _P, _P, _I32, _P]),
     "orth_sieve_hdiag_workspace": (_I64, [_I64, _I64]),
-    "orth_sieve_hdiag_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I64, _P, _P]),
+    "orth_sieve_hdiag_hip": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I64, _P, _I32, _P]),
     "orth_hip_device_info": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(OrthHipDeviceInfo)]),
     "orth_hip_set_kernel_policy": (ctypes.c_int, [ctypes.c_int]),
     "orth_hip_get_kernel_policy": (ctypes.c_int, []),

@@ -55,12 +55,13 @@ hipError_t launch_mid(const ForwardArgs &a, const void *plan, int cus, hipStream
 bool skinny_supported(const ForwardArgs &a);
 int64_t skinny_workspace_bytes(const ForwardArgs &a, int cus);
 hipError_t launch_skinny(const ForwardArgs &a, const void *plan, int cus, float *part, hipStream_t stream);
-hipError_t launch_sieve_quantize(const void *w, int dt, int64_t N, int64_t K, void *w_base, hipStream_t stream);
+hipError_t launch_sieve_quantize(const void *w, int dt, int64_t N, int64_t K, void *w_base, int ieee_div,
+                                 hipStream_t stream);
 hipError_t launch_sieve_split(const void *w, int dt, int64_t N, int64_t K, const void *h, int hdt, int64_t h_stride,
                               int score_dt, int use_rank, int64_t rank, float thresh, void *w_base, void *w_ortho,
-                              float *score, void *sel, hipStream_t stream);
+                              float *score, void *sel, int ieee_div, hipStream_t stream);
 int64_t sieve_hdiag_slices(int64_t n);
-hipError_t launch_sieve_hdiag(const void *x, int dt, int64_t n, int64_t K, float *partial, void *out,
+hipError_t launch_sieve_hdiag(const void *x, int dt, int64_t n, int64_t K, float *partial, void *out, int ieee_div,
                               hipStream_t stream);
 }  // namespace orth
 
@@ -672,15 +673,23 @@ int orth_pack_csr_fill_hip(const void *w, int32_t w_dtype, int64_t out_features,
     return ORTH_OK;
 }
 
+static int check_sieve_flags(int32_t flags) {
+    if (flags & ~ORTH_SIEVE_IEEE_DIV) return fail(ORTH_ERR_INVALID_ARGUMENT, "unknown sieve flags 0x%x", flags);
+    return ORTH_OK;
+}
+
 int orth_sieve_quantize_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
-                            void *w_base, void *stream) {
+                            void *w_base, int32_t flags, void *stream) {
     int rc = check_pack_dims(w, w_dtype, out_features, in_features);
+    if (rc != ORTH_OK) return rc;
+    rc = check_sieve_flags(flags);
     if (rc != ORTH_OK) return rc;
     if (!w_base) return fail(ORTH_ERR_INVALID_ARGUMENT, "w_base is NULL");
     if (out_features > INT32_MAX) return fail(ORTH_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
     rc = current_device_ok(nullptr);
     if (rc != ORTH_OK) return rc;
-    hipError_t e = launch_sieve_quantize(w, w_dtype, out_features, in_features, w_base, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_sieve_quantize(w, w_dtype, out_features, in_features, w_base,
+                                         (flags & ORTH_SIEVE_IEEE_DIV) ? 1 : 0, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail_hip(e, "sieve quantize launch");
     return ORTH_OK;
 }
@@ -690,8 +699,10 @@ int64_t orth_sieve_select_bytes(void) { return 1040; }
 int orth_sieve_split_hip(const void *w, int32_t w_dtype, int64_t out_features, int64_t in_features,
                          const void *h_inv, int32_t h_dtype, int64_t h_stride, int32_t score_dtype,
                          int32_t use_rank, int64_t rank, float threshold, void *w_base, void *w_ortho,
-                         float *score, void *select_state, void *stream) {
+                         float *score, void *select_state, int32_t flags, void *stream) {
     int rc = check_pack_dims(w, w_dtype, out_features, in_features);
+    if (rc != ORTH_OK) return rc;
+    rc = check_sieve_flags(flags);
     if (rc != ORTH_OK) return rc;
     if (!h_inv || !valid_dtype(h_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "h_inv is NULL or of a bad dtype");
     if (!valid_dtype(score_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "score dtype %d is not F16, BF16 or F32", score_dtype);
@@ -707,7 +718,7 @@ int orth_sieve_split_hip(const void *w, int32_t w_dtype, int64_t out_features, i
     if (rc != ORTH_OK) return rc;
     hipError_t e = launch_sieve_split(w, w_dtype, out_features, in_features, h_inv, h_dtype, h_stride, score_dtype,
                                       use_rank, rank, threshold, w_base, w_ortho, score, select_state,
-                                      static_cast<hipStream_t>(stream));
+                                      (flags & ORTH_SIEVE_IEEE_DIV) ? 1 : 0, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail_hip(e, "sieve split launch");
     return ORTH_OK;
 }
@@ -718,8 +729,9 @@ int64_t orth_sieve_hdiag_workspace(int64_t rows, int64_t in_features) {
 }
 
 int orth_sieve_hdiag_hip(const void *x, int32_t x_dtype, int64_t rows, int64_t in_features, float *workspace,
-                         int64_t workspace_floats, void *out, void *stream) {
+                         int64_t workspace_floats, void *out, int32_t flags, void *stream) {
     if (!x || !out || !workspace) return fail(ORTH_ERR_INVALID_ARGUMENT, "x, out or workspace is NULL");
+    if (check_sieve_flags(flags) != ORTH_OK) return ORTH_ERR_INVALID_ARGUMENT;
     if (!valid_dtype(x_dtype)) return fail(ORTH_ERR_INVALID_ARGUMENT, "x dtype %d is not F16, BF16 or F32", x_dtype);
     if (rows <= 0 || in_features <= 0) return fail(ORTH_ERR_INVALID_ARGUMENT, "rows and in_features must be positive");
     if (workspace_floats < sieve_hdiag_slices(rows) * in_features)
@@ -728,7 +740,8 @@ int orth_sieve_hdiag_hip(const void *x, int32_t x_dtype, int64_t rows, int64_t i
     if (in_features > ((int64_t)1 << 40) / rows) return fail(ORTH_ERR_INVALID_ARGUMENT, "x is too large");
     int rc = current_device_ok(nullptr);
     if (rc != ORTH_OK) return rc;
-    hipError_t e = launch_sieve_hdiag(x, x_dtype, rows, in_features, workspace, out, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_sieve_hdiag(x, x_dtype, rows, in_features, workspace, out,
+                                      (flags & ORTH_SIEVE_IEEE_DIV) ? 1 : 0, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail_hip(e, "hessian diagonal launch");
     return ORTH_OK;
 }
@@ -769,6 +782,6 @@ int orth_hip_last_kernel(void) { return t_last_kernel; }
 
 const char *orth_hip_last_error(void) { return t_error.c_str(); }
 
-int orth_hip_abi_version(void) { return 102; }
+int orth_hip_abi_version(void) { return 103; }
 
 }  // extern "C"

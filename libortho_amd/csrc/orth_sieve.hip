@@ -4,8 +4,9 @@
 //
 //  quantize_int4 (:13-23)   one workgroup per row: max|w| (NaN propagates),
 //                            clamp at 1e-8 in w's dtype, s = max * fp32(1/7)
-//                            (torch divides by a host scalar through its
-//                            reciprocal), q = clamp(rint(w / s), -8, 7),
+//                            (torch divides a GPU tensor by a host scalar
+//                            through its reciprocal; a CPU tensor by IEEE
+//                            division, the ieee_div mode), q = clamp(rint(w / s), -8, 7),
 //                            w_base = q * s, non-finite results 0.  Every
 //                            intermediate is rounded to w's dtype, as the
 //                            torch ops round each result.
@@ -57,7 +58,14 @@ struct SieveArgs {
     int hdt;
     int64_t h_stride;
     int score_dt;       // dtype of the score (torch's promotion of w's and H's)
+    int ieee_div;       // 1: division by a host scalar as IEEE division (CPU
+                        // tensors), 0: as a product with its FP32 reciprocal
 };
+
+// v / d for a host scalar d, as torch computes it on the tensor's device.
+__device__ __forceinline__ float sieve_scalar_div(float v, float d, int ieee_div) {
+    return ieee_div ? v / d : v * (1.0f / d);
+}
 
 __global__ void __launch_bounds__(kSieveNT) sieve_quant_kernel(SieveArgs a) {
     __shared__ float red[kSieveNT / 64];
@@ -76,7 +84,7 @@ __global__ void __launch_bounds__(kSieveNT) sieve_quant_kernel(SieveArgs a) {
     // clamp(min=1e-8): the bound in w's dtype (0 in FP16), NaN kept
     const float lo = round_as(a.dt, 1e-8f);
     const float mc = (m != m) ? m : fmaxf(m, lo);
-    const float s = round_as(a.dt, mc * (1.0f / 7.0f));
+    const float s = round_as(a.dt, sieve_scalar_div(mc, 7.0f, a.ieee_div));
     for (int64_t k = tid; k < a.K; k += kSieveNT) {
         const float wv = load_as_f32(a.w, a.dt, base + k);
         float t = rintf(round_as(a.dt, wv / s));
@@ -177,16 +185,16 @@ __global__ void __launch_bounds__(kSieveNT) sieve_hdiag_partial_kernel(const voi
 }
 
 // diag / n + 1e-6 with torch's steps: the diagonal rounded to x's dtype,
-// times the FP32 reciprocal of n (division by a host scalar), rounded, plus
-// 1e-6, rounded.
+// divided by n (a host scalar: times its FP32 reciprocal, or IEEE division
+// in the ieee_div mode), rounded, plus 1e-6, rounded.
 __global__ void __launch_bounds__(kSieveNT) sieve_hdiag_final_kernel(const float *partial, int slices, int64_t n,
-                                                                     int64_t K, int dt, void *out) {
+                                                                     int64_t K, int dt, void *out, int ieee_div) {
     const int64_t k = (int64_t)blockIdx.x * kSieveNT + threadIdx.x;
     if (k >= K) return;
     float s = 0.f;
     for (int i = 0; i < slices; i++) s += partial[(int64_t)i * K + k];
     const float d = round_as(dt, s);
-    const float q = round_as(dt, d * (1.0f / (float)n));
+    const float q = round_as(dt, sieve_scalar_div(d, (float)n, ieee_div));
     store_from_f32(out, dt, k, round_as(dt, q + 1e-6f));
 }
 
@@ -195,8 +203,10 @@ static unsigned sieve_grid(int64_t n) {
     return (unsigned)(b < 4096 ? (b > 0 ? b : 1) : 4096);
 }
 
-hipError_t launch_sieve_quantize(const void *w, int dt, int64_t N, int64_t K, void *w_base, hipStream_t stream) {
+hipError_t launch_sieve_quantize(const void *w, int dt, int64_t N, int64_t K, void *w_base, int ieee_div,
+                                 hipStream_t stream) {
     SieveArgs a{};
+    a.ieee_div = ieee_div;
     a.w = w;
     a.dt = dt;
     a.N = N;
@@ -208,8 +218,9 @@ hipError_t launch_sieve_quantize(const void *w, int dt, int64_t N, int64_t K, vo
 
 hipError_t launch_sieve_split(const void *w, int dt, int64_t N, int64_t K, const void *h, int hdt, int64_t h_stride,
                               int score_dt, int use_rank, int64_t rank, float thresh, void *w_base, void *w_ortho,
-                              float *score, void *sel, hipStream_t stream) {
+                              float *score, void *sel, int ieee_div, hipStream_t stream) {
     SieveArgs a{};
+    a.ieee_div = ieee_div;
     a.w = w;
     a.dt = dt;
     a.N = N;
@@ -249,7 +260,7 @@ int64_t sieve_hdiag_slices(int64_t n) {
     return s < 64 ? (s > 0 ? s : 1) : 64;
 }
 
-hipError_t launch_sieve_hdiag(const void *x, int dt, int64_t n, int64_t K, float *partial, void *out,
+hipError_t launch_sieve_hdiag(const void *x, int dt, int64_t n, int64_t K, float *partial, void *out, int ieee_div,
                               hipStream_t stream) {
     const int64_t slices = sieve_hdiag_slices(n);
     const int64_t rows = (n + slices - 1) / slices;
@@ -257,7 +268,7 @@ hipError_t launch_sieve_hdiag(const void *x, int dt, int64_t n, int64_t K, float
     hipLaunchKernelGGL(sieve_hdiag_partial_kernel, dim3(cb, (unsigned)slices), dim3(kSieveNT), 0, stream, x, dt, n, K,
                        rows, partial);
     hipLaunchKernelGGL(sieve_hdiag_final_kernel, dim3(cb), dim3(kSieveNT), 0, stream, partial, (int)slices, n, K, dt,
-                       out);
+                       out, ieee_div);
     return hipGetLastError();
 }
 

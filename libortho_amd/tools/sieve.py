@@ -16,6 +16,13 @@ On a ROCm GPU the CSR is built by the library's packing kernels
 (``_C_ops.pack_csr``, same result bit for bit); elsewhere by torch ops
 (``torch.nonzero`` already lists coordinates in row-major order, so no sort
 is needed).
+
+The offline sieve (``quantize_int4``, ``hessian_sieve``,
+``compute_hessian_diag_approx``) always runs the library's kernels
+(orth_sieve.hip).  A CPU tensor is copied to the current ROCm GPU, split
+there with the arithmetic torch uses on CPU tensors (IEEE division by the
+host scalars), and the results are copied back; without a ROCm GPU, or for
+dtypes other than float16 / bfloat16 / float32, these functions raise.
 """
 from __future__ import annotations
 
@@ -54,49 +61,40 @@ def pack_ortho_sparse_torch(w_ortho: torch.Tensor, format: str = "csr"):
 
 # ------------------------------------------------------------ offline sieve
 
-def quantize_int4_torch(weight: torch.Tensor) -> torch.Tensor:
-    """The torch-op form of ``quantize_int4`` (/root/reference/tools/sieve.py:13-23):
-    per-row scale max|w| (clamped at 1e-8) / 7, round-half-even of w / s
-    clamped to [-8, 7], times s; non-finite results become 0."""
-    max_vals = weight.abs().max(dim=1, keepdim=True)[0].clamp(min=1e-8)
-    scales = max_vals / 7.0
-    result = (weight / scales).round().clamp(-8, 7) * scales
-    return torch.where(torch.isfinite(result), result, torch.zeros_like(result))
+_SIEVE_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
-def hessian_sieve_torch(weight: torch.Tensor, H_inv: torch.Tensor, curvature_thresh: float = 10.0,
-                        sparsity_target: Optional[float] = None):
-    """The torch-op form of ``hessian_sieve`` (/root/reference/tools/sieve.py:25-76)."""
-    w_base = quantize_int4_torch(weight)
-    residual = weight - w_base
-    if H_inv.dim() > 1:
-        H_inv = torch.diag(H_inv)
-    score = (residual ** 2) / (H_inv + 1e-6).unsqueeze(0)
-    if sparsity_target is not None:
-        k = int(sparsity_target * score.numel())
-        threshold = torch.topk(score.flatten(), k, largest=True).values[-1] if k > 0 else score.max() + 1.0
-    else:
-        threshold = curvature_thresh
-    return w_base, residual * (score > threshold)
+def _sieve_device(*tensors: torch.Tensor):
+    """The GPU the sieve runs on and whether the inputs came from the CPU
+    (then torch's CPU arithmetic is reproduced and results are copied back)."""
+    for t in tensors:
+        if t.dtype not in _SIEVE_DTYPES:
+            raise TypeError(f"the sieve kernels take float16, bfloat16 or float32 tensors, got {t.dtype}")
+    first = tensors[0]
+    if first.is_cuda:
+        return first.device, False
+    if first.device.type != "cpu":
+        raise RuntimeError(f"the sieve runs on a ROCm GPU; tensors on {first.device} are not supported")
+    if not torch.cuda.is_available():
+        raise RuntimeError("the sieve runs on the library's GPU kernels: a CPU tensor needs a ROCm GPU to be "
+                           "split on (none is available)")
+    return torch.device("cuda", torch.cuda.current_device()), True
 
 
-def compute_hessian_diag_approx_torch(inputs: torch.Tensor, outputs: Optional[torch.Tensor] = None):
-    """The torch-op form of ``compute_hessian_diag_approx``
-    (/root/reference/tools/sieve.py:79-95): diag(X^T X) / n + 1e-6."""
-    n = inputs.shape[0]
-    return torch.diag(torch.matmul(inputs.T, inputs)) / n + 1e-6
-
-
-def _sieve_on_device(t: torch.Tensor) -> bool:
-    return t.is_cuda and t.dtype in (torch.float16, torch.bfloat16, torch.float32)
+def _require_2d(t: torch.Tensor, what: str) -> None:
+    if t.dim() != 2:
+        raise ValueError(f"{what} must be 2-D, got shape {tuple(t.shape)}")
 
 
 def quantize_int4(weight: torch.Tensor) -> torch.Tensor:
-    """Per-row INT4 fake quantisation, /root/reference/tools/sieve.py:13-23."""
-    if weight.dim() == 2 and _sieve_on_device(weight):
-        from .. import _C_ops
-        return _C_ops.sieve_quantize(weight)
-    return quantize_int4_torch(weight)
+    """Per-row INT4 fake quantisation, /root/reference/tools/sieve.py:13-23:
+    s = clamp(max|w|, 1e-8) / 7 per row, clamp(round(w / s), -8, 7) * s,
+    non-finite results 0; same dtype, shape and device as ``weight``."""
+    from .. import _C_ops
+    _require_2d(weight, "weight")
+    dev, from_cpu = _sieve_device(weight)
+    out = _C_ops.sieve_quantize(weight.to(dev), ieee_div=from_cpu)
+    return out.cpu() if from_cpu else out
 
 
 def hessian_sieve(weight: torch.Tensor, H_inv: torch.Tensor, curvature_thresh: float = 10.0,
@@ -104,17 +102,23 @@ def hessian_sieve(weight: torch.Tensor, H_inv: torch.Tensor, curvature_thresh: f
     """Base/Ortho split, /root/reference/tools/sieve.py:25-76: (w_base,
     w_ortho) with w_base = quantize_int4(weight) and w_ortho the residual
     where residual^2 / (H_inv + 1e-6) exceeds the threshold (the k-th
-    largest score for ``sparsity_target``, else ``curvature_thresh``)."""
-    if weight.dim() == 2 and _sieve_on_device(weight) and H_inv.is_cuda and \
-            H_inv.dtype in (torch.float16, torch.bfloat16, torch.float32) and H_inv.dim() in (1, 2):
-        from .. import _C_ops
-        return _C_ops.sieve_split(weight, H_inv, curvature_thresh, sparsity_target)
-    return hessian_sieve_torch(weight, H_inv, curvature_thresh, sparsity_target)
+    largest score for ``sparsity_target``, else ``curvature_thresh``);
+    H_inv is a vector or a matrix whose diagonal is used."""
+    from .. import _C_ops
+    _require_2d(weight, "weight")
+    if H_inv.dim() not in (1, 2):
+        raise ValueError(f"H_inv must be 1-D or 2-D, got shape {tuple(H_inv.shape)}")
+    dev, from_cpu = _sieve_device(weight, H_inv)
+    wb, wo = _C_ops.sieve_split(weight.to(dev), H_inv.to(dev), curvature_thresh, sparsity_target,
+                                ieee_div=from_cpu)
+    return (wb.cpu(), wo.cpu()) if from_cpu else (wb, wo)
 
 
 def compute_hessian_diag_approx(inputs: torch.Tensor, outputs: Optional[torch.Tensor] = None):
-    """diag(X^T X) / n + 1e-6, /root/reference/tools/sieve.py:79-95."""
-    if inputs.dim() == 2 and _sieve_on_device(inputs):
-        from .. import _C_ops
-        return _C_ops.sieve_hdiag(inputs)
-    return compute_hessian_diag_approx_torch(inputs, outputs)
+    """diag(X^T X) / n + 1e-6 for X = ``inputs`` [n, in_features],
+    /root/reference/tools/sieve.py:79-95 (``outputs`` is unused there too)."""
+    from .. import _C_ops
+    _require_2d(inputs, "inputs")
+    dev, from_cpu = _sieve_device(inputs)
+    out = _C_ops.sieve_hdiag(inputs.to(dev), ieee_div=from_cpu)
+    return out.cpu() if from_cpu else out

@@ -149,12 +149,13 @@ int main(void) {
            "csr short mask");
     expect(orth_pack_csr_fill_hip(xbuf, ORTH_DT_F32, 4, 8, rp, NULL, 0, col, vals, 9, NULL),
            ORTH_ERR_INVALID_ARGUMENT, "csr fill dtype");
-    expect(orth_sieve_quantize_hip(xbuf, ORTH_DT_F32, 4, 8, NULL, NULL), ORTH_ERR_INVALID_ARGUMENT, "sieve NULL");
+    expect(orth_sieve_quantize_hip(xbuf, ORTH_DT_F32, 4, 8, NULL, 0, NULL), ORTH_ERR_INVALID_ARGUMENT, "sieve NULL");
+    expect(orth_sieve_quantize_hip(xbuf, ORTH_DT_F32, 4, 8, qbuf, 6, NULL), ORTH_ERR_INVALID_ARGUMENT, "sieve flags");
     expect(orth_sieve_split_hip(xbuf, ORTH_DT_F32, 4, 8, NULL, ORTH_DT_F32, 1, ORTH_DT_F32, 0, 0, 1.0f, qbuf, sbuf,
-                                (float *)ybuf, NULL, NULL), ORTH_ERR_INVALID_ARGUMENT, "split NULL h");
+                                (float *)ybuf, NULL, 0, NULL), ORTH_ERR_INVALID_ARGUMENT, "split NULL h");
     expect(orth_sieve_split_hip(xbuf, ORTH_DT_F32, 4, 8, sbuf, ORTH_DT_F32, 1, ORTH_DT_F32, 1, 33, 1.0f, qbuf, sbuf,
-                                (float *)ybuf, ybuf, NULL), ORTH_ERR_INVALID_ARGUMENT, "split rank");
-    expect(orth_sieve_hdiag_hip(xbuf, ORTH_DT_F32, 4, 8, (float *)ybuf, 1, sbuf, NULL), ORTH_ERR_INVALID_ARGUMENT,
+                                (float *)ybuf, ybuf, ORTH_SIEVE_IEEE_DIV, NULL), ORTH_ERR_INVALID_ARGUMENT, "split rank");
+    expect(orth_sieve_hdiag_hip(xbuf, ORTH_DT_F32, 4, 8, (float *)ybuf, 1, sbuf, 0, NULL), ORTH_ERR_INVALID_ARGUMENT,
            "hdiag workspace");
     expect(orth_hip_set_kernel_policy(7), ORTH_ERR_INVALID_ARGUMENT, "policy");
     expect(orth_hip_set_kernel_policy(0), ORTH_OK, "policy auto");

@@ -43,13 +43,13 @@ hipError_t plan_prepare_device() { return hipSuccess; }
 bool skinny_supported(const ForwardArgs &) { return false; }
 int64_t skinny_workspace_bytes(const ForwardArgs &, int) { return 0; }
 hipError_t launch_skinny(const ForwardArgs &, const void *, int, float *, hipStream_t) { return hipErrorInvalidValue; }
-hipError_t launch_sieve_quantize(const void *, int, int64_t, int64_t, void *, hipStream_t) {
+hipError_t launch_sieve_quantize(const void *, int, int64_t, int64_t, void *, int, hipStream_t) {
     return hipErrorInvalidValue;
 }
 hipError_t launch_sieve_split(const void *, int, int64_t, int64_t, const void *, int, int64_t, int, int, int64_t, float,
-                              void *, void *, float *, void *, hipStream_t) { return hipErrorInvalidValue; }
+                              void *, void *, float *, void *, int, hipStream_t) { return hipErrorInvalidValue; }
 int64_t sieve_hdiag_slices(int64_t n) { return n < 64 ? (n > 0 ? n : 1) : 64; }
-hipError_t launch_sieve_hdiag(const void *, int, int64_t, int64_t, float *, void *, hipStream_t) {
+hipError_t launch_sieve_hdiag(const void *, int, int64_t, int64_t, float *, void *, int, hipStream_t) {
     return hipErrorInvalidValue;
 }
 }  // namespace orth

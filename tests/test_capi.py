@@ -196,7 +196,7 @@ def test_plan_size(L):
 
 
 def test_policy_alpha_and_version(L):
-    assert L.orth_hip_abi_version() == 102
+    assert L.orth_hip_abi_version() == 103
     before = L.orth_hip_get_kernel_policy()
     for name, val in _lib.POLICIES.items():
         _lib.set_kernel_policy(name)

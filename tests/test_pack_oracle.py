@@ -1,8 +1,14 @@
 """The packing oracle (oracle/pack_oracle.py) pinned on the CPU: closed
-forms, a library routine for the CSR, and the reference's own torch ops
-(the torch-op forms in libortho_amd, which follow
-/root/reference/torch_bind/ortho_linear.py:89-120 and
-/root/reference/tools/sieve.py:119-152 line by line) run on CPU tensors."""
+forms, a library routine for the CSR (scipy.sparse), and the outputs the
+reference's own load_from_weights and pack_ortho_sparse gave on CPU tensors
+(tests/golden/pack_cases.npz, written by tests/golden/make_sieve_golden.py
+from /root/reference/torch_bind/ortho_linear.py:79-128 and
+/root/reference/tools/sieve.py:119-152): FP16 / BF16 weights whose W / s
+rounds across a half step in the dtype, given FP16 and FP32 scales, the
+1e-6 floor.  The product's CPU packers (pack_base_torch,
+pack_ortho_sparse_torch) are checked against the oracle."""
+import os
+
 import numpy as np
 import pytest
 import scipy.sparse as sp
@@ -39,6 +45,47 @@ def random_dense(rng, N, K, dtype, scale=1.0):
     if dtype == "bf16":
         return PO.f32_to_bf16_bits(w)
     return w
+
+
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "pack_cases.npz"))
+
+
+def gold_dense(key, dtype):
+    """A fixture weight in the oracle's input form (BF16 as bit patterns)."""
+    a = GOLD[key]
+    return a.view(np.float16) if dtype == "f16" else a
+
+
+@pytest.mark.parametrize("dtype", PO.DTYPES)
+def test_pack_base_oracle_equals_reference_load_from_weights(dtype):
+    w = gold_dense(f"lw_{dtype}_w", dtype)
+    q, s = PO.pack_base(w, dtype, scale_div="ieee")
+    assert np.array_equal(q, GOLD[f"lw_{dtype}_q"])
+    assert np.array_equal(s.view(np.uint16), GOLD[f"lw_{dtype}_s"])
+    for sdt in ("f16", "f32"):
+        s_in = GOLD[f"lws_{dtype}_{sdt}_s_in"]
+        q, s = PO.pack_base(w, dtype, scales=s_in.view(np.float16) if sdt == "f16" else s_in,
+                            scales_dtype=sdt, scale_div="ieee")
+        assert np.array_equal(q, GOLD[f"lws_{dtype}_{sdt}_q"]), sdt
+        assert np.array_equal(s.view(np.uint16), GOLD[f"lws_{dtype}_{sdt}_s"]), sdt
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_pack_base_fixture_rejects_fp32_math(dtype):
+    # the same weights packed with W / s in FP32 (no rounding to the
+    # weight's dtype before round()) give other nibbles
+    w = PO.as_f32(gold_dense(f"lw_{dtype}_w", dtype), dtype)
+    q, _ = PO.pack_base(w, "f32", scale_div="ieee")
+    assert not np.array_equal(q, GOLD[f"lw_{dtype}_q"])
+
+
+@pytest.mark.parametrize("dtype", PO.DTYPES)
+def test_csr_oracle_equals_reference_pack_ortho_sparse(dtype):
+    w = gold_dense(f"csr_{dtype}_w", dtype)
+    rp, col, vals = PO.pack_csr(w, dtype)
+    vb = np.uint16 if dtype != "f32" else np.uint32
+    assert np.array_equal(rp, GOLD[f"csr_{dtype}_row_ptr"]) and np.array_equal(col, GOLD[f"csr_{dtype}_col"])
+    assert np.array_equal(np.asarray(vals).view(vb), GOLD[f"csr_{dtype}_vals"].view(vb))
 
 
 def test_bf16_rounding_is_nearest_even():
@@ -97,7 +144,7 @@ def test_the_two_scale_divisions_differ():
 @pytest.mark.parametrize("dtype", PO.DTYPES)
 @pytest.mark.parametrize("group", [None, 128])
 @pytest.mark.parametrize("given", [None, "f16", "f32"])
-def test_oracle_equals_the_reference_torch_ops_on_cpu(dtype, group, given):
+def test_product_cpu_packer_equals_oracle(dtype, group, given):
     rng = np.random.default_rng(11)
     N, K = 33, 512
     w = random_dense(rng, N, K, dtype, scale=0.05)
@@ -115,7 +162,7 @@ def test_oracle_equals_the_reference_torch_ops_on_cpu(dtype, group, given):
 
 
 @pytest.mark.parametrize("dtype", PO.DTYPES)
-def test_csr_oracle_equals_the_reference_ops_and_scipy(dtype):
+def test_csr_oracle_equals_scipy_and_the_product_cpu_packer(dtype):
     rng = np.random.default_rng(12)
     N, K = 40, 300
     w32 = rng.standard_normal((N, K)).astype(np.float32)
