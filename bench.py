@@ -12,13 +12,14 @@ no step finds its weights in the 256 MB Infinity Cache.  Each copy carries
 its ortho plan, built once before timing, as OrthoLinear builds and caches
 it on its first call with alpha > 0.  The K timed steps are one replay of a
 HIP graph holding exactly K launches (launch cost on the host is not what is
-measured), replayed right behind an untimed replay of the same graph and
-bracketed by HIP events on the launch stream.
+measured) behind untimed launches of the same workload, bracketed by two
+device clock stamps (tiny kernels reading the GPU's 100 MHz clock,
+orth_hip_clock_stamp) inside that graph.
 
 Printed: one JSON line with the contract fields plus
   roofline      the decode kernel: algorithmic bytes per launch / its average
-                launch duration (HIP events on the launch stream around the
-                timed graph replay, divided by K) against 8 TB/s
+                launch duration (the device-clock interval around the K
+                timed launches, divided by K) against 8 TB/s
   cpu_baseline  the reference CPU forward restated (oracle/cpu_baseline.c,
                 reference flags, 1 pinned core) on a bounded sample
                 (c2 M=1), plus c1 (whole layer) and c3 (token subset,
@@ -50,7 +51,9 @@ HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk, dense
 ROTATE_MIN_BYTES = 512 << 20
 ROTATE_MIN_COPIES = 16
-PRE_STEPS = 200      # untimed launches in the timing graph before its first event
+PRE_STEPS = 1500     # untimed launches in the timing graph before its first clock stamp: the
+                     # GPU's clocks are still ramping ~1 ms into a burst (20 decode launches
+                     # timed after 200 untimed ones: 6.90 us each; after 1,000 or 3,000: 6.63)
 STEADY_STEPS = 2000  # launches of the long graph behind ms_per_step_steady
 
 
@@ -258,84 +261,75 @@ _HIP = None
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # hip_runtime_api.h
 
 
+def _clock_stamp(torch, buf, stream_ptr):
+    """Launch the library's device clock stamp into buf (int64 [16]) on the
+    stream: 8 workgroups each write (100 MHz device clock, XCD id)."""
+    from libortho_amd import _lib
+    import ctypes
+    _lib.check(_lib.lib().orth_hip_clock_stamp(ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(stream_ptr)))
+
+
+def _stamp_interval_ms(t0, t1) -> float:
+    """Milliseconds between two clock stamps (int64 [16] host tensors of
+    (clock, XCD) pairs): the median over the XCDs both stamps ran on."""
+    a = {int(t0[2 * i + 1]): int(t0[2 * i]) for i in range(8)}
+    b = {int(t1[2 * i + 1]): int(t1[2 * i]) for i in range(8)}
+    d = sorted(b[k] - a[k] for k in a if k in b)
+    if not d:
+        raise RuntimeError("clock stamps share no XCD")
+    return d[len(d) // 2] * 1e-5  # 100 MHz ticks -> ms
+
+
 def graph_steps_time(torch, fn, steps, pre):
-    """Milliseconds per call of fn(pre + i), i < steps, timed by HIP events
-    recorded inside one HIP graph: [pre untimed calls] -> [event -> the
-    `steps` calls -> event].  The untimed calls put graph start-up and the
-    clock ramp before the first event; the events bracket exactly `steps`
-    calls, and sit inside the timed segment's own graph (its first and last
-    nodes), so the start of that segment is not timed either.  The graph is
-    built on a stream of its own (default priority) from two captured
-    segments, replayed once untimed, then once timed."""
+    """Milliseconds per call of fn(pre + i), i < steps, on the GPU's own
+    clock: one captured HIP graph holds [pre untimed calls, clock stamp,
+    the `steps` calls, clock stamp].  Each stamp is a tiny kernel whose
+    workgroups read the 100 MHz device clock as they start
+    (orth_hip_clock_stamp), so the interval between the two covers exactly
+    the `steps` calls and one launch gap, with no event record (whose
+    cache flush and completion signal cost several microseconds a segment,
+    spread over few steps) and no host round trip inside it.  The untimed
+    calls put graph start-up and the clock ramp before the first stamp.
+    The graph is built on a stream of its own (default priority), replayed
+    once untimed, then once timed; the stream is synchronized on both
+    sides of each replay."""
     global _HIP
     if _HIP is None:
         _HIP = _Hip()
     H, c = _HIP, _HIP.c
     s = H.new("hipStreamCreate")
     ts = torch.cuda.ExternalStream(s.value)
-    graphs, execs, events = [], [], []
+    graphs, execs = [], []
+    stamps = torch.zeros(2, 16, dtype=torch.int64, device="cuda")
     try:
         with torch.cuda.stream(ts):
             fn(0)  # any per-stream set-up outside capture
         torch.cuda.synchronize()
-
-        def capture(lo, n):
-            with torch.cuda.stream(ts):
-                H("hipStreamBeginCapture", s, 2)  # relaxed: other threads may allocate
-                for i in range(lo, lo + n):
-                    fn(i)
-                g = c.c_void_p()
-                H("hipStreamEndCapture", s, c.byref(g))
-            graphs.append(g)
-            return g
-        gA = capture(0, pre)
-        gB = capture(pre, steps)
-        # timing-only events: hipEventDisableSystemFence skips the system-scope
-        # cache writeback and invalidation at each event, which HIP documents
-        # for exactly this use; it cuts the fixed cost of one measurement
-        # from ~13 to ~8 us (measured: 20 decode launches 7.2 -> 7.0 us each,
-        # 2,000 launches 6.60 us either way)
-        e0 = H.new("hipEventCreateWithFlags", HIP_EVENT_DISABLE_SYSTEM_FENCE)
-        e1 = H.new("hipEventCreateWithFlags", HIP_EVENT_DISABLE_SYSTEM_FENCE)
-        events += [e0, e1]
-        # the timed segment's roots and leaves, then an event node before the
-        # roots and one after the leaves, inside the segment's graph
-        n = c.c_size_t(0)
-        H("hipGraphGetNodes", gB, None, c.byref(n))
-        nodes = (c.c_void_p * n.value)()
-        H("hipGraphGetNodes", gB, nodes, c.byref(n))
-
-        def count(api, node):
-            k = c.c_size_t(0)
-            H(api, node, None, c.byref(k))
-            return k.value
-        roots = [x for x in nodes if count("hipGraphNodeGetDependencies", x) == 0]
-        leaves = [x for x in nodes if count("hipGraphNodeGetDependentNodes", x) == 0]
-        n0 = H.new("hipGraphAddEventRecordNode", gB, None, 0, e0)
-        for r in roots:
-            H("hipGraphAddDependencies", gB, c.byref(n0), (c.c_void_p * 1)(r), 1)
-        H.new("hipGraphAddEventRecordNode", gB, (c.c_void_p * len(leaves))(*leaves), len(leaves), e1)
-        G = H.new("hipGraphCreate", 0)
-        graphs.append(G)
-        nA = H.new("hipGraphAddChildGraphNode", G, None, 0, gA)
-        H.new("hipGraphAddChildGraphNode", G, (c.c_void_p * 1)(nA), 1, gB)
-        ex = H.new("hipGraphInstantiate", G, None, None, 0)
+        with torch.cuda.stream(ts):
+            H("hipStreamBeginCapture", s, 2)  # relaxed: other threads may allocate
+            for i in range(pre):
+                fn(i)
+            _clock_stamp(torch, stamps[0], s.value)
+            for i in range(pre, pre + steps):
+                fn(i)
+            _clock_stamp(torch, stamps[1], s.value)
+            g = c.c_void_p()
+            H("hipStreamEndCapture", s, c.byref(g))
+        graphs.append(g)
+        ex = H.new("hipGraphInstantiate", g, None, None, 0)
         execs.append(ex)
         H("hipGraphLaunch", ex, s)
         H("hipStreamSynchronize", s)
         H("hipGraphLaunch", ex, s)
         H("hipStreamSynchronize", s)
-        ms = c.c_float()
-        H("hipEventElapsedTime", c.byref(ms), e0, e1)
-        return ms.value / steps
+        host = stamps.cpu()
+        return _stamp_interval_ms(host[0], host[1]) / steps
     finally:
         torch.cuda.synchronize()
         for ex in execs:
             H("hipGraphExecDestroy", ex)
         for g in graphs:
             H("hipGraphDestroy", g)
-        for e in events:
-            H("hipEventDestroy", e)
         H("hipStreamDestroy", s)
 
 
@@ -856,8 +850,9 @@ def main():
                    "bytes_per_step": bytes_step, "flops_per_step": flops_step,
                    "weight_copies_rotated": r["copies"], "kernel": r["kernel"],
                    "ortho_plan": "built once per copy before timing (as OrthoLinear caches it)",
-                   "timing": f"HIP events recorded inside one HIP graph around the K launches, "
-                             f"after {PRE_STEPS} untimed launches in the same graph"},
+                   "timing": f"device clock stamps (100 MHz s_memrealtime, per XCD, median) launched "
+                             f"inside one HIP graph around the K launches, after {PRE_STEPS} untimed "
+                             f"launches in the same graph"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": (load_traffic(workload) or {}).get("bytes"),
@@ -865,8 +860,8 @@ def main():
                      "launch_us_steady": round(r["ms_per_step_steady"] * 1e3, 3),
                      "steady_note": f"launch_us_steady: {STEADY_STEPS} launches in one graph, events around "
                                     "its replay (the per-launch time a kernel trace reports); launch_us: "
-                                    "the timed K steps, which also carry the fixed cost of the two "
-                                    "in-graph timing events",
+                                    "the timed K steps between two device clock stamps (one launch gap "
+                                    "of fixed cost, spread over K)",
                      "bytes_per_launch": bytes_step},
         "cpu_baseline": cpu,
         "secondary": secondary,

@@ -314,6 +314,17 @@ int orth_hip_get_kernel_policy(void);
  * mid-batch, 7 K quarters over the grid, 0 none. */
 int orth_hip_last_kernel(void);
 
+/* Device clock stamp for timing stream-ordered work (benchmarks; no
+ * counterpart in the reference): launches ORTH_CLOCK_GROUPS workgroups on
+ * `stream`; workgroup i writes dst[2i] = the 100 MHz constant device clock
+ * (s_memrealtime) read as it starts and dst[2i + 1] = the id of the XCD it
+ * ran on.  dst: device memory of 2 * ORTH_CLOCK_GROUPS uint64_t.  Two
+ * stamps around K launches, differenced per XCD, time the K launches plus
+ * one launch gap. */
+#define ORTH_CLOCK_GROUPS 8
+#define ORTH_CLOCK_HZ 100000000
+int orth_hip_clock_stamp(uint64_t *dst, void *stream);
+
 /* Message of the calling thread's last failure ("" if none). */
 const char *orth_hip_last_error(void);
 

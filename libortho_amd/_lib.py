@@ -83,6 +83,7 @@ SIGNATURES = {
     "orth_hip_last_kernel": (ctypes.c_int, []),
     "orth_hip_last_error": (ctypes.c_char_p, []),
     "orth_hip_abi_version": (ctypes.c_int, []),
+    "orth_hip_clock_stamp": (ctypes.c_int, [_P, _P]),
 }
 
 _lib = None

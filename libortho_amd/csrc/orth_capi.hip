@@ -63,6 +63,7 @@ hipError_t launch_sieve_split(const void *w, int dt, int64_t N, int64_t K, const
 int64_t sieve_hdiag_slices(int64_t n);
 hipError_t launch_sieve_hdiag(const void *x, int dt, int64_t n, int64_t K, float *partial, void *out, int ieee_div,
                               hipStream_t stream);
+hipError_t launch_clock_stamp(uint64_t *dst, hipStream_t stream);
 }  // namespace orth
 
 using namespace orth;
@@ -781,6 +782,16 @@ int orth_hip_get_kernel_policy(void) { return g_policy.load(); }
 int orth_hip_last_kernel(void) { return t_last_kernel; }
 
 const char *orth_hip_last_error(void) { return t_error.c_str(); }
+
+int orth_hip_clock_stamp(uint64_t *dst, void *stream) {
+    if (!dst) return fail(ORTH_ERR_INVALID_ARGUMENT, "dst is NULL");
+    if (reinterpret_cast<uintptr_t>(dst) % 8) return fail(ORTH_ERR_INVALID_ARGUMENT, "dst is not 8-byte aligned");
+    int rc = current_device_ok(nullptr);
+    if (rc != ORTH_OK) return rc;
+    hipError_t e = launch_clock_stamp(dst, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail_hip(e, "clock stamp launch");
+    return ORTH_OK;
+}
 
 int orth_hip_abi_version(void) { return 103; }
 

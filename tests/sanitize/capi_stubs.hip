@@ -49,6 +49,7 @@ hipError_t launch_sieve_quantize(const void *, int, int64_t, int64_t, void *, in
 hipError_t launch_sieve_split(const void *, int, int64_t, int64_t, const void *, int, int64_t, int, int, int64_t, float,
                               void *, void *, float *, void *, int, hipStream_t) { return hipErrorInvalidValue; }
 int64_t sieve_hdiag_slices(int64_t n) { return n < 64 ? (n > 0 ? n : 1) : 64; }
+hipError_t launch_clock_stamp(uint64_t *, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_sieve_hdiag(const void *, int, int64_t, int64_t, float *, void *, int, hipStream_t) {
     return hipErrorInvalidValue;
 }
