@@ -187,6 +187,13 @@ struct DeviceState {
     int cus = 256;
     char arch[64] = {0};
     void *scratch = nullptr;      // device address of this device's scratch array
+    // the last no-allocation call's completion on this device (recorded on
+    // its stream), so that a call on another stream waits for it before it
+    // touches the scratch array
+    hipEvent_t noalloc_done = nullptr;
+    hipStream_t noalloc_stream = nullptr;
+    bool noalloc_recorded = false;
+    std::mutex noalloc_mu;
 };
 std::mutex g_dev_mu;
 DeviceState g_dev[64];
@@ -215,6 +222,8 @@ int current_device_ok(int *dev_out) {
                 e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
                 if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress (scratch)");
                 st.scratch = ptr;
+                e = hipEventCreateWithFlags(&st.noalloc_done, hipEventDisableTiming);
+                if (e != hipSuccess) return fail_hip(e, "hipEventCreateWithFlags (no-allocation ordering)");
             }
             st.checked.store(ok ? 1 : -1, std::memory_order_release);
         }
@@ -228,13 +237,12 @@ int current_device_ok(int *dev_out) {
 // Split-K workspace of the mid-batch kernel, one per (device, stream): the
 // FP32 partials its reduction kernel sums.  Calls on one stream are ordered;
 // calls on different streams use different workspaces.  Allocation happens
-// on first use (and on growth) outside graph capture.  Inside a capture the
-// call uses the capturing stream's own workspace when it has one large
-// enough (the graph is then ordered with that stream's work when it is
-// replayed on that stream, the usual pattern of eager warm-up, capture and
-// replay); otherwise it gets a stream-ordered workspace of its own
-// (hipMallocAsync before the launch, hipFreeAsync after it, both recorded
-// in the graph).  A capture never takes another stream's workspace.
+// on first use (and on growth) outside graph capture.  A captured call
+// always gets a stream-ordered workspace of its own (hipMallocAsync before
+// the launch, hipFreeAsync after it, both recorded in the graph and owned
+// by it): a graph may be replayed on any stream, concurrently with eager
+// calls on the stream it was captured on, so it never shares a stream's
+// workspace.
 struct Workspace {
     void *buf = nullptr;
     int64_t part_bytes = 0;
@@ -251,14 +259,6 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part,
     hipError_t e = hipStreamIsCapturing(stream, &cs);
     if (e != hipSuccess) return fail_hip(e, "hipStreamIsCapturing");
     if (cs != hipStreamCaptureStatusNone) {
-        {
-            std::lock_guard<std::mutex> lk(g_ws_mu);
-            auto it = g_ws.find({dev, static_cast<void *>(stream)});
-            if (it != g_ws.end() && it->second.buf && it->second.part_bytes >= part_bytes) {
-                *part = static_cast<float *>(it->second.buf);
-                return ORTH_OK;
-            }
-        }
         void *tmp = nullptr;
         e = hipMallocAsync(&tmp, (size_t)part_bytes, stream);
         if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (mid-batch workspace in a captured graph)");
@@ -334,6 +334,8 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
     return ORTH_OK;
 }
 
+int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, hipStream_t stream, bool noalloc);
+
 // noalloc: scratch from the device's scratch array instead of the stream's
 // workspace or stream-ordered allocations (orth_layer_forward_hip_noalloc).
 int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
@@ -362,6 +364,46 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
     rc = pick_kernel(a, plan, g_policy.load(std::memory_order_relaxed), &kernel);
     if (rc != ORTH_OK) return rc;
 
+    // No-allocation calls share the device's scratch array: a call on a
+    // stream other than the last one's first waits for that call (its
+    // completion event), and records its own completion after its launches.
+    // The lock keeps wait, launches and record of one call together when
+    // several host threads call at once.  A stream under graph capture is not
+    // ordered this way (a captured wait on an event recorded outside the
+    // capture is not allowed): calls captured into graphs on one GPU must be
+    // ordered by the caller.
+    std::unique_lock<std::mutex> noalloc_lk;
+    bool noalloc_order = false;
+    if (noalloc) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        hipError_t ce = hipStreamIsCapturing(stream, &cs);
+        if (ce != hipSuccess) return fail_hip(ce, "hipStreamIsCapturing");
+        noalloc_order = cs == hipStreamCaptureStatusNone;
+        if (noalloc_order) {
+            DeviceState &st = g_dev[dev];
+            noalloc_lk = std::unique_lock<std::mutex>(st.noalloc_mu);
+            if (st.noalloc_recorded && st.noalloc_stream != stream) {
+                ce = hipStreamWaitEvent(stream, st.noalloc_done, 0);
+                if (ce != hipSuccess) return fail_hip(ce, "hipStreamWaitEvent (no-allocation ordering)");
+            }
+        }
+    }
+    rc = launch_kernel(a, plan, kernel, dev, stream, noalloc);
+    if (noalloc_order && rc == ORTH_OK) {
+        DeviceState &st = g_dev[dev];
+        hipError_t ce = hipEventRecord(st.noalloc_done, stream);
+        if (ce != hipSuccess) return fail_hip(ce, "hipEventRecord (no-allocation ordering)");
+        st.noalloc_stream = stream;
+        st.noalloc_recorded = true;
+    }
+    if (rc != ORTH_OK) return rc;
+    t_last_kernel = kernel;
+    return ORTH_OK;
+}
+
+// The launches of one forward call with the kernel already chosen.
+int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, hipStream_t stream, bool noalloc) {
+    int rc = ORTH_OK;
     hipError_t e = hipSuccess;
     if (kernel == KERNEL_DECODE) {
         e = launch_decode(a, plan, g_dev[dev].cus, stream);
@@ -421,8 +463,7 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
         e = launch_general(a, stream);
     }
     if (e != hipSuccess) return fail_hip(e, "kernel launch");
-    t_last_kernel = kernel;
-    return ORTH_OK;
+    return rc;
 }
 
 // Layers that read one input: a single decode launch when every layer takes

@@ -4,7 +4,10 @@ stream-ordered allocations), through the C ABI: same bits, on two calls in
 a row with the second smaller, for each kernel that uses scratch (the
 mid-batch split-K partials; the prefill plan built for an unplanned
 alpha > 0 call) and for decode; and a request beyond the scratch size is
-refused before anything is launched."""
+refused before anything is launched.  Captured into a graph, a no-allocation
+call adds kernel nodes only (the allocating entry adds memory nodes); calls
+on two streams of one GPU are ordered by the library, so they do not race on
+the shared scratch."""
 import ctypes
 
 import numpy as np
@@ -88,3 +91,96 @@ def test_request_beyond_the_scratch_is_refused(gpu):
     assert "scratch" in _lib.last_error()
     torch.cuda.synchronize()
     assert bool((y == 7.0).all().item()), "nothing may be launched"
+
+
+# ------------------------------------------------------------ graph capture
+
+_GRAPH_NODE_KERNEL, _GRAPH_NODE_MEM_ALLOC, _GRAPH_NODE_MEM_FREE = 0, 10, 11
+
+
+def _hip():
+    h = ctypes.CDLL("libamdhip64.so")
+    V, P = ctypes.c_void_p, ctypes.POINTER
+    for name, args in (("hipStreamCreate", [P(V)]), ("hipStreamDestroy", [V]),
+                       ("hipStreamBeginCapture", [V, ctypes.c_int]), ("hipStreamEndCapture", [V, P(V)]),
+                       ("hipGraphGetNodes", [V, P(V), P(ctypes.c_size_t)]),
+                       ("hipGraphNodeGetType", [V, P(ctypes.c_int)]), ("hipGraphDestroy", [V])):
+        getattr(h, name).argtypes = args
+        getattr(h, name).restype = ctypes.c_int
+    return h
+
+
+def captured_node_types(entry, desc, x, y):
+    """Types of the nodes one call of `entry` adds to a graph captured on a
+    fresh stream."""
+    h = _hip()
+    s = ctypes.c_void_p()
+    assert h.hipStreamCreate(ctypes.byref(s)) == 0
+    g = ctypes.c_void_p()
+    try:
+        assert h.hipStreamBeginCapture(s, 0) == 0  # global mode
+        rc = getattr(_lib.lib(), entry)(ctypes.byref(desc), None, 0, None, 0, _p(x), _p(y), int(x.shape[0]),
+                                        _lib.DT_F16, s)
+        assert h.hipStreamEndCapture(s, ctypes.byref(g)) == 0
+        _lib.check(rc)
+        n = ctypes.c_size_t(0)
+        assert h.hipGraphGetNodes(g, None, ctypes.byref(n)) == 0
+        nodes = (ctypes.c_void_p * n.value)()
+        assert h.hipGraphGetNodes(g, nodes, ctypes.byref(n)) == 0
+        types = []
+        for nd in nodes:
+            t = ctypes.c_int(-1)
+            assert h.hipGraphNodeGetType(ctypes.c_void_p(nd), ctypes.byref(t)) == 0
+            types.append(t.value)
+        return types
+    finally:
+        if g.value:
+            h.hipGraphDestroy(g)
+        h.hipStreamDestroy(s)
+
+
+@pytest.mark.parametrize("cfg,M,alpha,kernel", [("c2", 24, 1.0, "skinny"), ("c3", 600, 1.0, "prefill"),
+                                                ("c2", 32, 0.0, "quarter"), ("c2", 1, 1.0, "decode")])
+def test_noalloc_capture_has_kernel_nodes_only(gpu, cfg, M, alpha, kernel):
+    layer = W.config_layer(cfg)
+    d = W.to_device(layer)
+    desc = _C_ops.make_layer(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], layer.K, layer.N, alpha,
+                             torch.device("cuda:0"))
+    x = torch.from_numpy(W.make_x(M, layer.K, 8600 + M)).cuda()
+    y = torch.empty(M, layer.N, dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    types = captured_node_types("orth_layer_forward_hip_noalloc", desc, x, y)
+    assert _C_ops.last_kernel() == kernel
+    assert types and all(t == _GRAPH_NODE_KERNEL for t in types), types
+    if kernel in ("skinny", "prefill", "quarter"):
+        # control: the allocating entry on a fresh capture stream records memory nodes
+        ctl = captured_node_types("orth_layer_forward_hip_ex", desc, x, y)
+        assert _GRAPH_NODE_MEM_ALLOC in ctl and _GRAPH_NODE_MEM_FREE in ctl, ctl
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(gpu):
+    """Split-K calls (partials in the shared scratch) launched back to back on
+    two streams with no synchronisation between them: each output equals
+    that of the allocating entry on one stream, bit for bit."""
+    layer = W.config_layer("c2")
+    d = W.to_device(layer)
+    desc = _C_ops.make_layer(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], layer.K, layer.N, 1.0,
+                             torch.device("cuda:0"))
+    xs = [torch.from_numpy(W.make_x(24, layer.K, 8700 + i)).cuda() for i in range(2)]
+    refs = []
+    for x in xs:
+        y = torch.empty(24, layer.N, dtype=torch.float16, device="cuda")
+        _lib.check(call("orth_layer_forward_hip_ex", desc, x, y))
+        refs.append(y)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rep in range(8):
+        outs = [torch.full((24, layer.N), float("nan"), dtype=torch.float16, device="cuda") for _ in xs]
+        torch.cuda.synchronize()
+        for i in (0, 1, 0, 1):
+            with torch.cuda.stream(streams[i]):
+                _lib.check(call("orth_layer_forward_hip_noalloc", desc, xs[i], outs[i]))
+                assert _C_ops.last_kernel() == "skinny"
+        torch.cuda.synchronize()
+        for i in (0, 1):
+            assert torch.equal(outs[i].view(torch.int16), refs[i].view(torch.int16)), f"rep {rep} stream {i}"
