@@ -529,24 +529,6 @@ __device__ __forceinline__ void fold_fast(f16 *Bs, f16 *trash, uint32_t e, bool 
     *p = fold_add<XB>(*p, alpha * v);
 }
 
-// Duplicate (row, col) entries may share a cell: CAS on its 32-bit word
-// (index arithmetic keeps the pointer in the LDS address space).
-template <bool XB>
-__device__ __forceinline__ void fold_cas(f16 *Bs, uint32_t e, float alpha) {
-    const int r = (e >> 24) & (PF_BN - 1), c = (e >> 16) & (PF_BK - 1);
-    const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
-    const int cell = pf_swz(r, c >> 3) + (c & 7);
-    uint32_t *w = reinterpret_cast<uint32_t *>(Bs) + (cell >> 1);
-    const int sh = (cell & 1) ? 16 : 0;
-    uint32_t old = *w, assumed;
-    do {
-        assumed = old;
-        const uint16_t nv = fold_add<XB>((uint16_t)(assumed >> sh), alpha * v);
-        const uint32_t upd = (assumed & ~(0xffffu << sh)) | ((uint32_t)nv << sh);
-        old = atomicCAS(w, assumed, upd);
-    } while (old != assumed);
-}
-
 // Folds step u's plan entries into the weight stage Bs.  The first 512
 // entries come from the prefetched register; a step with more (dense rows,
 // skewed outliers) reads the rest here.
@@ -562,9 +544,24 @@ __device__ __forceinline__ void pf_fold(const PrefillArgs &a, const int32_t *off
         // canonical entries are distinct cells: no ordering between passes
         if (hi - lo > PF_NT)
             for (int32_t e = lo + PF_NT + tid; e < hi; e += PF_NT) fold_fast<XB>(Bs, trash, a.entries[e], true, a.alpha);
-    } else {
-        if (lo + tid < hi) fold_cas<XB>(Bs, r.e, a.alpha);
-        for (int32_t e = lo + PF_NT + tid; e < hi; e += PF_NT) fold_cas<XB>(Bs, a.entries[e], a.alpha);
+    } else if (tid < PF_BN) {
+        // rows with duplicate or unsorted columns: one thread per row of the
+        // block applies that row's entries of the step one after another in
+        // plan order (row, then CSR position), so entries of one cell add in
+        // a fixed order (the result is reproducible bit for bit) and no two
+        // threads touch one cell.  The step's entries are sorted by row:
+        // this row's run starts at the first entry whose row is not below it.
+        int32_t b = lo, e_hi = hi;
+        while (b < e_hi) {
+            const int32_t mid = b + ((e_hi - b) >> 1);
+            if ((int)((a.entries[mid] >> 24) & (PF_BN - 1)) < tid) b = mid + 1;
+            else e_hi = mid;
+        }
+        for (int32_t e = b; e < hi; e++) {
+            const uint32_t w = a.entries[e];
+            if ((int)((w >> 24) & (PF_BN - 1)) != tid) break;
+            fold_fast<XB>(Bs, trash, w, true, a.alpha);
+        }
     }
 }
 

@@ -600,6 +600,26 @@ def test_deterministic(c2):
     assert np.array_equal(a, b)
 
 
+def test_prefill_fold_is_deterministic_with_duplicate_columns():
+    """A CSR whose rows repeat columns (a non-canonical plan): the prefill
+    fold adds each row's entries in plan order from one thread, so repeated
+    calls give the same bits (and still match the oracle)."""
+    rng = np.random.default_rng(11)
+    K, N = 1024, 256
+    L = W.make_layer(K, N, 128, 0.0, seed=111)
+    counts = rng.integers(0, 40, size=N)
+    rp = np.zeros(N + 1, np.int32)
+    rp[1:] = np.cumsum(counts)
+    col = rng.integers(0, 24, size=rp[-1]).astype(np.int32)  # every row repeats columns
+    vals = rng.normal(0, 0.05, rp[-1]).astype(np.float16)
+    lay = W.Layer(K, N, L.q, L.scales, rp, col, vals)
+    x = W.make_x(512, K, 3300)
+    ys = [run(lay, x, 1.0, plan=True) for _ in range(4)]
+    assert all(k == "prefill" for _, k in ys)
+    for y, _ in ys[1:]:
+        assert np.array_equal(y.view(np.uint32), ys[0][0].view(np.uint32))
+
+
 def test_empty_batch_is_a_no_op():
     L = W.make_layer(256, 64, 128, 0.02, seed=7)
     y, k = run(L, np.zeros((0, 256), np.float16), 1.0)
