@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import collections
 import ctypes
+import os
 import weakref
 
 import torch
@@ -42,7 +43,8 @@ _DT = {torch.float16: _lib.DT_F16, torch.bfloat16: _lib.DT_BF16, torch.float32: 
 # forward_layer and make_layer (descriptor reuse for OrthoLinear) stay internal;
 # forward_group takes make_layer descriptors (OrthoLinear.forward_group wraps it)
 __all__ = ["forward", "forward_planned", "forward_group", "build_plan", "dequant", "pack_base", "pack_csr", "sieve_quantize",
-           "sieve_split", "sieve_hdiag", "last_kernel", "set_kernel_policy", "get_kernel_policy", "device_info"]
+           "sieve_split", "sieve_hdiag", "last_kernel", "set_kernel_policy", "get_kernel_policy", "device_info",
+           "plan_cache_clear", "plan_cache_limit", "plan_cache_info"]
 
 
 def _req(cond: bool, msg: str) -> None:
@@ -144,11 +146,51 @@ def forward(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, 
     builds it, later calls take the planned kernels (at 2,048 tokens of c3
     ~100 instead of ~163 µs an eager call, which otherwise builds a
     temporary plan each time). Results are those of ``forward_planned`` with
-    that plan; calls under graph capture take none."""
+    that plan; calls under graph capture take none.
+
+    The first call on a weight set blocks until its plan is built (the build
+    reads the plan's flags back to the host).  The cache holds up to 4,096
+    plans and 8 GiB of device memory (a plan is ~12 % of its INT4 weights),
+    least recently used out; :func:`plan_cache_limit` changes the bounds (0
+    entries: no cache, every call reads the CSR), :func:`plan_cache_clear`
+    frees it, :func:`plan_cache_info` reports it."""
     plan = _PLANS.lookup((q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr), input,
                          alpha)
+    T = _lib.torch_ops()
+    if T is not None:
+        T.forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input, output,
+                          float(alpha), plan)
+        return
     forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input,
                     output, alpha, plan)
+
+
+def plan_cache_clear() -> None:
+    """Drops every plan the 8-argument :func:`forward` keeps (their device
+    memory is freed once the streams that used them are done with it)."""
+    _PLANS.clear()
+
+
+def plan_cache_limit(entries=None, max_bytes=None) -> tuple:
+    """Sets the bounds of the 8-argument :func:`forward`'s plan cache (None
+    keeps a bound) and returns them as (entries, bytes); least recently used
+    plans beyond the new bounds are dropped at once.  Defaults: 4,096 plans
+    and 8 GiB, or the environment's LIBORTHO_PLAN_CACHE_ENTRIES and
+    LIBORTHO_PLAN_CACHE_BYTES; entries=0 turns the cache off."""
+    if entries is not None:
+        _req(int(entries) >= 0, "entries must be >= 0")
+        _PLANS.max_entries = int(entries)
+    if max_bytes is not None:
+        _req(int(max_bytes) >= 0, "max_bytes must be >= 0")
+        _PLANS.max_bytes = int(max_bytes)
+    _PLANS.trim()
+    return _PLANS.max_entries, _PLANS.max_bytes
+
+
+def plan_cache_info() -> dict:
+    """Entries and device bytes the 8-argument :func:`forward`'s plan cache holds, and its bounds."""
+    return {"entries": len(_PLANS), "bytes": _PLANS._bytes, "max_entries": _PLANS.max_entries,
+            "max_bytes": _PLANS.max_bytes}
 
 
 class _PlanCache:
@@ -172,6 +214,8 @@ class _PlanCache:
     def __init__(self):
         self._d = collections.OrderedDict()
         self._bytes = 0
+        self.max_entries = int(os.environ.get("LIBORTHO_PLAN_CACHE_ENTRIES", self.MAX))
+        self.max_bytes = int(os.environ.get("LIBORTHO_PLAN_CACHE_BYTES", self.MAX_BYTES))
 
     def __len__(self):
         return len(self._d)
@@ -179,6 +223,10 @@ class _PlanCache:
     def clear(self):
         self._d.clear()
         self._bytes = 0
+
+    def trim(self):
+        while self._d and (len(self._d) > self.max_entries or self._bytes > self.max_bytes):
+            self._drop(next(iter(self._d)))
 
     def _drop(self, key):
         e = self._d.pop(key, None)
@@ -201,6 +249,8 @@ class _PlanCache:
             return None
         if torch.cuda.is_current_stream_capturing():
             return None  # a graph would keep the pointer of a plan this cache may free
+        if self.max_entries == 0:
+            return None
         e = self._d.get(key)
         if e is not None:
             r = e["refs"]
@@ -234,7 +284,7 @@ class _PlanCache:
         self._d[key] = {"refs": tuple(weakref.ref(t, drop) for t in ts), "sig": self._sig(ts), "plan": plan,
                         "event": ev, "streams": {_raw_stream(dev)}}
         self._bytes += plan.numel()
-        while len(self._d) > 1 and (len(self._d) > self.MAX or self._bytes > self.MAX_BYTES):
+        while len(self._d) > 1 and (len(self._d) > self.max_entries or self._bytes > self.max_bytes):
             self._drop(next(iter(self._d)))
         return plan
 
@@ -247,6 +297,11 @@ def forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_r
     """``forward`` with an ortho plan from :func:`build_plan` (or None) and,
     optionally, the bias [N] fused into the store (the bits of ``output +=
     bias`` after the kernel)."""
+    T = _lib.torch_ops()
+    if T is not None:
+        T.forward_planned(q_weight, q_scales, ortho_values, ortho_col_indices, ortho_row_ptr, input, output,
+                          float(alpha), plan, bias)
+        return
     _check_io(input, output)
     K, N = int(input.shape[1]), int(output.shape[1])
     dev = input.device

@@ -113,6 +113,28 @@ def lib():
     return _lib
 
 
+_torch_ops = None
+_torch_ops_tried = False
+
+
+def torch_ops():
+    """The compiled torch binding (libortho_amd/_torch_ops*.so, built by
+    libortho_amd.build beside libortho_amd.so), or None when it is absent:
+    the ctypes calls of this module then serve the same entry points."""
+    global _torch_ops, _torch_ops_tried
+    if not _torch_ops_tried:
+        with _lock:
+            if not _torch_ops_tried:
+                lib()  # the binding links libortho_amd.so: load (and check) it first
+                try:
+                    from . import _torch_ops as T
+                    _torch_ops = T if T.abi_version() == lib().orth_hip_abi_version() else None
+                except ImportError:
+                    _torch_ops = None
+                _torch_ops_tried = True
+    return _torch_ops
+
+
 class OrthoError(RuntimeError):
     """A C-ABI call returned a status other than ORTH_OK."""
 

@@ -4,8 +4,11 @@ C ABI of include/orth_hip.h) in-tree with hipcc.
     python -m libortho_amd.build          # or: python libortho_amd/build.py
 
 Every .hip file under csrc/ is compiled for gfx950 only and linked into one
-shared library.  No torch headers are involved: the Python side binds the
-plain C ABI with ctypes.
+shared library.  No torch headers are involved there: the Python side binds
+the plain C ABI with ctypes.  csrc/torch_ops.cpp, host code only, is then
+compiled with g++ against torch's headers into the compiled binding
+libortho_amd/_torch_ops*.so (the eager calls' fast path), linked to
+libortho_amd.so.
 """
 from __future__ import annotations
 
@@ -79,6 +82,34 @@ def build(verbose: bool = False, changed_only: bool = False) -> str:
     return LIB
 
 
+def build_torch_ops(verbose: bool = False) -> str:
+    """Compile csrc/torch_ops.cpp (host C++, torch extension) in-tree."""
+    import sysconfig
+    import torch
+    import torch.utils.cpp_extension as ce
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    out = os.path.join(HERE, "_torch_ops" + suffix)
+    src = os.path.join(CSRC, "torch_ops.cpp")
+    inc = [f"-I{p}" for p in ce.include_paths()] + [f"-I{sysconfig.get_paths()['include']}",
+                                                      "-I/opt/rocm/include", f"-I{os.path.join(ROOT, 'include')}"]
+    libdirs = ce.library_paths()
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = ["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-w", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=_torch_ops",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", *inc, src, "-o", out + ".tmp",
+           *[f"-L{d}" for d in libdirs], "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+           f"-L{HERE}", "-l:libortho_amd.so", "-Wl,-rpath,$ORIGIN",
+           *[f"-Wl,-rpath,{d}" for d in libdirs], "-L/opt/rocm/lib", "-lamdhip64"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch binding build failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(out + ".tmp", out)
+    if verbose:
+        print("built", out)
+    return out
+
+
 if __name__ == "__main__":
     build(verbose=True, changed_only="--changed" in sys.argv)
+    build_torch_ops(verbose=True)
     sys.exit(0)

@@ -162,13 +162,17 @@ class OrthoLinear(nn.Module):
         stream other than the one that built it waits on the build once, and
         the plan's memory is recorded on it (so a rebuilt plan's old memory
         is not reused before that stream's work is done).  Under graph
-        capture the plan is used as is (torch.cuda.graph synchronises the
-        device before capturing)."""
+        capture a valid plan is used as is (torch.cuda.graph synchronises
+        the device before capturing); a missing or stale one is not built
+        there (building reads the plan's flags back, a synchronisation a
+        capture does not allow): the captured call reads the CSR instead."""
         if self.ortho_values.numel() == 0 or not self.ortho_values.is_cuda:
             return None
         key = self._csr_key()
         dev = self.ortho_values.get_device()
         if not self._plan_valid(key):
+            if torch.cuda.is_current_stream_capturing():
+                return None
             self._plan = _C.build_plan(self.base_weight, self.base_scales, self.ortho_values,
                                        self.ortho_col_indices, self.ortho_row_ptr, self.in_features)
             self._plan_key = key
@@ -218,6 +222,26 @@ class OrthoLinear(nn.Module):
 
     # --------------------------------------------------------------- forward
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        T = _lib.torch_ops()
+        if T is None:
+            return self._forward_ctypes(x)
+        if not x.is_cuda:
+            raise RuntimeError("OrthoLinear runs on a ROCm GPU only; move the module and the input "
+                               "to a cuda device (the reference's CPU branch returns uninitialised memory)")
+        plan = self._ortho_plan() if self.alpha > 0 else None
+        # the bias is fused into the kernel's store (same bits as `output +=
+        # bias`) unless autograd must see the add
+        b = self.bias
+        fuse = b is not None and not (torch.is_grad_enabled() and b.requires_grad) and b.device == x.device
+        output = T.linear(x.reshape(-1, self.in_features), self.base_weight, self.base_scales, self.ortho_values,
+                          self.ortho_col_indices, self.ortho_row_ptr, self.out_features, float(self.alpha), plan,
+                          b.detach() if fuse else None)
+        if b is not None and not fuse:
+            output += b
+        return output.view(*x.shape[:-1], self.out_features)
+
+    def _forward_ctypes(self, x: torch.Tensor) -> torch.Tensor:
+        """forward through the ctypes binding (when the compiled one is absent)."""
         original_shape = x.shape
         x_flat = x.reshape(-1, self.in_features)
         batch_size = x_flat.shape[0]
@@ -228,8 +252,6 @@ class OrthoLinear(nn.Module):
         plan = None
         if self.alpha > 0:
             plan = self._ortho_plan()
-        # the bias is fused into the kernel's store (same bits as `output +=
-        # bias`) unless autograd must see the add
         fuse = self.bias is not None and not (torch.is_grad_enabled() and self.bias.requires_grad) and \
             self.bias.device == x.device
         _C.forward_layer(self._layer_desc(x.device), x_flat.contiguous(), output, plan,

@@ -176,6 +176,33 @@ def _ortholinear(K, N, seed):
 
 
 @torch.no_grad()
+def test_ortholinear_captured_without_warm_up_reads_the_csr():
+    """A freshly loaded OrthoLinear captured with no eager call first: the
+    plan cannot be built under capture (the build reads its flags back), so
+    the captured forward reads the CSR; every replay equals an eager
+    unplanned call, and the module builds its plan on its next eager call."""
+    m = _ortholinear(4096, 1040, 6800)
+    x = torch.from_numpy(W.make_x(1, 4096, 6801)).cuda()
+    want = torch.empty(1, 1040, dtype=torch.float16, device="cuda")
+    _C_ops.forward_planned(m.base_weight, m.base_scales, m.ortho_values, m.ortho_col_indices, m.ortho_row_ptr,
+                           x, want, 1.0, None)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g, stream=s):
+        y = m(x)
+    assert m._plan is None
+    for _ in range(3):
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    m(x)
+    assert m._plan is not None
+
+
+@torch.no_grad()
 def test_ortholinear_plan_used_on_another_stream_and_by_a_copy():
     """OrthoLinear's own plan: a second stream waits on its build before the
     first use there; a deep copy of a module that has run a forward rebuilds
@@ -200,24 +227,56 @@ def test_ortholinear_plan_used_on_another_stream_and_by_a_copy():
         assert torch.equal(y.view(torch.int16), want.view(torch.int16))
 
 
-def test_bounds_evict_the_least_recently_used_plans(monkeypatch):
-    """At most MAX entries and MAX_BYTES of plans (here shrunk to 2 entries,
-    then to one plan's bytes); the byte count follows every drop."""
+def test_bounds_evict_the_least_recently_used_plans():
+    """At most max_entries and max_bytes of plans (here set to 2 entries,
+    then to one plan's bytes, through the public plan_cache_limit); the byte
+    count follows every drop."""
     sets = [W.to_device(W.make_layer(4096, 520, 128, 0.02, 6900 + i)) for i in range(3)]
     x = torch.from_numpy(W.make_x(1, 4096, 6910)).cuda()
-    monkeypatch.setattr(_C_ops._PlanCache, "MAX", 2)
-    for d in sets:
+    saved = _C_ops.plan_cache_limit()
+    _C_ops.plan_cache_clear()
+    try:
+        _C_ops.plan_cache_limit(entries=2)
+        for d in sets:
+            ref_forward(d, x, 1.0)
+        assert len(_C_ops._PLANS) == 2
+        plans = [e["plan"] for e in _C_ops._PLANS._d.values()]
+        assert _C_ops._PLANS._bytes == sum(p.numel() for p in plans)
+        assert _C_ops.plan_cache_info()["bytes"] == _C_ops._PLANS._bytes
+        ref_forward(sets[1], x, 1.0)  # most recent: sets 2, 1
+        ref_forward(sets[0], x, 1.0)  # rebuilt; evicts set 2
+        keys = [k[2] for k in _C_ops._PLANS._d]
+        assert keys == [id(sets[1]["vals"]), id(sets[0]["vals"])]
+        _C_ops.plan_cache_limit(max_bytes=plans[0].numel())  # trims at once to the newest
+        assert len(_C_ops._PLANS) == 1 and [k[2] for k in _C_ops._PLANS._d] == [id(sets[0]["vals"])]
+        ref_forward(sets[2], x, 1.0)  # over the byte bound: only the newest stays
+        assert len(_C_ops._PLANS) == 1 and [k[2] for k in _C_ops._PLANS._d] == [id(sets[2]["vals"])]
+        del sets, d  # (the loop variable holds the last set too)
+        gc.collect()
+        assert len(_C_ops._PLANS) == 0 and _C_ops._PLANS._bytes == 0
+    finally:
+        _C_ops.plan_cache_limit(*saved)
+
+
+def test_cache_off_and_clear():
+    """entries=0 turns the cache off (calls read the CSR, same results as
+    a planned call within one FP16 step); plan_cache_clear drops every plan."""
+    d = W.to_device(W.make_layer(4096, 520, 128, 0.02, 6950))
+    x = torch.from_numpy(W.make_x(1, 4096, 6951)).cuda()
+    saved = _C_ops.plan_cache_limit()
+    try:
         ref_forward(d, x, 1.0)
-    assert len(_C_ops._PLANS) == 2
-    plans = [e["plan"] for e in _C_ops._PLANS._d.values()]
-    assert _C_ops._PLANS._bytes == sum(p.numel() for p in plans)
-    ref_forward(sets[1], x, 1.0)  # most recent: sets 2, 1
-    ref_forward(sets[0], x, 1.0)  # rebuilt; evicts set 2
-    keys = [k[2] for k in _C_ops._PLANS._d]
-    assert keys == [id(sets[1]["vals"]), id(sets[0]["vals"])]
-    monkeypatch.setattr(_C_ops._PlanCache, "MAX_BYTES", plans[0].numel())
-    ref_forward(sets[2], x, 1.0)  # over the byte bound: only the newest stays
-    assert len(_C_ops._PLANS) == 1 and [k[2] for k in _C_ops._PLANS._d] == [id(sets[2]["vals"])]
-    del sets, d  # (the loop variable holds the last set too)
-    gc.collect()
-    assert len(_C_ops._PLANS) == 0 and _C_ops._PLANS._bytes == 0
+        assert _C_ops.plan_cache_info()["entries"] >= 1
+        _C_ops.plan_cache_clear()
+        assert _C_ops.plan_cache_info() == {"entries": 0, "bytes": 0, "max_entries": saved[0],
+                                            "max_bytes": saved[1]}
+        _C_ops.plan_cache_limit(entries=0)
+        y, _ = ref_forward(d, x, 1.0)
+        assert len(_C_ops._PLANS) == 0
+        _C_ops.plan_cache_limit(entries=saved[0])
+        y2, _ = ref_forward(d, x, 1.0)
+        torch.cuda.synchronize()
+        diff = (y.float() - y2.float()).abs()
+        assert float(diff.max()) <= float(y.float().abs().max()) * 2e-3
+    finally:
+        _C_ops.plan_cache_limit(*saved)
