@@ -123,12 +123,12 @@ def torch_ops():
     the ctypes calls of this module then serve the same entry points."""
     global _torch_ops, _torch_ops_tried
     if not _torch_ops_tried:
+        L = lib()  # the binding links libortho_amd.so: load (and check) it first, outside the lock
         with _lock:
             if not _torch_ops_tried:
-                lib()  # the binding links libortho_amd.so: load (and check) it first
                 try:
                     from . import _torch_ops as T
-                    _torch_ops = T if T.abi_version() == lib().orth_hip_abi_version() else None
+                    _torch_ops = T if T.abi_version() == L.orth_hip_abi_version() else None
                 except ImportError:
                     _torch_ops = None
                 _torch_ops_tried = True

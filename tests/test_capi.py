@@ -206,3 +206,15 @@ def test_policy_alpha_and_version(L):
     layer = fake_layer()
     L.orth_layer_hip_set_alpha(ctypes.byref(layer), -0.25)
     assert layer.alpha == -0.25
+
+
+def test_torch_binding_loads_first_in_a_fresh_process():
+    """The compiled binding as the first thing a process loads (it loads the
+    C library itself first): no lock re-entry, and it matches the ABI."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r); from libortho_amd import _lib; T = _lib.torch_ops(); "
+            "print('binding', T is not None and T.abi_version() == _lib.lib().orth_hip_abi_version())" % ROOT)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert "binding True" in r.stdout
