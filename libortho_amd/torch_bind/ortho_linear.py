@@ -106,6 +106,7 @@ class OrthoLinear(nn.Module):
             self.register_parameter("bias", None)
         self._plan = None
         self._plan_key = None
+        self._plan_fast = None
 
     def set_alpha(self, alpha: float):
         """The kill switch: the ortho term is applied iff alpha > 0."""
@@ -142,6 +143,7 @@ class OrthoLinear(nn.Module):
         self.ortho_values = values.to(device=device, dtype=torch.float16)
         self._plan = None
         self._plan_key = None
+        self._plan_fast = None
 
     # ------------------------------------------------------------------ plan
     def _csr_key(self):
@@ -188,6 +190,9 @@ class OrthoLinear(nn.Module):
                 st.wait_event(self._plan_event)
                 self._plan.record_stream(st)
                 self._plan_streams.add(cur)
+            if cur in self._plan_streams:
+                v, c, r = key[0]
+                self._plan_fast = (v, c, r, (v._version, v.data_ptr(), c._version, r._version), cur)
         return self._plan
 
     def _layer_desc(self, device):
@@ -205,6 +210,7 @@ class OrthoLinear(nn.Module):
     def _apply(self, fn, *args, **kwargs):
         self._plan = None
         self._plan_key = None
+        self._plan_fast = None
         self._desc_key = None
         return super()._apply(fn, *args, **kwargs)
 
@@ -218,6 +224,7 @@ class OrthoLinear(nn.Module):
             state.pop(k, None)
         state["_plan"] = None
         state["_plan_key"] = None
+        state["_plan_fast"] = None
         return state
 
     # --------------------------------------------------------------- forward
@@ -228,17 +235,31 @@ class OrthoLinear(nn.Module):
         if not x.is_cuda:
             raise RuntimeError("OrthoLinear runs on a ROCm GPU only; move the module and the input "
                                "to a cuda device (the reference's CPU branch returns uninitialised memory)")
-        plan = self._ortho_plan() if self.alpha > 0 else None
+        bufs = self._buffers
+        vals = bufs["ortho_values"]
+        plan = None
+        if self.alpha > 0 and vals.numel() > 0:
+            # fast path: the same CSR tensors, unchanged, on the stream that
+            # last used the plan; anything else goes through _ortho_plan
+            f = self.__dict__.get("_plan_fast")
+            if f is not None and f[0] is vals and f[1] is bufs["ortho_col_indices"] and \
+                    f[2] is bufs["ortho_row_ptr"] and f[3] == (vals._version, vals.data_ptr(), f[1]._version,
+                                                               f[2]._version) and \
+                    f[4] == _C._raw_stream(vals.get_device()):
+                plan = self._plan
+            else:
+                plan = self._ortho_plan()
         # the bias is fused into the kernel's store (same bits as `output +=
         # bias`) unless autograd must see the add
-        b = self.bias
+        b = self._parameters["bias"]
         fuse = b is not None and not (torch.is_grad_enabled() and b.requires_grad) and b.device == x.device
-        output = T.linear(x.reshape(-1, self.in_features), self.base_weight, self.base_scales, self.ortho_values,
-                          self.ortho_col_indices, self.ortho_row_ptr, self.out_features, float(self.alpha), plan,
+        x2 = x if x.dim() == 2 else x.reshape(-1, self.in_features)
+        output = T.linear(x2, bufs["base_weight"], bufs["base_scales"], vals, bufs["ortho_col_indices"],
+                          bufs["ortho_row_ptr"], self.out_features, float(self.alpha), plan,
                           b.detach() if fuse else None)
         if b is not None and not fuse:
             output += b
-        return output.view(*x.shape[:-1], self.out_features)
+        return output if x.dim() == 2 else output.view(*x.shape[:-1], self.out_features)
 
     def _forward_ctypes(self, x: torch.Tensor) -> torch.Tensor:
         """forward through the ctypes binding (when the compiled one is absent)."""
@@ -352,6 +373,7 @@ class OrthoLinear(nn.Module):
             self.ortho_row_ptr = torch.zeros(rp.numel(), dtype=torch.int32, device=dev)
         self._plan = None
         self._plan_key = None
+        self._plan_fast = None
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
                                       unexpected_keys, error_msgs)
 
