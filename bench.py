@@ -106,10 +106,11 @@ def cpu_baseline(layer, x, alpha, budget_s):
 
 def cpu_secondary(budget_s):
     """The same single-core restatement on c1 (4096 -> 4096, per-row
-    scales, M=1, alpha 1: the whole layer) and c3 (4096 -> 4096, M=2048,
-    alpha 1) timed on 8 of its 2048 tokens and scaled by 2048 / 8: each
-    token is an independent pass of the reference's loop over the weights
-    (/root/reference/src/ortho.c:352-398), so the time is linear in M."""
+    scales, M=1, alpha 1: the whole layer), c3 (4096 -> 4096, M=2048,
+    alpha 1) timed on 8 of its 2048 tokens and scaled by 2048 / 8 (each
+    token is an independent pass of the reference's loop over the weights,
+    /root/reference/src/ortho.c:352-398, so the time is linear in M), c2 at
+    4 and 16 tokens, c4 at 8, and the c5 block at 1 and 32 tokens."""
     from libortho_amd import workloads as W
     out = []
     c1 = W.config_layer("c1")
@@ -128,6 +129,39 @@ def cpu_secondary(budget_s):
                 "sample": f"{sub} of 2048 tokens, {n} timed calls of {t * 1e3:.1f} ms, scaled by 2048/{sub} "
                           "(linear extrapolation: the loop is per token)"})
     log(f"  cpu {out[-1]}")
+    # the other decode-sized configs (4, 5): c2 at 4 and
+    # 16 tokens, c4 at 8, and the Llama-2-7B block at 1 token (its seven
+    # projections back to back) and at 32 tokens (2 of the 32 tokens timed,
+    # scaled by 16: the loop is per token)
+    c2 = W.config_layer("c2")
+    for M in (4, 16):
+        t, n = cpu_baseline(c2, W.make_x(M, c2.K, 7100 + M), 1.0, budget_s / 12)
+        b = W.algorithmic_bytes(c2, M, 1.0)
+        out.append({"workload": f"c2 M={M} alpha=1", "ms_per_call": round(t * 1e3, 2), "GB/s": round(b / t / 1e9, 4),
+                    "cores": 1, "sample": f"whole layer, {n} timed calls"})
+        log(f"  cpu {out[-1]}")
+    c4 = W.config_layer("c4")
+    t, n = cpu_baseline(c4, W.make_x(8, c4.K, 7208), 1.0, budget_s / 12)
+    b = W.algorithmic_bytes(c4, 8, 1.0)
+    out.append({"workload": "c4 M=8 alpha=1", "ms_per_call": round(t * 1e3, 2), "GB/s": round(b / t / 1e9, 4),
+                "cores": 1, "sample": f"whole layer, {n} timed calls"})
+    log(f"  cpu {out[-1]}")
+    block = W.llama_block()
+    for M, sub in ((1, 1), (32, 2)):
+        tot, bytes_, flops = 0.0, 0, 0
+        ns = []
+        for lay in block:
+            t, n = cpu_baseline(lay, W.make_x(sub, lay.K, 7300 + lay.K), 1.0, budget_s / 40)
+            tot += t * M / sub
+            bytes_ += W.algorithmic_bytes(lay, M, 1.0)
+            flops += W.algorithmic_flops(lay, M, 1.0)
+            ns.append(n)
+        sample = ("seven projections, each timed whole" if sub == M else
+                  f"{sub} of {M} tokens per projection, scaled by {M}/{sub} (linear extrapolation: the loop is per token)")
+        out.append({"workload": f"c5 Llama-2-7B block M={M} alpha=1", "ms_per_call": round(tot * 1e3, 2),
+                    "GB/s": round(bytes_ / tot / 1e9, 4), "GFLOP/s": round(flops / tot / 1e9, 3), "cores": 1,
+                    "sample": f"{sample}; {min(ns)}-{max(ns)} timed calls per projection"})
+        log(f"  cpu {out[-1]}")
     return out
 
 
