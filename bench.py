@@ -220,6 +220,7 @@ def time_workload(torch, layer, M, alpha, steps, warmup, plan=False, steady=Fals
     the activations' and output's dtype (FP16 unless given)."""
     from libortho_amd import _C_ops, workloads as W
     dtype = dtype or torch.float16
+    log(f"  [start {layer.name or f'{layer.K}->{layer.N}'} M={M} alpha={alpha} {str(dtype)[6:]} plan={plan}]")
     rot = Rotation(layer, torch, plan=plan)
     x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda().to(dtype)
     y = torch.empty(M, layer.N, dtype=dtype, device="cuda")
@@ -241,8 +242,7 @@ def time_workload(torch, layer, M, alpha, steps, warmup, plan=False, steady=Fals
         with torch.cuda.stream(s):
             rot.call(0, x, y, alpha)
         torch.cuda.current_stream().wait_stream(s)
-        # captured on the warmed-up stream: a library workspace it owns is
-        # reused by the graph instead of stream-ordered allocations
+        # captured on the warmed-up stream, as torch's graph capture asks
         with torch.cuda.graph(g, stream=s):
             for i in range(STEADY_STEPS):
                 rot.call(i, x, y, alpha)
@@ -399,6 +399,7 @@ def time_block(torch, M, steps, grouped=False):
     one orth_layers_forward_hip call (one launch at decode sizes).  Returns
     ms per block, algorithmic bytes and flops, and the kernels of the last
     step."""
+    log(f"  [start c5 block M={M} grouped={grouped}]")
     from libortho_amd import _C_ops, workloads as W
     layers = W.llama_block()
     per = sum(W.algorithmic_bytes(l, 0, 1.0) for l in layers)
@@ -434,6 +435,7 @@ def time_dropin(torch, layer, M, alpha, calls, graph_steps=0):
     with graph_steps, also the per-launch time of that many calls captured in
     a graph (weights rotated as in time_workload; captured calls take no
     plan, so this is the CSR-reading path)."""
+    log(f"  [start 8-argument forward {layer.name} M={M} graph_steps={graph_steps}]")
     import time as _t
     import libortho._C_ops as C
     from libortho_amd import workloads as W
@@ -471,6 +473,7 @@ def time_pack(torch, steps=30):
     INT4 base packing with group-128 and per-row scales, and the CSR of a
     1 % matrix (row counts + scan, then the fill).  Returns secondary
     entries; algorithmic bytes read W once and write each output once."""
+    log("  [start packing kernels]")
     import ctypes
     from libortho_amd import _lib
     L = _lib.lib()
@@ -530,6 +533,7 @@ def time_module(torch, calls=300):
     checks, plan-cache lookup, launch) and the GPU time per call (HIP
     events around the same loop).  The layer is loaded from a
     reference-layout state_dict of the c2 buffers."""
+    log("  [start OrthoLinear.forward eager]")
     import gc
     import time as _t
     from libortho_amd import OrthoLinear, workloads as W

@@ -234,40 +234,79 @@ int current_device_ok(int *dev_out) {
     return ORTH_OK;
 }
 
-// Split-K workspace of the mid-batch kernel, one per (device, stream): the
-// FP32 partials its reduction kernel sums.  Calls on one stream are ordered;
-// calls on different streams use different workspaces.  Allocation happens
-// on first use (and on growth) outside graph capture.  A captured call
-// always gets a stream-ordered workspace of its own (hipMallocAsync before
-// the launch, hipFreeAsync after it, both recorded in the graph and owned
-// by it): a graph may be replayed on any stream, concurrently with eager
-// calls on the stream it was captured on, so it never shares a stream's
-// workspace.
+// Split-K workspace of the mid-batch kernels, one per (device, stream): the
+// FP32 partials their reduction kernel sums.  Calls on one stream are
+// ordered; calls on different streams use different workspaces.  Allocation
+// happens on first use (and on growth), outside graph capture only.
+//
+// A captured call records no allocation: its partials (or the temporary
+// plan of an unplanned prefill call) go to the device's scratch array when
+// they fit it, else to the capturing stream's capture buffer, which eager
+// calls on that stream size (allocated only for requests larger than the
+// scratch array), else the call is refused.  Eager calls never touch either,
+// so a graph replayed on any stream, beside eager calls on any stream, does
+// not race with them; replays of graphs that overlap one another, or
+// no-allocation calls, on the same GPU share that memory and must be
+// ordered by the caller.
 struct Workspace {
     void *buf = nullptr;
     int64_t part_bytes = 0;
+    void *cap = nullptr;  // capture buffer
+    int64_t cap_bytes = 0;
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, void *>, Workspace> g_ws;
 std::vector<void *> g_ws_retired;
 
-// *part: the workspace; *temp: true when it is stream-ordered memory the
-// caller must release with hipFreeAsync after the launch.
-int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part, bool *temp) {
-    *temp = false;
+int capturing(hipStream_t stream, bool *cap) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     hipError_t e = hipStreamIsCapturing(stream, &cs);
     if (e != hipSuccess) return fail_hip(e, "hipStreamIsCapturing");
-    if (cs != hipStreamCaptureStatusNone) {
-        void *tmp = nullptr;
-        e = hipMallocAsync(&tmp, (size_t)part_bytes, stream);
-        if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (mid-batch workspace in a captured graph)");
-        *part = static_cast<float *>(tmp);
-        *temp = true;
+    *cap = cs != hipStreamCaptureStatusNone;
+    return ORTH_OK;
+}
+
+// Memory for a captured call (see above): *out, or ORTH_ERR_UNSUPPORTED.
+int capture_memory(int dev, hipStream_t stream, int64_t bytes, const char *what, void **out) {
+    if (bytes <= (int64_t)ORTH_NOALLOC_SCRATCH_BYTES) {
+        *out = g_dev[dev].scratch;
         return ORTH_OK;
     }
     std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto it = g_ws.find({dev, static_cast<void *>(stream)});
+    if (it != g_ws.end() && it->second.cap && it->second.cap_bytes >= bytes) {
+        *out = it->second.cap;
+        return ORTH_OK;
+    }
+    return fail(ORTH_ERR_UNSUPPORTED,
+                "a captured call needs %lld bytes of %s, more than the %lld-byte scratch array; run the same call "
+                "once outside capture on the capturing stream first (it sizes that stream's capture buffer)",
+                (long long)bytes, what, (long long)ORTH_NOALLOC_SCRATCH_BYTES);
+}
+
+int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part) {
+    bool cap = false;
+    int rc = capturing(stream, &cap);
+    if (rc != ORTH_OK) return rc;
+    if (cap) {
+        void *p = nullptr;
+        rc = capture_memory(dev, stream, part_bytes, "split-K workspace", &p);
+        *part = static_cast<float *>(p);
+        return rc;
+    }
+    std::lock_guard<std::mutex> lk(g_ws_mu);
     Workspace &w = g_ws[{dev, static_cast<void *>(stream)}];
+    hipError_t e = hipSuccess;
+    if (part_bytes > (int64_t)ORTH_NOALLOC_SCRATCH_BYTES && w.cap_bytes < part_bytes) {
+        // a capture of this call on this stream will find a buffer (an older,
+        // smaller one is retired: graphs captured earlier may still use it)
+        if (w.cap) g_ws_retired.push_back(w.cap);
+        w.cap = nullptr;
+        w.cap_bytes = 0;
+        e = hipMalloc(&w.cap, (size_t)part_bytes);
+        if (e != hipSuccess) return fail_hip(e, "hipMalloc (capture buffer)");
+        w.cap_bytes = part_bytes;
+    }
     if (w.buf && w.part_bytes >= part_bytes) {
         *part = static_cast<float *>(w.buf);
         return ORTH_OK;
@@ -275,7 +314,8 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part,
     if (w.buf) {
         // a smaller buffer is retired, not freed: in-flight work may still use it
         g_ws_retired.push_back(w.buf);
-        w = Workspace();
+        w.buf = nullptr;
+        w.part_bytes = 0;
     }
     e = hipMalloc(&w.buf, (size_t)part_bytes);
     if (e != hipSuccess) return fail_hip(e, "hipMalloc (mid-batch workspace)");
@@ -414,7 +454,6 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
         const bool qk = kernel == KERNEL_QUARTER;
         const int64_t pbytes = qk ? quarter_workspace_bytes(a) : skinny_workspace_bytes(a, cus);
         float *part = nullptr;
-        bool temp = false;
         if (pbytes > 0 && noalloc) {
             if (pbytes > (int64_t)ORTH_NOALLOC_SCRATCH_BYTES)
                 return fail(ORTH_ERR_UNSUPPORTED,
@@ -423,16 +462,12 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
                             (long long)ORTH_NOALLOC_SCRATCH_BYTES);
             part = static_cast<float *>(g_dev[dev].scratch);
         } else if (pbytes > 0) {
-            rc = workspace_for(dev, stream, pbytes, &part, &temp);
+            rc = workspace_for(dev, stream, pbytes, &part);
             if (rc != ORTH_OK) return rc;
         }
         // without a plan the split-K kernel filters each row's CSR by column
         e = qk ? launch_quarter(a, a.has_ortho ? plan : nullptr, part, stream)
                : launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
-        if (temp) {
-            hipError_t f = hipFreeAsync(part, stream);
-            if (e == hipSuccess) e = f;
-        }
     } else if (kernel == KERNEL_PREFILL) {
         if (a.has_ortho && !plan && noalloc) {
             // the prefill part of a plan, built in the scratch array
@@ -445,10 +480,23 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
             e = launch_plan_build_prefill(a, g_dev[dev].scratch, stream);
             if (e == hipSuccess) e = launch_prefill(a, g_dev[dev].scratch, stream);
         } else if (a.has_ortho && !plan) {
-            // stream-ordered temporary plan (its prefill part): allocated,
-            // built, used and freed in stream order, so the call stays
-            // asynchronous
+            // temporary plan (its prefill part).  Under capture: in the
+            // memory of captured calls (no allocation is recorded).  Else
+            // stream-ordered: allocated, built, used and freed in stream
+            // order, so the call stays asynchronous.
             const int64_t pb = plan_prefill_bytes(a.N, a.K, a.nnz);
+            bool cap = false;
+            rc = capturing(stream, &cap);
+            if (rc != ORTH_OK) return rc;
+            if (cap) {
+                void *p = nullptr;
+                rc = capture_memory(dev, stream, pb, "temporary ortho plan (pass a plan to capture this call)", &p);
+                if (rc != ORTH_OK) return rc;
+                e = launch_plan_build_prefill(a, p, stream);
+                if (e == hipSuccess) e = launch_prefill(a, p, stream);
+                if (e != hipSuccess) return fail_hip(e, "kernel launch");
+                return ORTH_OK;
+            }
             void *tmp = nullptr;
             e = hipMallocAsync(&tmp, (size_t)pb, stream);
             if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (temporary ortho plan)");

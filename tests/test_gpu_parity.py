@@ -671,7 +671,7 @@ def test_plan_cache_follows_replaced_csr_buffers(oracle_mod):
 def test_mid_batch_forward_captured_on_a_fresh_stream(c2, M):
     """A mid-batch forward captured in a HIP graph on a stream that never
     ran it eagerly (M = 8: the one-launch kernel; M = 32: the quarter-split
-    kernel, its workspace allocated inside the graph), replayed several times with
+    kernel, its partials in the GPU's scratch array), replayed several times with
     eager forwards of other shapes between the replays: every replay equals
     the eager result bit for bit."""
     d = W.to_device(c2)

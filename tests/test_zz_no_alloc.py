@@ -4,8 +4,9 @@ stream-ordered allocations), through the C ABI: same bits, on two calls in
 a row with the second smaller, for each kernel that uses scratch (the
 mid-batch split-K partials; the prefill plan built for an unplanned
 alpha > 0 call) and for decode; and a request beyond the scratch size is
-refused before anything is launched.  Captured into a graph, a no-allocation
-call adds kernel nodes only (the allocating entry adds memory nodes); calls
+refused before anything is launched.  Captured into a graph, a call of
+either entry adds kernel nodes only (no allocation node), and a captured
+call beyond the scratch size needs an eager call on its stream first; calls
 on two streams of one GPU are ordered by the library, so they do not race on
 the shared scratch."""
 import ctypes
@@ -104,20 +105,30 @@ def _hip():
     for name, args in (("hipStreamCreate", [P(V)]), ("hipStreamDestroy", [V]),
                        ("hipStreamBeginCapture", [V, ctypes.c_int]), ("hipStreamEndCapture", [V, P(V)]),
                        ("hipGraphGetNodes", [V, P(V), P(ctypes.c_size_t)]),
-                       ("hipGraphNodeGetType", [V, P(ctypes.c_int)]), ("hipGraphDestroy", [V])):
+                       ("hipGraphNodeGetType", [V, P(ctypes.c_int)]), ("hipGraphDestroy", [V]),
+                       ("hipStreamSynchronize", [V]), ("hipGraphInstantiate", [P(V), V, V, ctypes.c_char_p, ctypes.c_size_t]),
+                       ("hipGraphLaunch", [V, V]), ("hipGraphExecDestroy", [V])):
         getattr(h, name).argtypes = args
         getattr(h, name).restype = ctypes.c_int
     return h
 
 
-def captured_node_types(entry, desc, x, y):
+def captured_node_types(entry, desc, x, y, warm=False, replay=None):
     """Types of the nodes one call of `entry` adds to a graph captured on a
-    fresh stream."""
+    fresh stream (with ``warm``, after the same call made eagerly on that
+    stream).  With ``replay`` (an output tensor like y), the graph is also
+    instantiated and launched once with y as its output, then y is copied
+    into ``replay``."""
     h = _hip()
     s = ctypes.c_void_p()
     assert h.hipStreamCreate(ctypes.byref(s)) == 0
     g = ctypes.c_void_p()
+    ex = ctypes.c_void_p()
     try:
+        if warm:
+            _lib.check(getattr(_lib.lib(), entry)(ctypes.byref(desc), None, 0, None, 0, _p(x), _p(y),
+                                                  int(x.shape[0]), _lib.DT_F16, s))
+            assert h.hipStreamSynchronize(s) == 0
         assert h.hipStreamBeginCapture(s, 0) == 0  # global mode
         rc = getattr(_lib.lib(), entry)(ctypes.byref(desc), None, 0, None, 0, _p(x), _p(y), int(x.shape[0]),
                                         _lib.DT_F16, s)
@@ -132,8 +143,17 @@ def captured_node_types(entry, desc, x, y):
             t = ctypes.c_int(-1)
             assert h.hipGraphNodeGetType(ctypes.c_void_p(nd), ctypes.byref(t)) == 0
             types.append(t.value)
+        if replay is not None:
+            y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            assert h.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0) == 0
+            assert h.hipGraphLaunch(ex, s) == 0
+            assert h.hipStreamSynchronize(s) == 0
+            replay.copy_(y)
         return types
     finally:
+        if ex.value:
+            h.hipGraphExecDestroy(ex)
         if g.value:
             h.hipGraphDestroy(g)
         h.hipStreamDestroy(s)
@@ -152,10 +172,41 @@ def test_noalloc_capture_has_kernel_nodes_only(gpu, cfg, M, alpha, kernel):
     types = captured_node_types("orth_layer_forward_hip_noalloc", desc, x, y)
     assert _C_ops.last_kernel() == kernel
     assert types and all(t == _GRAPH_NODE_KERNEL for t in types), types
-    if kernel in ("skinny", "prefill", "quarter"):
-        # control: the allocating entry on a fresh capture stream records memory nodes
-        ctl = captured_node_types("orth_layer_forward_hip_ex", desc, x, y)
-        assert _GRAPH_NODE_MEM_ALLOC in ctl and _GRAPH_NODE_MEM_FREE in ctl, ctl
+    # the allocating entry records no allocation under capture either: on a
+    # fresh stream its partials (or temporary plan) go to the scratch array
+    y_eager = torch.empty_like(y)
+    _lib.check(call("orth_layer_forward_hip_ex", desc, x, y_eager))
+    y_graph = torch.empty_like(y)
+    ctl = captured_node_types("orth_layer_forward_hip_ex", desc, x, y, replay=y_graph)
+    assert ctl and all(t == _GRAPH_NODE_KERNEL for t in ctl), ctl
+    torch.cuda.synchronize()
+    assert torch.equal(y_graph.view(torch.int16), y_eager.view(torch.int16))
+
+
+def test_capture_beyond_the_scratch_needs_an_eager_call_first(gpu):
+    """A captured call whose partials exceed the scratch array (quarter-split
+    kernel, M = 32, N = 65600: 33.6 MB) is refused on a fresh stream; after
+    one eager call on the capture stream (which sizes that stream's capture
+    buffer) it captures as kernel nodes only, and the graph's output equals
+    the eager one."""
+    layer = W.make_layer(4096, 65600, 128, 0.0, seed=8800)
+    d = W.to_device(layer)
+    desc = _C_ops.make_layer(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], layer.K, layer.N, 0.0,
+                             torch.device("cuda:0"))
+    x = torch.from_numpy(W.make_x(32, layer.K, 8801)).cuda()
+    y = torch.empty(32, layer.N, dtype=torch.float16, device="cuda")
+    assert 4 * 32 * layer.N * 4 > _lib.lib().orth_noalloc_scratch_bytes()
+    y_eager = torch.empty_like(y)
+    _lib.check(call("orth_layer_forward_hip_ex", desc, x, y_eager))
+    assert _C_ops.last_kernel() == "quarter"
+    torch.cuda.synchronize()
+    with pytest.raises(_lib.OrthoError, match="capture buffer"):
+        captured_node_types("orth_layer_forward_hip_ex", desc, x, y)
+    y_graph = torch.empty_like(y)
+    types = captured_node_types("orth_layer_forward_hip_ex", desc, x, y, warm=True, replay=y_graph)
+    assert types and all(t == _GRAPH_NODE_KERNEL for t in types), types
+    torch.cuda.synchronize()
+    assert torch.equal(y_graph.view(torch.int16), y_eager.view(torch.int16))
 
 
 def test_noalloc_calls_on_two_streams_are_ordered(gpu):
