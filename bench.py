@@ -76,6 +76,11 @@ def parse():
     ap.add_argument("--profile-prefill", action="store_true",
                     help="six eager planned prefill forwards at c3 (M=2048, alpha=1), for counter passes "
                          "of rocprofv3 --pmc over the prefill kernel alone")
+    ap.add_argument("--profile-workload", metavar="NAME",
+                    help="eager launches of one workload for rocprofv3 (kernel trace or counters): "
+                         + ", ".join(PROFILE_WORKLOADS))
+    ap.add_argument("--profile-steps", type=int, default=50,
+                    help="forwards (blocks for c5) per --profile-workload run")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two --profile counter runs into profiles/traffic.json")
     return ap.parse_args()
@@ -624,6 +629,60 @@ def profile_run(torch):
                       "copy_bytes": COPY_BYTES}), flush=True)
 
 
+# --profile-workload names: layer, tokens, alpha (c5: the block, grouped or not)
+PROFILE_WORKLOADS = {
+    "c2_m1_a1": ("c2", 1, 1.0), "c2_m1_a0": ("c2", 1, 0.0), "c2_m2_a1": ("c2", 2, 1.0),
+    "c2_m4_a1": ("c2", 4, 1.0), "c2_m8_a1": ("c2", 8, 1.0), "c2_m16_a1": ("c2", 16, 1.0),
+    "c2_m32_a1": ("c2", 32, 1.0), "c2_m32_a0": ("c2", 32, 0.0), "c2_m2048_a1": ("c2", 2048, 1.0),
+    "c1_m1_a1": ("c1", 1, 1.0),
+    "c1_m1_a0": ("c1", 1, 0.0), "c3_m2048_a1": ("c3", 2048, 1.0), "c3_m2048_a0": ("c3", 2048, 0.0),
+    "c4_m8_a1": ("c4", 8, 1.0), "c5_m1": ("c5", 1, 1.0), "c5_m1_grouped": ("c5", 1, 1.0),
+    "c5_m32": ("c5", 32, 1.0), "c5_m32_grouped": ("c5", 32, 1.0), "copy": (None, 0, 0.0),
+}
+
+
+def profile_workload(torch, name, steps):
+    """Eager forwards of one workload (no graph: a kernel trace or counter
+    pass sees one dispatch per launch), each with its cached plan, weights
+    rotated past the Infinity Cache as in the timed runs; ``copy``: device
+    copies of COPY_BYTES (the FETCH_SIZE / WRITE_SIZE calibration)."""
+    from libortho_amd import _C_ops, workloads as W
+    cfg, M, alpha = PROFILE_WORKLOADS[name]
+    kernels = set()
+    if cfg is None:
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(steps):
+            dst.copy_(src)
+    elif cfg == "c5":
+        layers = W.llama_block()
+        per = sum(W.algorithmic_bytes(l, 0, 1.0) for l in layers)
+        copies = max(4, -(-ROTATE_MIN_BYTES // per))
+        rots = [Rotation(l, torch, min_copies=copies, min_bytes=0, plan=True) for l in layers]
+        xs = {K: torch.from_numpy(W.make_x(M, K, 7100 + K)).cuda() for K in {l.K for l in layers}}
+        ys = [torch.empty(M, l.N, dtype=torch.float16, device="cuda") for l in layers]
+        groups = [[0, 1, 2], [3], [4, 5], [6]] if name.endswith("grouped") else [[j] for j in range(len(layers))]
+        for i in range(steps):
+            for g in groups:
+                if len(g) == 1:
+                    rots[g[0]].call(i, xs[layers[g[0]].K], ys[g[0]], 1.0)
+                else:
+                    _C_ops.forward_group([rots[j].desc(i, 1.0) for j in g], xs[layers[g[0]].K], [ys[j] for j in g],
+                                         [rots[j].plans[i % rots[j].n] for j in g])
+                kernels.add(_C_ops.last_kernel())
+    else:
+        layer = W.config_layer(cfg)
+        rot = Rotation(layer, torch, plan=alpha > 0) if M < 2048 else \
+            Rotation(layer, torch, min_copies=2, min_bytes=0, plan=alpha > 0)
+        x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda()
+        y = torch.empty(M, layer.N, dtype=torch.float16, device="cuda")
+        for i in range(steps):
+            rot.call(i, x, y, alpha)
+            kernels.add(_C_ops.last_kernel())
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_workload": name, "steps": steps, "kernels": sorted(kernels)}), flush=True)
+
+
 def _pmc_rows(path, counter):
     import csv
     rows = []
@@ -723,6 +782,14 @@ def main():
     if args.profile:
         import torch
         profile_run(torch)
+        return
+    if args.profile_workload:
+        import torch
+        if args.profile_workload not in PROFILE_WORKLOADS:
+            print(f"bench.py: unknown workload {args.profile_workload!r}; one of {', '.join(PROFILE_WORKLOADS)}",
+                  file=sys.stderr)
+            sys.exit(2)
+        profile_workload(torch, args.profile_workload, args.profile_steps)
         return
     if args.profile_prefill:
         import torch

@@ -103,14 +103,16 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  *   output  [batch_size, out_features] of io_dtype, written in full
  * Picks, for FP16 I/O and the supported shapes, the decode kernel (batch <=
  * 4), the one-launch mid-batch kernel (5..16, K = 4096, a plan or no ortho
- * term), the quarter-split kernel (17..32, the same conditions), the
- * split-K mid-batch kernel (other batches up to 64), the MFMA prefill
+ * term), the slice-split kernel (17..32, K % 128 == 0, a plan or no ortho
+ * term), the quarter-split kernel (17..32, K = 4096, when the slice-split
+ * kernel cannot take the call), the split-K mid-batch kernel (other
+ * batches up to 64), the MFMA prefill
  * kernel (above), and a general kernel for shapes and dtypes the fast
  * kernels do not take (orth_hip_last_kernel() names the choice).  BF16 I/O
  * takes the decode kernel for 1..4 tokens and the one-launch mid-batch
  * kernel for 5..16 (both K = 4096 with a plan or no ortho term), the
- * quarter-split kernel for 17..32 (K = 4096, 256-word plan records or no
- * ortho term), the split-K mid-batch kernel for the other batches up to 64
+ * slice-split kernel for 17..32 (K % 128 == 0, a plan or no ortho term),
+ * the split-K mid-batch kernel for the other batches up to 64
  * (K % 128 == 0), the prefill kernel above; FP32 I/O the general kernel.  Kernels
  * that need scratch memory (split-K partials, a prefill plan when none is
  * given) take it from a per-stream workspace or stream-ordered allocations.
@@ -303,7 +305,8 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info);
 /* Kernel choice override for benchmarking and tests: 0 = automatic (the
  * default), 1 = decode, 2 = prefill, 3 = general, 4 = split-K mid-batch
  * (5..64 tokens), 5 = one-launch mid-batch (5..16 tokens), 6 = K quarters
- * over the grid (17..32 tokens).  A forced kernel that cannot take a call returns
+ * over the grid (17..32 tokens, K = 4096), 7 = 1024-column slices over the
+ * grid (1..32 tokens).  A forced kernel that cannot take a call returns
  * ORTH_ERR_UNSUPPORTED.  Process-wide. */
 int orth_hip_set_kernel_policy(int policy);
 int orth_hip_get_kernel_policy(void);
@@ -311,7 +314,8 @@ int orth_hip_get_kernel_policy(void);
 /* The kernel the calling thread's last successful forward launched:
  * 1 decode, 2 prefill, 3 general, 4 split-K mid-batch, 5 decode for a
  * group of layers in one launch (orth_layers_forward_hip), 6 one-launch
- * mid-batch, 7 K quarters over the grid, 0 none. */
+ * mid-batch, 7 K quarters over the grid, 8 1024-column slices over the
+ * grid, 0 none. */
 int orth_hip_last_kernel(void);
 
 /* Device clock stamp for timing stream-ordered work (benchmarks; no

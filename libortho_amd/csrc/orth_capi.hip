@@ -51,6 +51,9 @@ bool mid_supported(const ForwardArgs &a, const void *plan);
 bool quarter_supported(const ForwardArgs &a, const void *plan);
 int64_t quarter_workspace_bytes(const ForwardArgs &a);
 hipError_t launch_quarter(const ForwardArgs &a, const void *plan, float *part, hipStream_t stream);
+bool split_supported(const ForwardArgs &a, const void *plan);
+int64_t split_workspace_bytes(const ForwardArgs &a);
+hipError_t launch_split(const ForwardArgs &a, const void *plan, float *part, hipStream_t stream);
 hipError_t launch_mid(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream);
 bool skinny_supported(const ForwardArgs &a);
 int64_t skinny_workspace_bytes(const ForwardArgs &a, int cus);
@@ -82,6 +85,7 @@ int policy_from_env() {
     if (!std::strcmp(e, "skinny")) return 4;
     if (!std::strcmp(e, "mid")) return 5;
     if (!std::strcmp(e, "quarter")) return 6;
+    if (!std::strcmp(e, "split")) return 7;
     return 0;
 }
 
@@ -336,6 +340,7 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
     const bool sk_pref = sk_ok && (plan || !a.has_ortho || !dec_ok || a.M > 8);
     const bool mid_ok = mid_supported(a, a.has_ortho ? plan : nullptr);
     const bool qu_ok = quarter_supported(a, a.has_ortho ? plan : nullptr);
+    const bool sp_ok = split_supported(a, a.has_ortho ? plan : nullptr);
     switch (policy) {
         case 1:
             if (!dec_ok) return fail(ORTH_ERR_UNSUPPORTED, "decode kernel forced but it cannot take this call");
@@ -360,6 +365,10 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
             if (!qu_ok) return fail(ORTH_ERR_UNSUPPORTED, "quarter-split kernel forced but it cannot take this call");
             *kernel = KERNEL_QUARTER;
             break;
+        case 7:
+            if (!sp_ok) return fail(ORTH_ERR_UNSUPPORTED, "slice-split kernel forced but it cannot take this call");
+            *kernel = KERNEL_SPLIT;
+            break;
         default:
             // the one-launch mid-batch kernel beats the split-K one on every
             // shape both take (c2 M=8 alpha=1 10.3 against 14.4 us, M=16
@@ -367,6 +376,10 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
             if (dec_ok && a.M <= 4) *kernel = KERNEL_DECODE;
             else if (mid_ok) *kernel = KERNEL_MID;
             else if (qu_ok) *kernel = KERNEL_QUARTER;
+            // 17..32 tokens where the quarter-split kernel cannot go (K != 4096,
+            // BF16 with 512-word records): c5 down_proj M=32 23.7 against
+            // 35.5 us for the split-K kernel
+            else if (sp_ok && a.M > 16) *kernel = KERNEL_SPLIT;
             else if (sk_pref) *kernel = KERNEL_SKINNY;
             else if (dec_ok) *kernel = KERNEL_DECODE;
             else *kernel = pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL;
@@ -449,16 +462,16 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
         e = launch_decode(a, plan, g_dev[dev].cus, stream);
     } else if (kernel == KERNEL_MID) {
         e = launch_mid(a, a.has_ortho ? plan : nullptr, g_dev[dev].cus, stream);
-    } else if (kernel == KERNEL_SKINNY || kernel == KERNEL_QUARTER) {
+    } else if (kernel == KERNEL_SKINNY || kernel == KERNEL_QUARTER || kernel == KERNEL_SPLIT) {
         const int cus = g_dev[dev].cus;
-        const bool qk = kernel == KERNEL_QUARTER;
-        const int64_t pbytes = qk ? quarter_workspace_bytes(a) : skinny_workspace_bytes(a, cus);
+        const bool qk = kernel == KERNEL_QUARTER, sk = kernel == KERNEL_SPLIT;
+        const int64_t pbytes = qk ? quarter_workspace_bytes(a) : sk ? split_workspace_bytes(a) : skinny_workspace_bytes(a, cus);
         float *part = nullptr;
         if (pbytes > 0 && noalloc) {
             if (pbytes > (int64_t)ORTH_NOALLOC_SCRATCH_BYTES)
                 return fail(ORTH_ERR_UNSUPPORTED,
                             "the %s kernel needs %lld bytes of scratch for this call; the no-allocation "
-                            "entry point has %lld", qk ? "quarter-split" : "mid-batch", (long long)pbytes,
+                            "entry point has %lld", qk ? "quarter-split" : sk ? "slice-split" : "mid-batch", (long long)pbytes,
                             (long long)ORTH_NOALLOC_SCRATCH_BYTES);
             part = static_cast<float *>(g_dev[dev].scratch);
         } else if (pbytes > 0) {
@@ -467,7 +480,8 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
         }
         // without a plan the split-K kernel filters each row's CSR by column
         e = qk ? launch_quarter(a, a.has_ortho ? plan : nullptr, part, stream)
-               : launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
+            : sk ? launch_split(a, a.has_ortho ? plan : nullptr, part, stream)
+                 : launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
     } else if (kernel == KERNEL_PREFILL) {
         if (a.has_ortho && !plan && noalloc) {
             // the prefill part of a plan, built in the scratch array
@@ -861,7 +875,7 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info) {
 }
 
 int orth_hip_set_kernel_policy(int policy) {
-    if (policy < 0 || policy > 6) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..6");
+    if (policy < 0 || policy > 7) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..7");
     g_policy.store(policy);
     return ORTH_OK;
 }

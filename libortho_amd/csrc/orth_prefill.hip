@@ -40,9 +40,10 @@ namespace orth {
 //                                         columns of decode wave w), the rows' entries
 //                                         packed (cell records, see orth_common.h);
 //                                         Wq = 256 .. 2048 words, in pad[0]
-//   uint32 srecs[ceil(N/16)][K/1024][W]   (K % 1024 == 0) the same per 1024-column
-//                                         slice for the mid-batch kernel; W = 256 or
-//                                         512 words, in pad[1] (0: none)
+//   uint32 srecs[ceil(N/16)][ceil(K/1024)][W]  (K % 128 == 0) the same per 1024-column
+//                                         slice (the last one may be narrower) for the
+//                                         mid-batch kernels; W = 256 or 512 words, in
+//                                         pad[1] (0: none)
 // Entries of one (block, step) are ordered by row then by CSR position.  The
 // chunk table locates a row's entries of columns [128 c0, 128 c1) in the CSR
 // itself when the row's columns ascend strictly (flag kPlanUnsorted clear).
@@ -51,7 +52,7 @@ namespace orth {
 // is itself a load); a cell whose entries do not fit is read from the CSR.
 
 static const uint32_t kPlanMagic = 0x504f5254u;  // "TROP"
-static const uint32_t kPlanVersion = 4;
+static const uint32_t kPlanVersion = 5;
 static const int kPlanBN = 128;
 static const int kPlanBK = 64;
 static const uint32_t kPlanNonCanonical = 1u;  // duplicate or unsorted columns in a row
@@ -102,9 +103,10 @@ int plan_qrec_words(int64_t N, int64_t K, int64_t nnz) {
     return cell_words(N, K, nnz, (int64_t)decode_chunks_per_wave(K) * 128, 2048);
 }
 
-// mid-batch slices (K % 1024 == 0): 256 or 512 words
+// mid-batch slices of 1024 columns (K % 128 == 0; the last slice holds the
+// rest of K): 256 or 512 words
 int plan_srec_words(int64_t N, int64_t K, int64_t nnz) {
-    if (K % 1024 != 0) return 0;
+    if (K % 128 != 0) return 0;
     return cell_words(N, K, nnz, 1024, 512);
 }
 
@@ -118,7 +120,7 @@ int64_t plan_srec_at(int64_t N, int64_t K, int64_t nnz) {
 
 int64_t plan_bytes_for(int64_t N, int64_t K, int64_t nnz) {
     if (nnz <= 0) return 0;
-    return plan_srec_at(N, K, nnz) + ((N + 15) / 16) * (K / 1024) * (int64_t)plan_srec_words(N, K, nnz) * 4;
+    return plan_srec_at(N, K, nnz) + ((N + 15) / 16) * ((K + 1023) / 1024) * (int64_t)plan_srec_words(N, K, nnz) * 4;
 }
 
 // Largest K the plan builder's LDS counters take (int32 per (step, row)).
@@ -335,7 +337,7 @@ hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t strea
                            decode_chunks_per_wave(a.K) * 128, kCellQuarter);
     }
     if (swords > 0) {
-        const int nslices = (int)(a.K / 1024);
+        const int nslices = (int)((a.K + 1023) / 1024);
         uint32_t *srec = reinterpret_cast<uint32_t *>(static_cast<char *>(plan) + plan_srec_at(a.N, a.K, a.nnz));
         hipLaunchKernelGGL(plan_cell_kernel, dim3(ngroups * (unsigned)nslices), dim3(64), 0, stream, a, srec,
                            swords, nslices, 1024, kCellSlice);

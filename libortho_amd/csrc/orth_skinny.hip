@@ -65,7 +65,7 @@ __device__ __forceinline__ int quad_bcast(int x) {
     return __builtin_amdgcn_update_dpp(0, x, S | (S << 2) | (S << 4) | (S << 6), 0xf, 0xf, false);
 }
 constexpr uint32_t kSkPlanMagic = 0x504f5254u;
-constexpr uint32_t kSkPlanVersion = 4;
+constexpr uint32_t kSkPlanVersion = 5;
 constexpr uint32_t kSkPlanUnsorted = 4u;  // plan flag: the chunk table does not locate ranges
 
 // Chunks per slice the kernel of ntt token tiles is built for: even (group

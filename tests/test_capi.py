@@ -163,8 +163,9 @@ def qrec_words(N, K, nnz):
 
 
 def srec_words(N, K, nnz):
-    # mid-batch records: one per (16-row block, 1024-column slice)
-    return 0 if K % 1024 else cell_words(N, K, nnz, 1024, 512)
+    # mid-batch records: one per (16-row block, 1024-column slice; the last
+    # slice holds the rest of K)
+    return 0 if K % 128 else cell_words(N, K, nnz, 1024, 512)
 
 
 def test_plan_size(L):
@@ -188,6 +189,13 @@ def test_plan_size(L):
     assert srec_words(4096, 4096, 4096 * 4096 // 10) == 0
     # down_proj shape (K = 11008: quarters of 22 chunks, 2816 columns) at 1 %
     assert qrec_words(4096, 11008, 450888) == 768
+    # ... and its 11 slices (10 of 1024 columns, one of 768): 256 words each
+    assert srec_words(4096, 11008, 450888) == 256
+    n11 = L.orth_ortho_plan_bytes(ctypes.byref(fake_layer(K=11008, N=4096, nnz=450888)))
+    off11 = ((4096 // 128) * (11008 // 64 + 1) * 4 + 15) // 16 * 16
+    ch11 = (4096 * (11008 // 128 + 1) * 2 + 15) // 16 * 16
+    assert n11 == ((64 + off11 + 4 * 450888 + 15) // 16 * 16 + ch11 + (4096 // 16) * 4 * 768 * 4
+                   + (4096 // 16) * 11 * 256 * 4)
     assert qrec_words(4096, 11008, 2 * 450888) == 1280   # down_proj at 2 %
     assert qrec_words(4096, 4096, 4096 * 4096 // 10) == 2048
     assert qrec_words(4096, 4096, 4096 * 4096 // 5) == 0  # 20 %: the CSR path

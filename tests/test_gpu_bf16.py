@@ -207,7 +207,7 @@ def test_bf16_split_k_down_proj(oracle_mod, M, alpha):
     FP32 partials, a BF16 reduction)."""
     lay = {l.name: l for l in W.llama_block(case=1)}["down_proj"]
     x_np, xd = bf16_x(M, lay.K, 5600 + M)
-    y, k = run(lay, xd, alpha)
+    y, k = run(lay, xd, alpha, policy="skinny")  # (17..32 tokens take the slice-split kernel by default)
     assert k == "skinny"
     check(oracle_mod, lay, x_np, alpha, y, f"bf16 skinny down_proj M={M} alpha={alpha}")
     agree_with_general(lay, xd, alpha, y, f"bf16 skinny down_proj M={M}")
@@ -221,12 +221,12 @@ def test_bf16_split_k_bias_matches_the_unfused_add(oracle_mod, K, N, M):
     from oracle import pack_oracle as PO
     lay = W.make_layer(K, N, 128, 0.01, 5700 + N)
     x_np, xd = bf16_x(M, K, 5701 + M)
-    y0, k = run(lay, xd, 1.0)
+    y0, k = run(lay, xd, 1.0, policy="skinny")
     assert k == "skinny"
     check(oracle_mod, lay, x_np, 1.0, y0, f"bf16 skinny K={K} N={N} M={M}")
     for dt in (torch.bfloat16, torch.float32):
         b = (torch.randn(N, generator=torch.Generator(device="cpu").manual_seed(6)) * 0.5).to(dt).cuda()
-        y, kb = run(lay, xd, 1.0, bias=b)
+        y, kb = run(lay, xd, 1.0, policy="skinny", bias=b)
         assert kb == "skinny"
         want = PO.f32_to_bf16_bits(y0.astype(np.float32) + b.float().cpu().numpy()[None, :])
         got = torch.from_numpy(y).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
@@ -266,11 +266,11 @@ def test_bf16_quarter_shapes_and_bias(oracle_mod, N, group, M):
         assert np.array_equal(got, want)
 
 
-def test_bf16_quarter_leaves_larger_records_to_split_k(oracle_mod):
+def test_bf16_quarter_leaves_larger_records_to_the_slice_split(oracle_mod):
     """c5's q_proj (2 % ortho: 512-word records) at 32 BF16 tokens takes the
-    split-K kernel (the quarter kernel takes BF16 with 256-word records only)."""
+    slice-split kernel (the quarter kernel takes BF16 with 256-word records only)."""
     lay = {l.name: l for l in W.llama_block(case=1)}["q_proj"]
     x_np, xd = bf16_x(32, lay.K, 6000)
     y, k = run(lay, xd, 1.0)
-    assert k == "skinny"
+    assert k == "split"
     check(oracle_mod, lay, x_np, 1.0, y, "bf16 c5 q_proj M=32")

@@ -93,13 +93,16 @@ def auto_kernel(M, planned=False, K=4096):
     mid-batch kernels read the ortho plan, so without one (and with an ortho
     term) batches up to 8 stay on the decode kernel; with one (or without an
     ortho term) 5..16 tokens at K = 4096 take the one-launch kernel and
-    17..32 the quarter-split one."""
+    17..32 the quarter-split one (K = 4096) or the slice-split one (other
+    K)."""
     if M <= 4 or (M <= 8 and not planned):
         return "decode"
     if planned and M <= 16 and K == 4096:
         return "mid"
     if planned and M <= 32 and K == 4096:
         return "quarter"
+    if planned and 17 <= M <= 32 and K % 128 == 0:
+        return "split"
     return "skinny" if M <= 64 else "prefill"
 
 
