@@ -167,8 +167,14 @@ int64_t orth_noalloc_scratch_bytes(void);
  * the decode kernel with the same instantiation (the same in_features,
  * scale layout, ortho mode and plan record size) the layers share one
  * launch, each layer's output rows dealt to their own workgroups
- * (orth_hip_last_kernel() then returns 5); otherwise each layer is its own
- * forward call.  Outputs must not overlap.  No counterpart in the
+ * (orth_hip_last_kernel() then returns 5); at 17..32 tokens, when every
+ * layer takes the quarter- or slice-split kernel and the layers share K,
+ * scale layout, ortho class and record size, one slice-split launch and one
+ * reduction take them all (returns 9; each output then has the bits of
+ * that layer's slice-split call, kernel policy 7, which at K = 4096 differs
+ * from the default quarter-split call in FP32 summation order only);
+ * otherwise each layer is its own forward call.  Outputs must not overlap.
+ * No counterpart in the
  * reference, which calls its forward once per projection
  * (OrthoLinear.forward, /root/reference/torch_bind/ortho_linear.py:130-168, per module): for the
  * projections of one block that read one activation (q/k/v, gate/up) it
@@ -315,7 +321,7 @@ int orth_hip_get_kernel_policy(void);
  * 1 decode, 2 prefill, 3 general, 4 split-K mid-batch, 5 decode for a
  * group of layers in one launch (orth_layers_forward_hip), 6 one-launch
  * mid-batch, 7 K quarters over the grid, 8 1024-column slices over the
- * grid, 0 none. */
+ * grid, 9 the same for a group of layers in one launch, 0 none. */
 int orth_hip_last_kernel(void);
 
 /* Device clock stamp for timing stream-ordered work (benchmarks; no

@@ -54,6 +54,10 @@ hipError_t launch_quarter(const ForwardArgs &a, const void *plan, float *part, h
 bool split_supported(const ForwardArgs &a, const void *plan);
 int64_t split_workspace_bytes(const ForwardArgs &a);
 hipError_t launch_split(const ForwardArgs &a, const void *plan, float *part, hipStream_t stream);
+bool split_group_ok(const ForwardArgs *as, const void *const *plans, int count);
+int64_t split_group_workspace_bytes(const ForwardArgs *as, int count);
+hipError_t launch_split_group(const ForwardArgs *as, const void *const *plans, int count, float *part,
+                              hipStream_t stream);
 hipError_t launch_mid(const ForwardArgs &a, const void *plan, int cus, hipStream_t stream);
 bool skinny_supported(const ForwardArgs &a);
 int64_t skinny_workspace_bytes(const ForwardArgs &a, int cus);
@@ -581,6 +585,33 @@ int group_forward_impl(const orth_hip_layer_t *const *layers, const void *const 
         if (e != hipSuccess) return fail_hip(e, "kernel launch");
         t_last_kernel = KERNEL_DECODE_GROUP;
         return ORTH_OK;
+    }
+    // 17..32 tokens: one slice-split launch (and one reduction) for layers
+    // that each take a kernel of that range, when they share the launch's
+    // shape class (c5 q/k/v M=32: one launch instead of three)
+    bool split_all = count > 1 && (policy == 0 || policy == 7) && as[0].M > 16;
+    for (int l = 0; l < count && split_all; l++) {
+        int kernel = KERNEL_NONE;
+        rc = pick_kernel(as[l], pl[l], policy, &kernel);
+        if (rc != ORTH_OK) return rc;
+        split_all = kernel == KERNEL_QUARTER || kernel == KERNEL_SPLIT;
+    }
+    if (split_all) {
+        const void *spl[ORTH_GROUP_MAX];
+        for (int l = 0; l < count; l++) spl[l] = as[l].has_ortho ? pl[l] : nullptr;
+        if (split_group_ok(as, spl, count)) {
+            hipStream_t stream = static_cast<hipStream_t>(stream_v);
+            const int64_t pbytes = split_group_workspace_bytes(as, count);
+            float *part = nullptr;
+            if (pbytes > 0) {
+                rc = workspace_for(dev, stream, pbytes, &part);
+                if (rc != ORTH_OK) return rc;
+            }
+            hipError_t e = launch_split_group(as, spl, count, part, stream);
+            if (e != hipSuccess) return fail_hip(e, "kernel launch");
+            t_last_kernel = KERNEL_SPLIT_GROUP;
+            return ORTH_OK;
+        }
     }
     for (int l = 0; l < count; l++) {
         rc = forward_impl(layers[l], pl[l], pl[l] ? plan_bytes[l] : 0, input, outputs[l], batch, io_dtype, stream_v,

@@ -32,7 +32,8 @@ enum KernelId {
     KERNEL_DECODE_GROUP = 5,  // one decode launch for several layers
     KERNEL_MID = 6,           // one-launch mid-batch kernel (5..16 tokens)
     KERNEL_QUARTER = 7,       // K quarters over the grid (17..32 tokens)
-    KERNEL_SPLIT = 8          // 1024-column slices over the grid (17..32 tokens)
+    KERNEL_SPLIT = 8,         // 1024-column slices over the grid (17..32 tokens)
+    KERNEL_SPLIT_GROUP = 9    // the same for a group of layers in one launch
 };
 
 // Everything a forward launch needs, resolved on the host.

@@ -29,6 +29,11 @@ hipError_t launch_quarter(const ForwardArgs &, const void *, float *, hipStream_
 bool split_supported(const ForwardArgs &, const void *) { return false; }
 int64_t split_workspace_bytes(const ForwardArgs &) { return 0; }
 hipError_t launch_split(const ForwardArgs &, const void *, float *, hipStream_t) { return hipErrorInvalidValue; }
+bool split_group_ok(const ForwardArgs *, const void *const *, int) { return false; }
+int64_t split_group_workspace_bytes(const ForwardArgs *, int) { return 0; }
+hipError_t launch_split_group(const ForwardArgs *, const void *const *, int, float *, hipStream_t) {
+    return hipErrorInvalidValue;
+}
 hipError_t launch_mid(const ForwardArgs &, const void *, int, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_decode_group(const ForwardArgs *, const void *const *, int, int, hipStream_t) {
     return hipErrorInvalidValue;

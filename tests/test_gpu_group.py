@@ -1,9 +1,10 @@
 """Grouped forward (orth_layers_forward_hip): the projections of one
 Llama-2-7B block that read one activation (q/k/v, gate/up) in one decode
-launch.  Each output must have the bits of that layer's own forward call
-(the same kernel arithmetic per workgroup), and be within the parity bar of
-the FP64 oracle; groups the decode kernel cannot share fall back to one call
-per layer with the same results."""
+launch, and at 17..32 tokens in one slice-split launch.  Each output must
+have the bits of that layer's own forward call with the same kernel (the
+same arithmetic per workgroup), and be within the parity bar of the FP64
+oracle; groups that cannot share a launch fall back to one call per layer
+with the same results."""
 import numpy as np
 import pytest
 import torch
@@ -34,17 +35,21 @@ def desc(l, d, alpha):
                              torch.device("cuda:0"))
 
 
-def separate(l, d, x, alpha, plan, bias=None):
-    y = torch.full((x.shape[0], l.N), float("nan"), dtype=torch.float16, device="cuda")
-    _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y, alpha,
-                           d["plan"] if plan else None, bias)
+def separate(l, d, x, alpha, plan, bias=None, policy="auto"):
+    y = torch.full((x.shape[0], l.N), float("nan"), dtype=x.dtype, device="cuda")
+    _lib.set_kernel_policy(policy)
+    try:
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y, alpha,
+                               d["plan"] if plan else None, bias)
+    finally:
+        _lib.set_kernel_policy("auto")
     return y
 
 
 def grouped(names, layers, dev, x, alphas, plan, biases=None):
     ls = [layers[n] for n in names]
     ds = [dev[n] for n in names]
-    outs = [torch.full((x.shape[0], l.N), float("nan"), dtype=torch.float16, device="cuda") for l in ls]
+    outs = [torch.full((x.shape[0], l.N), float("nan"), dtype=x.dtype, device="cuda") for l in ls]
     _C_ops.forward_group([desc(l, d, a) for l, d, a in zip(ls, ds, alphas)], x, outs,
                          [d["plan"] if plan else None for d in ds], biases)
     kernel = _C_ops.last_kernel()
@@ -91,7 +96,7 @@ def test_group_with_biases_and_mixed_alpha(block):
         assert torch.equal(y.view(torch.int16), separate(layers[n], dev[n], x, a, True, b).view(torch.int16))
 
 
-@pytest.mark.parametrize("M", [8, 32, 300])
+@pytest.mark.parametrize("M", [8, 300])
 def test_group_above_decode_falls_back(block, oracle_mod, M):
     layers, dev = block
     names = ("gate_proj", "up_proj")
@@ -105,6 +110,64 @@ def test_group_above_decode_falls_back(block, oracle_mod, M):
     ref = oracle_mod.forward_f64(l.q, l.scales, l.row_ptr, l.col, l.vals, x_np[rows], 1.0)
     err = float(np.abs(outs[1].float().cpu().numpy()[rows] - ref).max())
     assert err <= TOL * float(np.abs(ref).max())
+
+
+@pytest.mark.parametrize("names", [("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"),
+                                   ("q_proj", "k_proj", "v_proj", "o_proj")])
+@pytest.mark.parametrize("M", [17, 32])
+@pytest.mark.parametrize("alpha", [1.0, 0.0])
+def test_group_17_to_32_tokens_in_one_slice_split_launch(block, oracle_mod, names, M, alpha):
+    """17..32 tokens: one slice-split launch and one reduction for the
+    group; each output has the bits of that layer's own slice-split call
+    (policy "split"; the default single call at K = 4096 takes the quarter
+    kernel, equal up to FP32 summation order)."""
+    layers, dev = block
+    x_np = W.make_x(M, 4096, 950 + M)
+    x = torch.from_numpy(x_np).cuda()
+    outs, kernel = grouped(names, layers, dev, x, [alpha] * len(names), alpha > 0)
+    assert kernel == "split_group", kernel
+    for n, y in zip(names, outs):
+        ys = separate(layers[n], dev[n], x, alpha, alpha > 0, policy="split")
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ys.view(torch.int16)), f"{n}: group differs from its own call"
+        yq = separate(layers[n], dev[n], x, alpha, alpha > 0).float().cpu().numpy()
+        yv = y.float().cpu().numpy()
+        assert float(np.abs(yv - yq).max()) <= 2e-3 * float(np.abs(yq).max()), n
+        l = layers[n]
+        rows = np.array([0, 5, 16, M - 1])
+        ref = oracle_mod.forward_f64(l.q, l.scales, l.row_ptr, l.col, l.vals, x_np[rows], alpha)
+        err = float(np.abs(yv[rows] - ref).max())
+        assert err <= TOL * float(np.abs(ref).max()), f"{n} M={M}: {err}"
+
+
+def test_group_17_to_32_tokens_bf16_bias_and_fallbacks(block):
+    """BF16 activations and per-layer biases in the grouped launch; a mixed
+    alpha (another ortho class) and a forced kernel policy run one call per
+    layer with the same bits as separate calls."""
+    layers, dev = block
+    names = ("q_proj", "k_proj", "v_proj")
+    x = torch.from_numpy(W.make_x(24, 4096, 977)).to(torch.bfloat16).cuda()
+    g = torch.Generator(device="cpu").manual_seed(8)
+    biases = [(torch.randn(4096, generator=g) * 0.1).to(dt).cuda()
+              for dt in (torch.bfloat16, torch.float32, torch.bfloat16)]
+    outs, kernel = grouped(names, layers, dev, x, [1.0] * 3, True, biases)
+    assert kernel == "split_group"
+    for n, y, b in zip(names, outs, biases):
+        ys = separate(layers[n], dev[n], x, 1.0, True, b, policy="split")
+        assert torch.equal(y.view(torch.int16), ys.view(torch.int16)), n
+    outs, kernel = grouped(names, layers, dev, x, [1.0, 0.0, 1.0], True, biases)
+    assert kernel != "split_group"
+    for n, y, a, b in zip(names, outs, (1.0, 0.0, 1.0), biases):
+        assert torch.equal(y.view(torch.int16), separate(layers[n], dev[n], x, a, True, b).view(torch.int16))
+    _lib.set_kernel_policy("skinny")
+    try:
+        outs, kernel = grouped(names, layers, dev, x, [1.0] * 3, True, biases)
+    finally:
+        _lib.set_kernel_policy("auto")
+    assert kernel == "skinny"
+    for n, y, b in zip(names, outs, biases):
+        ys = separate(layers[n], dev[n], x, 1.0, True, b, policy="skinny")
+        assert torch.equal(y.view(torch.int16), ys.view(torch.int16)), n
 
 
 def test_group_argument_checks(block):
