@@ -273,14 +273,11 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
             float sacc[16];
 #pragma unroll
             for (int m = 0; m < 16; m++) sacc[m] = 0.f;
-            // a pair of entries (columns ca, cb of the slice, values as the
-            // FP16 pair vp): each token's two products
-            auto pair = [&](int ca, int cb, uint32_t vp) {
-                const u32x4 *pa = reinterpret_cast<const u32x4 *>(xt_col(ca) + 16 * th);
-                const u32x4 *pb = reinterpret_cast<const u32x4 *>(xt_col(cb) + 16 * th);
-                const u32x4 a0 = pa[0], a1 = pa[1], b0 = pb[0], b1 = pb[1];
-                const uint32_t xa[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-                const uint32_t xb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+            // a pair of entries (their columns' 16 tokens xa, xb; values as
+            // the FP16 pair vp): each token's two products
+            auto products = [&](const u32x4 (&ua)[2], const u32x4 (&ub)[2], uint32_t vp) {
+                const uint32_t xa[8] = {ua[0].x, ua[0].y, ua[0].z, ua[0].w, ua[1].x, ua[1].y, ua[1].z, ua[1].w};
+                const uint32_t xb[8] = {ub[0].x, ub[0].y, ub[0].z, ub[0].w, ub[1].x, ub[1].y, ub[1].z, ub[1].w};
                 if constexpr (XB) {
                     const float va = (float)__builtin_bit_cast(f16, (uint16_t)(vp & 0xffffu));
                     const float vb = (float)__builtin_bit_cast(f16, (uint16_t)(vp >> 16));
@@ -302,6 +299,12 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
                     }
                 }
             };
+            auto pair = [&](int ca, int cb, uint32_t vp) {
+                const u32x4 *pa = reinterpret_cast<const u32x4 *>(xt_col(ca) + 16 * th);
+                const u32x4 *pb = reinterpret_cast<const u32x4 *>(xt_col(cb) + 16 * th);
+                const u32x4 ua[2] = {pa[0], pa[1]}, ub[2] = {pb[0], pb[1]};
+                products(ua, ub, vp);
+            };
             const bool ok = (er[0] == plan_cell_tag(kCellSlice, L.N, K, L.nnz, a.swords, blk, s)) &
                             (er[1] == 0u);  // (uniform)
             if (ok) {
@@ -309,10 +312,29 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
                 const int32_t lo = (int32_t)(hw & 0xffffu);
                 const int32_t hi = row < L.N ? (int32_t)(hw >> 16) : lo;
                 const uint32_t *ee = er + kCellHdrWords;
-                for (int32_t j0 = lo + qe; j0 < hi; j0 += 8) {
-                    const bool vb = j0 + 4 < hi;
-                    const uint32_t wa = ee[j0], wb = ee[vb ? j0 + 4 : j0];
-                    pair((int)(wa & 0xffffu), (int)(wb & 0xffffu), (wa >> 16) | (vb ? (wb & 0xffff0000u) : 0u));
+                // two pairs per pass (entries j0 + 4 u, u < 4): every LDS
+                // read of the pass is issued before the products, one round
+                // trip for the record words and one for the activations
+                for (int32_t j0 = lo + qe; j0 < hi; j0 += 16) {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) w[u] = ee[min(j0 + 4 * u, hi - 1)];
+                    uint32_t vp[2];
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const bool va = j0 + 8 * h < hi, vb = j0 + 8 * h + 4 < hi;
+                        vp[h] = (va ? (w[2 * h] >> 16) : 0u) | (vb ? (w[2 * h + 1] & 0xffff0000u) : 0u);
+                    }
+                    u32x4 xv[4][2];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const u32x4 *pc = reinterpret_cast<const u32x4 *>(xt_col((int)(w[u] & 0xffffu)) + 16 * th);
+                        xv[u][0] = pc[0];
+                        xv[u][1] = pc[1];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int h = 0; h < 2; h++) products(xv[2 * h], xv[2 * h + 1], vp[h]);
                 }
             } else {
                 int32_t fs = 0, fe = 0;
