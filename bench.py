@@ -634,6 +634,7 @@ PROFILE_WORKLOADS = {
     "c2_m1_a1": ("c2", 1, 1.0), "c2_m1_a0": ("c2", 1, 0.0), "c2_m2_a1": ("c2", 2, 1.0),
     "c2_m4_a1": ("c2", 4, 1.0), "c2_m8_a1": ("c2", 8, 1.0), "c2_m16_a1": ("c2", 16, 1.0),
     "c2_m32_a1": ("c2", 32, 1.0), "c2_m32_a0": ("c2", 32, 0.0), "c2_m2048_a1": ("c2", 2048, 1.0),
+    "c2_m2048_a0": ("c2", 2048, 0.0),
     "c1_m1_a1": ("c1", 1, 1.0),
     "c1_m1_a0": ("c1", 1, 0.0), "c3_m2048_a1": ("c3", 2048, 1.0), "c3_m2048_a0": ("c3", 2048, 0.0),
     "c4_m8_a1": ("c4", 8, 1.0), "c5_m1": ("c5", 1, 1.0), "c5_m1_grouped": ("c5", 1, 1.0),

@@ -22,9 +22,9 @@ STATUS_NAMES = {OK: "ORTH_OK", ERR_INVALID_ARGUMENT: "ORTH_ERR_INVALID_ARGUMENT"
                 ERR_NO_DEVICE: "ORTH_ERR_NO_DEVICE"}
 # kernel ids (orth_hip_last_kernel) and policies (orth_hip_set_kernel_policy)
 KERNEL_NAMES = {0: "none", 1: "decode", 2: "prefill", 3: "general", 4: "skinny", 5: "decode_group", 6: "mid", 7: "quarter",
-                8: "split", 9: "split_group"}
+                8: "split", 9: "split_group", 10: "prefill_wide"}
 GROUP_MAX = 4
-POLICIES = {"auto": 0, "decode": 1, "prefill": 2, "general": 3, "skinny": 4, "mid": 5, "quarter": 6, "split": 7}
+POLICIES = {"auto": 0, "decode": 1, "prefill": 2, "general": 3, "skinny": 4, "mid": 5, "quarter": 6, "split": 7, "prefill_wide": 8}
 
 
 class OrthHipBase(ctypes.Structure):

@@ -45,6 +45,9 @@ int64_t plan_prefill_bytes(int64_t N, int64_t K, int64_t nnz);
 hipError_t launch_plan_build_prefill(const ForwardArgs &a, void *plan, hipStream_t stream);
 hipError_t plan_read_flags(const void *plan, hipStream_t stream, uint32_t *flags);
 hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream);
+bool prefill_wide_supported(const ForwardArgs &a);
+bool prefill_wide_preferred(const ForwardArgs &a, int cus);
+hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream_t stream);
 hipError_t prefill_prepare_device();
 hipError_t plan_prepare_device();
 bool mid_supported(const ForwardArgs &a, const void *plan);
@@ -90,6 +93,7 @@ int policy_from_env() {
     if (!std::strcmp(e, "mid")) return 5;
     if (!std::strcmp(e, "quarter")) return 6;
     if (!std::strcmp(e, "split")) return 7;
+    if (!std::strcmp(e, "prefill_wide")) return 8;
     return 0;
 }
 
@@ -333,7 +337,7 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part)
 }
 
 // The kernel a forward call takes under `policy` (orth_hip_set_kernel_policy).
-int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel) {
+int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int cus, int *kernel) {
     const bool dec_ok = decode_supported(a) || decode_bf16_supported(a, a.has_ortho ? plan : nullptr);
     const bool pre_ok = prefill_supported(a);
     // the mid-batch kernel reads each row's ortho entries through the plan;
@@ -373,6 +377,11 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
             if (!sp_ok) return fail(ORTH_ERR_UNSUPPORTED, "slice-split kernel forced but it cannot take this call");
             *kernel = KERNEL_SPLIT;
             break;
+        case 8:
+            if (!prefill_wide_supported(a))
+                return fail(ORTH_ERR_UNSUPPORTED, "wide-row prefill kernel forced but it cannot take this call");
+            *kernel = KERNEL_PREFILL_WIDE;
+            break;
         default:
             // the one-launch mid-batch kernel beats the split-K one on every
             // shape both take (c2 M=8 alpha=1 10.3 against 14.4 us, M=16
@@ -386,7 +395,8 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int *kernel)
             else if (sp_ok && a.M > 16) *kernel = KERNEL_SPLIT;
             else if (sk_pref) *kernel = KERNEL_SKINNY;
             else if (dec_ok) *kernel = KERNEL_DECODE;
-            else *kernel = pre_ok && a.M > 16 ? KERNEL_PREFILL : KERNEL_GENERAL;
+            else if (pre_ok && a.M > 16) *kernel = prefill_wide_preferred(a, cus) ? KERNEL_PREFILL_WIDE : KERNEL_PREFILL;
+            else *kernel = KERNEL_GENERAL;
     }
     return ORTH_OK;
 }
@@ -418,7 +428,7 @@ int forward_impl(const orth_hip_layer_t *layer, const void *plan, int64_t plan_b
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
 
     int kernel = KERNEL_NONE;
-    rc = pick_kernel(a, plan, g_policy.load(std::memory_order_relaxed), &kernel);
+    rc = pick_kernel(a, plan, g_policy.load(std::memory_order_relaxed), g_dev[dev].cus, &kernel);
     if (rc != ORTH_OK) return rc;
 
     // No-allocation calls share the device's scratch array: a call on a
@@ -486,7 +496,10 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
         e = qk ? launch_quarter(a, a.has_ortho ? plan : nullptr, part, stream)
             : sk ? launch_split(a, a.has_ortho ? plan : nullptr, part, stream)
                  : launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
-    } else if (kernel == KERNEL_PREFILL) {
+    } else if (kernel == KERNEL_PREFILL || kernel == KERNEL_PREFILL_WIDE) {
+        auto pf = [&](const void *p) {
+            return kernel == KERNEL_PREFILL_WIDE ? launch_prefill_wide(a, p, stream) : launch_prefill(a, p, stream);
+        };
         if (a.has_ortho && !plan && noalloc) {
             // the prefill part of a plan, built in the scratch array
             const int64_t pb = plan_prefill_bytes(a.N, a.K, a.nnz);
@@ -496,7 +509,7 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
                             "entry point has %lld bytes of scratch (pass a plan from orth_ortho_plan_build)",
                             (long long)pb, (long long)ORTH_NOALLOC_SCRATCH_BYTES);
             e = launch_plan_build_prefill(a, g_dev[dev].scratch, stream);
-            if (e == hipSuccess) e = launch_prefill(a, g_dev[dev].scratch, stream);
+            if (e == hipSuccess) e = pf(g_dev[dev].scratch);
         } else if (a.has_ortho && !plan) {
             // temporary plan (its prefill part).  Under capture: in the
             // memory of captured calls (no allocation is recorded).  Else
@@ -511,7 +524,7 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
                 rc = capture_memory(dev, stream, pb, "temporary ortho plan (pass a plan to capture this call)", &p);
                 if (rc != ORTH_OK) return rc;
                 e = launch_plan_build_prefill(a, p, stream);
-                if (e == hipSuccess) e = launch_prefill(a, p, stream);
+                if (e == hipSuccess) e = pf(p);
                 if (e != hipSuccess) return fail_hip(e, "kernel launch");
                 return ORTH_OK;
             }
@@ -519,11 +532,11 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
             e = hipMallocAsync(&tmp, (size_t)pb, stream);
             if (e != hipSuccess) return fail_hip(e, "hipMallocAsync (temporary ortho plan)");
             e = launch_plan_build_prefill(a, tmp, stream);
-            if (e == hipSuccess) e = launch_prefill(a, tmp, stream);
+            if (e == hipSuccess) e = pf(tmp);
             hipError_t f = hipFreeAsync(tmp, stream);
             if (e == hipSuccess) e = f;
         } else {
-            e = launch_prefill(a, a.has_ortho ? plan : nullptr, stream);
+            e = pf(a.has_ortho ? plan : nullptr);
         }
     } else {
         e = launch_general(a, stream);
@@ -576,7 +589,7 @@ int group_forward_impl(const orth_hip_layer_t *const *layers, const void *const 
     const int policy = g_policy.load(std::memory_order_relaxed);
     for (int l = 0; l < count && grouped; l++) {
         int kernel = KERNEL_NONE;
-        rc = pick_kernel(as[l], pl[l], policy, &kernel);
+        rc = pick_kernel(as[l], pl[l], policy, g_dev[dev].cus, &kernel);
         if (rc != ORTH_OK) return rc;
         grouped = kernel == KERNEL_DECODE;
     }
@@ -592,7 +605,7 @@ int group_forward_impl(const orth_hip_layer_t *const *layers, const void *const 
     bool split_all = count > 1 && (policy == 0 || policy == 7) && as[0].M > 16;
     for (int l = 0; l < count && split_all; l++) {
         int kernel = KERNEL_NONE;
-        rc = pick_kernel(as[l], pl[l], policy, &kernel);
+        rc = pick_kernel(as[l], pl[l], policy, g_dev[dev].cus, &kernel);
         if (rc != ORTH_OK) return rc;
         split_all = kernel == KERNEL_QUARTER || kernel == KERNEL_SPLIT;
     }
@@ -906,7 +919,7 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info) {
 }
 
 int orth_hip_set_kernel_policy(int policy) {
-    if (policy < 0 || policy > 7) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..7");
+    if (policy < 0 || policy > 8) return fail(ORTH_ERR_INVALID_ARGUMENT, "policy must be 0..8");
     g_policy.store(policy);
     return ORTH_OK;
 }

@@ -33,7 +33,8 @@ enum KernelId {
     KERNEL_MID = 6,           // one-launch mid-batch kernel (5..16 tokens)
     KERNEL_QUARTER = 7,       // K quarters over the grid (17..32 tokens)
     KERNEL_SPLIT = 8,         // 1024-column slices over the grid (17..32 tokens)
-    KERNEL_SPLIT_GROUP = 9    // the same for a group of layers in one launch
+    KERNEL_SPLIT_GROUP = 9,   // the same for a group of layers in one launch
+    KERNEL_PREFILL_WIDE = 10  // prefill with one 256 x 352 tile per CU
 };
 
 // Everything a forward launch needs, resolved on the host.

@@ -24,6 +24,8 @@
 //    dequant entry point gives the bit-exact FP32 weights.)
 //  * Tiles are mapped XCD-aware: consecutive workgroup ids land on different
 //    XCDs, so the tile order is remapped to give each XCD a contiguous run.
+#include <type_traits>
+
 #include "orth_common.h"
 
 namespace orth {
@@ -744,6 +746,443 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
     }
 }
 
+// ------------------------------------------------- wide-row prefill tile
+//
+// For layers wide enough to give every CU one tile in one round (4096 ->
+// 11008 at 2048 tokens: 8 token tiles x 32 row ranges of 352 rows = 256
+// workgroups; the 256 x 128 tile above needs 688 tiles, 2.69 rounds).
+//
+//  * Workgroup tile 256 tokens x R = 32 * NRT rows, 8 waves (two per SIMD,
+//    so one's MFMAs run beside the other's dequantisation) in a 4 x 2 grid,
+//    each 64 tokens x 16 NRT rows with v_mfma_f32_16x16x32_f16: 4 x NRT
+//    accumulator tiles, 176 AGPRs at NRT = 11.  Each operand read from LDS
+//    feeds NRT (activations) or 4 (weights) MFMAs: a CU reads 120 KB of
+//    operands per 352 MFMA cycles' worth of one step (the 256 x 128 tile
+//    read 128 KB per 128).
+//  * K advances 32 columns a step: activations in 2 LDS stages of 16 KB,
+//    dequantised weights (the same fp16(q * s) as above, 16 bytes of nibbles
+//    per row and step, two threads per row) in 3 stages of R x 64 bytes.
+//  * The ortho plan's (128-row block, 64-column step) entries of the up to
+//    four blocks the row range touches are folded into the weight stage one
+//    step after its dequantisation (each 64-column step in two halves), so
+//    one barrier a step orders everything.
+//  * Workgroup b takes token tile b % TT and row range b / TT: with 8 token
+//    tiles each XCD holds one token tile's activations in its L2.
+constexpr int PW_BM = 256, PW_BK = 32, PW_NT = 512;
+constexpr int PW_A_BYTES = PW_BM * PW_BK * 2;  // one activation stage (16 KB)
+constexpr int PW_MAX_BLOCKS = 4;               // plan blocks a row range may touch
+constexpr int PW_E = 1;                        // plan entries per thread prefetched per 64-column step
+
+// LDS rows of 4 chunks of 16 bytes; chunk c of row r sits at c ^ g(r),
+// g(r) = (r1 ^ r2 ^ r3) | r2 << 1 (r_i: bit i of r).  Whether a phase of a
+// 16-byte access serves 8 lanes (32 banks) or 16 (64 banks), its lanes fall
+// in distinct bank groups for the three patterns used: 8 / 16 consecutive
+// rows of one chunk (the MFMA operand reads), rows of 4 chunks (activation
+// writes) and row pairs of chunks {w, w + 2} (weight writes).  (A swizzle
+// by (r >> 2) & 3, distinct only for 16-lane phases, measured 43 % of the
+// LDS's active cycles stalled on bank conflicts.)
+__device__ __forceinline__ int pw_swz(int r, int c) {
+    const int g = (((r >> 1) ^ (r >> 2) ^ (r >> 3)) & 1) | ((r >> 1) & 2);
+    return r * PW_BK + ((c ^ g) << 3);
+}
+
+// A weight stage holds max(R, 512) rows: a thread's second half-row job
+// lands in rows R .. 511 when it has none (never read; no branch).
+__host__ __device__ constexpr int pw_b_rows(int nrt) { return 32 * nrt > PW_NT ? 32 * nrt : PW_NT; }
+__host__ __device__ constexpr int pw_b_bytes(int nrt) { return pw_b_rows(nrt) * PW_BK * 2; }
+__host__ __device__ constexpr int pw_off_at(int nrt) { return 2 * PW_A_BYTES + 3 * pw_b_bytes(nrt); }
+__host__ __device__ constexpr int pw_trash_at(int nrt) {
+    return pw_off_at(nrt) + PW_MAX_BLOCKS * (int)(kPlanMaxK / kPlanBK + 1) * 4;
+}
+__host__ __device__ constexpr int pw_lds_bytes(int nrt) { return pw_trash_at(nrt) + PW_NT * 2; }
+
+struct PwA { u32x4 v[2]; };                    // 256 tokens x 64 bytes: 2 x 16 B per thread
+struct PwB { uint2 v[2]; uint32_t s[2]; };     // up to 2 half rows (8 bytes of nibbles) + scale bits
+struct PwE { uint32_t e[PW_E]; int brow[PW_E]; int total; };  // a thread's plan entries of one 64-column step (total: its block's count)
+
+// f(integral_constant<int, k>) for k = 0 .. N-1, unrolled at compile time
+template <class F, int... Is>
+__device__ __forceinline__ void pw_static_for(F &&f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+
+// Slot plan of a step (4 NRT MFMA slots): the 8 NJ dequantised byte pairs
+// spread evenly over the slots (byte b at slot b NRT / 4), the rest in the
+// gaps.  pw_dq_at: the byte pair of slot k, or -1.
+constexpr int pw_dq_at(int k, int nrt, int nbytes) {
+    for (int b = 0; b < nbytes; b++)
+        if ((b * nrt) / 4 == k) return b;
+    return -1;
+}
+
+template <int NRT, bool FOLD, bool XB>
+__global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
+    constexpr int R = 32 * NRT;                 // rows of the workgroup tile
+    constexpr int NJ = (2 * R + PW_NT - 1) / PW_NT;  // half-row jobs per thread (dequantisation)
+    static_assert(NJ <= 2, "two half-row jobs per thread at most");
+    extern __shared__ __align__(16) unsigned char smem[];
+    f16 *As0 = reinterpret_cast<f16 *>(smem);
+    f16 *Bs0 = reinterpret_cast<f16 *>(smem + 2 * PW_A_BYTES);
+    int32_t *offs = reinterpret_cast<int32_t *>(smem + pw_off_at(NRT));
+    f16 *trash = reinterpret_cast<f16 *>(smem + pw_trash_at(NRT));
+
+    const int tt = (int)(blockIdx.x % (unsigned)a.nbm), rr = (int)(blockIdx.x / (unsigned)a.nbm);
+    const int64_t m0 = (int64_t)tt * PW_BM, n0 = (int64_t)rr * R;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: scalar addressing)
+    const int wm = wave & 3, wn = wave >> 2;
+    const int nk = (int)(a.K / PW_BK);
+    const int nk64 = (int)(a.K / kPlanBK);
+
+    // per-thread byte offsets (step 0) of the first chunk / job; the others
+    // are formed at each load (registers are the limit here).  Rows past M
+    // / N repeat the last row.
+    const uint32_t xrow = (uint32_t)(m0 + (tid >> 2));
+    const uint32_t xcol = (uint32_t)((tid & 3) * 16);
+    auto xoff = [&](int i) -> uint32_t {
+        return min(xrow + (uint32_t)(i * (PW_NT / 4)), (uint32_t)(a.M - 1)) * (uint32_t)(a.K * 2) + xcol;
+    };
+    // half-row job i of this thread: tid + 512 i (row job / 2, chunks 2 (job
+    // % 2) and 2 (job % 2) + 1); past 2 R it writes the stage's spare rows
+    auto job = [&](int i) -> int { return tid + PW_NT * i; };
+    static_assert(PW_NT * NJ / 2 <= pw_b_rows(NRT), "half-row jobs stay inside the stage");
+    // LDS write offsets (halves) of job 0, chunk 2 (tid % 2), and of the
+    // thread's first activation chunk: the other writes are fixed offsets
+    // or one XOR from these (the swizzle leaves bits 4 and up of a row alone)
+    const int bwo = pw_swz(tid >> 1, (tid & 1) * 2);
+    const int awo = pw_swz(tid >> 2, tid & 3);
+    auto qrow_of = [&](int i) -> uint32_t {
+        return min((uint32_t)(n0 + (job(i) >> 1)), (uint32_t)(a.N - 1));
+    };
+    const int gshift = a.ngroups == 1 ? 31 : __builtin_ctzll(a.G / PW_BK);
+
+    // plan blocks of the row range, their offsets staged in LDS
+    const int nblk = (int)((a.N + kPlanBN - 1) / kPlanBN);
+    const int b_lo = (int)(n0 / kPlanBN);
+    const int nb = FOLD ? max(0, min(PW_MAX_BLOCKS, min(nblk, (int)((n0 + R - 1) / kPlanBN) + 1) - b_lo)) : 0;
+    bool canonical = true;
+    if (FOLD) {
+        const PlanHeader *h = a.plan;
+        const bool ok = h->magic == kPlanMagic && h->version == kPlanVersion && h->n == a.N &&
+                        h->k == a.K && h->nnz == a.nnz;
+        for (int i = tid; i < nb * (nk64 + 1); i += PW_NT) {
+            const int bb = i / (nk64 + 1), u = i - bb * (nk64 + 1);
+            offs[i] = ok ? min(max(a.offsets[(int64_t)(b_lo + bb) * (nk64 + 1) + u], 0), a.nnz) : 0;
+        }
+        canonical = !ok || (h->flags & kPlanNonCanonical) == 0;
+        __syncthreads();
+    }
+
+    // buffer loads: a 32-bit lane offset that stays the same for the whole
+    // K loop plus the step's offset in a scalar register (one VGPR per
+    // stream instead of a 64-bit address each; registers are the limit)
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<f16 *>(a.x), (short)0, (int)(uint32_t)(a.M * a.K * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.q), (short)0, (int)(uint32_t)(a.N * (a.K / 2)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16 *>(a.scales), (short)0, (int)(uint32_t)(a.N * a.ngroups * 2), 0x00020000);
+    auto load_a = [&](int u, PwA &r) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            r.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff(i), u * (PW_BK * 2), 0));
+    };
+    auto store_a = [&](const PwA &r, f16 *As) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int idx = tid + PW_NT * i;
+            *reinterpret_cast<u32x4 *>(As + pw_swz(idx >> 2, idx & 3)) = r.v[i];
+        }
+    };
+    auto load_b = [&](int u, PwB &r) {
+#pragma unroll
+        for (int i = 0; i < NJ; i++) {
+            const uint32_t n = qrow_of(i);
+            r.v[i] = __builtin_bit_cast(
+                uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, n * (uint32_t)(a.K >> 1) + (uint32_t)(job(i) & 1) * 8,
+                                                            u * (PW_BK / 2), 0));
+            r.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, n * (uint32_t)(a.ngroups * 2), ((uint32_t)u >> gshift) * 2, 0);
+        }
+    };
+    auto store_b = [&](const PwB &r, f16 *Bs) {
+#pragma unroll
+        for (int i = 0; i < NJ; i++) {
+            const int j = job(i);
+            const int row = j >> 1, c0 = (j & 1) * 2;
+            const f16 sc = __builtin_bit_cast(f16, (uint16_t)r.s[i]);
+            const f16x2 s2 = {sc, sc};
+            const float sf = (float)sc;
+            const uint32_t words[2] = {r.v[i].x, r.v[i].y};
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                u32x4 o;
+                if constexpr (XB) {
+                    const uint32_t lo = (words[w] & 0x0F0F0F0Fu) ^ 0x08080808u;
+                    const uint32_t hi = ((words[w] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+                    const float s8 = -8.0f * sf;
+                    auto pair = [&](int b) {
+                        return pk_bf16(__builtin_fmaf((float)((lo >> (8 * b)) & 0xFFu), sf, s8),
+                                       __builtin_fmaf((float)((hi >> (8 * b)) & 0xFFu), sf, s8));
+                    };
+                    o = u32x4{pair(0), pair(1), pair(2), pair(3)};
+                } else {
+                    o = u32x4{dq_byte(words[w], s2, 0), dq_byte(words[w], s2, 1), dq_byte(words[w], s2, 2),
+                              dq_byte(words[w], s2, 3)};
+                }
+                *reinterpret_cast<u32x4 *>(Bs + pw_swz(row, c0 + w)) = o;
+            }
+        }
+    };
+
+    // thread tid takes entries tid % 128 (+ 128 e) of block tid / 128 of the
+    // row range (the range touches at most 4 blocks): two offset reads, no
+    // search
+    const int eb = tid >> 7, ep = tid & 127;
+    constexpr int EPB = PW_NT / PW_MAX_BLOCKS;  // threads per block
+    auto load_e = [&](int u, PwE &r) {
+        u = min(u, nk64 - 1);
+        const bool vb = eb < nb;
+        const int o = (vb ? eb : 0) * (nk64 + 1) + u;
+        const int l = offs[o], h = max(l, offs[o + 1]);
+        r.total = vb ? h - l : 0;  // (this thread's block)
+#pragma unroll
+        for (int e = 0; e < PW_E; e++) {
+            r.e[e] = a.entries[min(max(l + ep + EPB * e, 0), a.nnz - 1)];
+            r.brow[e] = ep + EPB * e < r.total ? (b_lo + eb) * kPlanBN - (int)n0 : -(1 << 20);
+        }
+    };
+    // alpha * v of every entry of 64-column step u whose column falls in
+    // half `half` into the weight stage Bs (rows of the range only).  The
+    // cell of (local row, column c of the 64) gets alpha * v; a thread with
+    // nothing to add updates its own trash cell (no branch).
+    auto cell = [&](f16 *Bs, int local, int c, uint32_t w, bool ok) {
+        const float v = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xffffu));
+        uint16_t *p = reinterpret_cast<uint16_t *>(
+            ok ? Bs + pw_swz(min(max(local, 0), R - 1), (c & 31) >> 3) + (c & 7) : trash + tid);
+        *p = fold_add<XB>(*p, a.alpha * v);
+    };
+    auto one = [&](f16 *Bs, int half, uint32_t w, int brow) {
+        const int local = brow + (int)(w >> 24);
+        const int c = (int)((w >> 16) & (kPlanBK - 1));
+        cell(Bs, local, c, w, local >= 0 && local < R && (c >> 5) == half);
+    };
+    // the prefetched entries (canonical plans), no branch
+    auto fold_common = [&](int half, const PwE &r, f16 *Bs) {
+#pragma unroll
+        for (int e = 0; e < PW_E; e++) one(Bs, half, r.e[e], canonical ? r.brow[e] : -(1 << 20));
+    };
+    // the rest (uniform branch): entries past the prefetched ones, or the
+    // whole step for a plan with duplicate or unsorted columns
+    auto fold_rare = [&](int u, int half, int total, f16 *Bs) {
+        u = min(u, nk64 - 1);
+        if (canonical) {
+            // this thread's block holds more entries than the prefetched ones
+            const int l = offs[(eb < nb ? eb : 0) * (nk64 + 1) + u];
+            for (int v = PW_E * EPB + ep; v < total; v += EPB)
+                one(Bs, half, a.entries[min(max(l + v, 0), a.nnz - 1)], (b_lo + eb) * kPlanBN - (int)n0);
+        } else {
+            // one thread per row applies the row's entries of the step in
+            // plan order (the result is reproducible bit for bit)
+            for (int lr = tid; lr < R; lr += PW_NT) {
+                const int64_t n = n0 + lr;
+                if (n >= a.N) break;
+                const int bb = (int)(n / kPlanBN) - b_lo;
+                if (bb < 0 || bb >= nb) continue;
+                const int rib = (int)(n % kPlanBN);
+                const int32_t lo = offs[bb * (nk64 + 1) + u], hi = min(offs[bb * (nk64 + 1) + u + 1], a.nnz);
+                int32_t b = lo, e_hi = hi;
+                while (b < e_hi) {
+                    const int32_t mid = b + ((e_hi - b) >> 1);
+                    if ((int)(a.entries[mid] >> 24) < rib) b = mid + 1;
+                    else e_hi = mid;
+                }
+                for (int32_t e = b; e < hi; e++) {
+                    const uint32_t w = a.entries[e];
+                    if ((int)(w >> 24) != rib) break;
+                    const int c = (int)((w >> 16) & (kPlanBK - 1));
+                    if ((c >> 5) == half) cell(Bs, lr, c, w, true);
+                }
+            }
+        }
+    };
+
+    f32x4 acc[4][NRT];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < NRT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+
+    // one register set each for the activations, the raw weights and the
+    // plan entries: a step writes the set it holds to LDS (or folds it), then
+    // loads the next step's into it (a load still has a full step to land)
+    PwA ra;
+    PwB rb;
+    PwE re;
+    auto Bst = [&](int s) { return Bs0 + s * (pw_b_bytes(NRT) / 2); };
+    auto Ast = [&](int s) { return As0 + s * (PW_A_BYTES / 2); };
+
+    // prologue: stage 0 folded, stage 1 dequantised; A(1), B(2) and the
+    // entries of stage 1's fold in flight
+    if (FOLD) load_e(0, re);
+    load_a(0, ra);
+    load_b(0, rb);
+    store_a(ra, Ast(0));
+    load_a(min(1, nk - 1), ra);
+    store_b(rb, Bst(0));
+    load_b(min(1, nk - 1), rb);
+    store_b(rb, Bst(1));
+    load_b(min(2, nk - 1), rb);
+    __syncthreads();
+    if (FOLD) {
+        fold_common(0, re, Bst(0));
+        if (!canonical || re.total > PW_E * EPB) fold_rare(0, 0, re.total, Bst(0));
+        load_e(0, re);
+    }
+    __syncthreads();
+
+    // step t: MFMAs on A(t % 2), B(t % 3); A(t+1) written and A(t+2) loaded,
+    // B(t+2) dequantised and B(t+3) loaded, B(t+1) folded (64-column step
+    // (t+1)/2, half (t+1)%2) and the entries of the next step's fold loaded;
+    // one barrier.
+    //
+    // The step is laid out by hand in 4 NRT slots, one MFMA each followed by
+    // a slice of the rest (sched_barrier between slots): the dequantisation
+    // and the LDS and memory traffic of the next stages run while the
+    // matrix core works.  (Left to the scheduler, each wave issued its MFMAs
+    // back to back and its VALU work after them, and the step's barrier kept
+    // the two waves of a SIMD in the same phase: 3,600 cycles a step
+    // against 1,408 of MFMAs.)
+    int b3 = 0;  // t % 3
+    const int aro = pw_swz(lane & 15, lane >> 4);
+    for (int t = 0; t < nk; t++) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int b3_1 = b3 == 2 ? 0 : b3 + 1, b3_2 = b3 == 0 ? 2 : b3 - 1;
+        const int u1 = (t + 1) >> 1, h1 = (t + 1) & 1;
+        const int total1 = FOLD ? re.total : 0;
+        const bool rare = FOLD && (!canonical || total1 > PW_E * EPB);  // (per thread: its block overflows)
+        const f16 *As = Ast(t & 1), *Bs = Bst(b3);
+        f16 *Bw = Bst(b3_2), *Bf = Bst(b3_1), *Aw = Ast((t + 1) & 1);
+
+        // operand reads: row 16 m + lr, chunk lc sits at aro + 16 m rows
+        // (the swizzle depends on the row's bits 1..3 only)
+        f16x8 af[4], bcur, bnext;
+        const f16 *Ar = As + aro + 64 * wm * PW_BK, *Br = Bs + aro + (R / 2) * wn * PW_BK;
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const f16x8 *>(Ar + 16 * i * PW_BK);
+        bnext = *reinterpret_cast<const f16x8 *>(Br);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // dequantisation state of the current job and word
+        f16x2 s2 = {};
+        float sf = 0.f;
+        uint32_t wlo = 0, whi = 0, out[4] = {0, 0, 0, 0};
+        // fold state
+        uint16_t *fp = nullptr;
+        uint16_t fold_old = 0;
+        float fold_add_v = 0.f;
+
+        pw_static_for([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            constexpr int j = k / 4, i = k % 4;
+            if constexpr (i == 0) {
+                bcur = bnext;
+                if constexpr (j + 1 < NRT) bnext = *reinterpret_cast<const f16x8 *>(Br + 16 * (j + 1) * PW_BK);
+            }
+            if constexpr (XB)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
+                                                                    __builtin_bit_cast(bf16x8, bcur), acc[i][j], 0, 0, 0);
+            else
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bcur, acc[i][j], 0, 0, 0);
+
+            constexpr int q = pw_dq_at(k, NRT, 8 * NJ);
+            if constexpr (q >= 0) {
+                // B(t+2): job q / 8, word (q / 4) % 2, byte q % 4
+                constexpr int jb = q / 8, w = (q / 4) % 2, b = q % 4;
+                const uint32_t word = w ? rb.v[jb].y : rb.v[jb].x;
+                if constexpr (w == 0 && b == 0) {
+                    const f16 sc = __builtin_bit_cast(f16, (uint16_t)rb.s[jb]);
+                    s2 = f16x2{sc, sc};
+                    sf = (float)sc;
+                }
+                if constexpr (XB) {
+                    if constexpr (b == 0) {
+                        wlo = (word & 0x0F0F0F0Fu) ^ 0x08080808u;
+                        whi = ((word >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+                    }
+                    out[b] = pk_bf16(__builtin_fmaf((float)((wlo >> (8 * b)) & 0xFFu), sf, -8.0f * sf),
+                                     __builtin_fmaf((float)((whi >> (8 * b)) & 0xFFu), sf, -8.0f * sf));
+                } else {
+                    out[b] = dq_byte(word, s2, b);
+                }
+                if constexpr (b == 3)
+                    *reinterpret_cast<u32x4 *>(Bw + (bwo ^ (w << 3)) + jb * (PW_NT / 2) * PW_BK) =
+                        u32x4{out[0], out[1], out[2], out[3]};
+            }
+            if constexpr (k == 1 || k == 3) {
+                // A(t+1) to LDS
+                constexpr int c = (k - 1) / 2;
+                *reinterpret_cast<u32x4 *>(Aw + awo + c * (PW_NT / 4) * PW_BK) = ra.v[c];
+            }
+            if constexpr (k == 4 || k == 6) {
+                // A(t+2) loads (after the writes of the registers they reuse)
+                constexpr int c = (k - 4) / 2;
+                ra.v[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        rx, xoff(c), min(t + 2, nk - 1) * (PW_BK * 2), 0));
+            }
+            // B(t+3) loads of job c, in the slot after job c's last byte pair
+            // (a full step before job 0's first use, most of one for job 1)
+            constexpr int bl = (k == ((8 * 0 + 7) * NRT) / 4 + 1) ? 0 : (NJ > 1 && k == ((8 * 1 + 7) * NRT) / 4 + 1) ? 1 : -1;
+            if constexpr (bl >= 0) {
+                const int u = min(t + 3, nk - 1);
+                const uint32_t n = qrow_of(bl);
+                rb.v[bl] = __builtin_bit_cast(
+                    uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, n * (uint32_t)(a.K >> 1) + (uint32_t)(job(bl) & 1) * 8,
+                                                                u * (PW_BK / 2), 0));
+                rb.s[bl] = __builtin_amdgcn_raw_buffer_load_b16(rs, n * (uint32_t)(a.ngroups * 2), ((uint32_t)u >> gshift) * 2, 0);
+            }
+            if constexpr (FOLD && k == 9) {
+                // fold of B(t+1), prefetched entry: the cell (or the trash cell)
+                const uint32_t w = re.e[0];
+                const int local = (canonical ? re.brow[0] : -(1 << 20)) + (int)(w >> 24);
+                const int c = (int)((w >> 16) & (kPlanBK - 1));
+                const bool ok = local >= 0 && local < R && (c >> 5) == h1;
+                fp = reinterpret_cast<uint16_t *>(ok ? Bf + pw_swz(min(max(local, 0), R - 1), (c & 31) >> 3) + (c & 7)
+                                                     : trash + tid);
+                fold_add_v = a.alpha * (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xffffu));
+                fold_old = *fp;
+            }
+            if constexpr (FOLD && k == 14) *fp = fold_add<XB>(fold_old, fold_add_v);
+            if constexpr (FOLD && k == 25) load_e((t + 2) >> 1, re);  // the next step's entries
+            __builtin_amdgcn_sched_barrier(0);
+        }, std::make_integer_sequence<int, 4 * NRT>{});
+        static_assert(4 * NRT >= ((8 * NJ - 1) * NRT) / 4 + 2 && 4 * NRT > 25, "every slice of the step needs a slot");
+
+        if (rare) fold_rare(u1, h1, total1, Bf);
+        __syncthreads();
+        b3 = b3_1;
+    }
+
+    // epilogue: lane holds D[token 16 i + 4 (lane / 16) + r][row 16 j + lane % 16]
+#pragma unroll
+    for (int j = 0; j < NRT; j++) {
+        const int64_t n = n0 + (R / 2) * wn + 16 * j + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int64_t m = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
+                if (m < a.M && n < a.N) {
+                    if constexpr (XB)
+                        reinterpret_cast<uint16_t *>(a.y)[m * a.N + n] = out_bf16(acc[i][j][r], a.bias, a.bias_dtype, n);
+                    else
+                        a.y[m * a.N + n] = out_f16(acc[i][j][r], a.bias, a.bias_dtype, n);
+                }
+            }
+        }
+    }
+}
+
 bool prefill_supported(const ForwardArgs &a) {
     if ((a.io_dtype != ORTH_DT_F16 && a.io_dtype != ORTH_DT_BF16) || a.scale_dtype != ORTH_DT_F16) return false;
     if (a.K % PF_BK != 0) return false;
@@ -792,6 +1231,64 @@ hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t st
     return hipGetLastError();
 }
 
+// The wide-row tile: rows per workgroup 32 * kPwNrt.  Taken when the layer
+// has at least 16 row ranges (every workgroup a full MFMA load of rows).
+constexpr int kPwNrt = 11;
+static_assert(pw_lds_bytes(kPwNrt) <= 160 * 1024, "wide prefill LDS budget");
+
+bool prefill_wide_supported(const ForwardArgs &a) {
+    if (!prefill_supported(a)) return false;
+    return a.ngroups == 1 || (a.G % PW_BK == 0 && ((a.G / PW_BK) & (a.G / PW_BK - 1)) == 0);
+}
+
+// Wide rows pay where the 256 x 128 tile needs more rounds of the grid than
+// the wide tile: 4096 -> 11008 at 2048 tokens, 688 tiles (2.69 rounds)
+// against 256 (one).
+bool prefill_wide_preferred(const ForwardArgs &a, int cus) {
+    if (!prefill_wide_supported(a) || a.M < 512 || a.N < 16 * 32 * kPwNrt) return false;
+    const int64_t tt = (a.M + PW_BM - 1) / PW_BM;
+    const int64_t wide = tt * ((a.N + 32 * kPwNrt - 1) / (32 * kPwNrt));
+    const int64_t tiles = ((a.M + PF_BM - 1) / PF_BM) * ((a.N + PF_BN - 1) / PF_BN);
+    const double t_wide = (double)((wide + cus - 1) / cus) * (32 * kPwNrt);
+    const double t_tile = (double)((tiles + cus - 1) / cus) * PF_BN;
+    return t_wide <= t_tile;
+}
+
+hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream_t stream) {
+    PrefillArgs p;
+    p.q = a.q;
+    p.scales = static_cast<const f16 *>(a.scales);
+    p.ngroups = a.ngroups;
+    p.G = a.G;
+    p.x = static_cast<const f16 *>(a.x);
+    p.y = static_cast<f16 *>(a.y);
+    p.bias = a.bias;
+    p.bias_dtype = a.bias_dtype;
+    p.M = a.M;
+    p.K = a.K;
+    p.N = a.N;
+    p.alpha = a.alpha;
+    p.nnz = (int32_t)a.nnz;
+    p.fold = a.has_ortho && plan != nullptr;
+    p.plan = static_cast<const PlanHeader *>(plan);
+    p.offsets = plan ? reinterpret_cast<const int32_t *>(static_cast<const char *>(plan) + sizeof(PlanHeader))
+                     : nullptr;
+    p.entries = plan ? reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(p.offsets) +
+                                                          plan_offsets_bytes(a.N, a.K))
+                     : nullptr;
+    p.nbm = (int)((a.M + PW_BM - 1) / PW_BM);
+    p.nbn = (int)((a.N + 32 * kPwNrt - 1) / (32 * kPwNrt));
+    const unsigned blocks = (unsigned)(p.nbm * p.nbn);
+    if (p.fold && p.nnz <= 0) return hipErrorInvalidValue;
+    const bool xb = a.io_dtype == ORTH_DT_BF16;
+    const int lds = pw_lds_bytes(kPwNrt);
+    if (p.fold && xb) hipLaunchKernelGGL((prefill_wide_kernel<kPwNrt, true, true>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+    else if (p.fold) hipLaunchKernelGGL((prefill_wide_kernel<kPwNrt, true, false>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+    else if (xb) hipLaunchKernelGGL((prefill_wide_kernel<kPwNrt, false, true>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+    else hipLaunchKernelGGL((prefill_wide_kernel<kPwNrt, false, false>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+    return hipGetLastError();
+}
+
 }  // namespace orth
 
 namespace orth {
@@ -804,6 +1301,14 @@ hipError_t prefill_prepare_device() {
                          reinterpret_cast<const void *>(prefill_kernel<false, true>)};
     for (const void *k : ks) {
         hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS_BYTES);
+        if (e != hipSuccess) return e;
+    }
+    const void *kw[4] = {reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, true, false>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, false, false>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, true, true>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, false, true>)};
+    for (const void *k : kw) {
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, pw_lds_bytes(kPwNrt));
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -157,7 +157,7 @@ int main(void) {
                                 (float *)ybuf, ybuf, ORTH_SIEVE_IEEE_DIV, NULL), ORTH_ERR_INVALID_ARGUMENT, "split rank");
     expect(orth_sieve_hdiag_hip(xbuf, ORTH_DT_F32, 4, 8, (float *)ybuf, 1, sbuf, 0, NULL), ORTH_ERR_INVALID_ARGUMENT,
            "hdiag workspace");
-    expect(orth_hip_set_kernel_policy(8), ORTH_ERR_INVALID_ARGUMENT, "policy");
+    expect(orth_hip_set_kernel_policy(9), ORTH_ERR_INVALID_ARGUMENT, "policy");
     expect(orth_hip_set_kernel_policy(0), ORTH_OK, "policy auto");
     orth_hip_device_info_t info;
     expect(orth_hip_device_info(0, NULL), ORTH_ERR_INVALID_ARGUMENT, "device info NULL");

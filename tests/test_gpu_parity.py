@@ -286,7 +286,8 @@ def test_prefill_every_tile(oracle_mod, shape, alpha, plan):
     L = W.config_layer(shape)
     x = W.make_x(2048, L.K, 3100 + L.N)
     y, k = run(L, x, alpha, plan=plan)
-    assert k == "prefill"
+    # (the wide-row kernel takes the metric's shape: one 256 x 352 tile per CU)
+    assert k == ("prefill_wide" if shape == "c2" else "prefill")
     rows = prefill_rows(2048)
     ref = oracle_y(oracle_mod, L, x[rows], alpha)
     rel = assert_close(y[rows], ref, tol=PREFILL_TOL, what=f"prefill {shape} alpha={alpha} plan={plan}")
