@@ -798,7 +798,10 @@ __host__ __device__ constexpr int pw_lds_bytes(int nrt) { return pw_trash_at(nrt
 
 struct PwA { u32x4 v[2]; };                    // 256 tokens x 64 bytes: 2 x 16 B per thread
 struct PwB { uint2 v[2]; uint32_t s[2]; };     // up to 2 half rows (8 bytes of nibbles) + scale bits
-struct PwE { uint32_t e[PW_E]; int brow[PW_E]; int total; };  // a thread's plan entries of one 64-column step (total: its block's count)
+// a thread's plan entries of one 64-column step: the entry words and the
+// row offset of their block in the range (even; bit 0 of brow[0]: the block
+// holds more entries than its threads prefetch)
+struct PwE { uint32_t e[PW_E]; int brow[PW_E]; };
 
 // f(integral_constant<int, k>) for k = 0 .. N-1, unrolled at compile time
 template <class F, int... Is>
@@ -806,12 +809,13 @@ __device__ __forceinline__ void pw_static_for(F &&f, std::integer_sequence<int, 
     (f(std::integral_constant<int, Is>{}), ...);
 }
 
-// Slot plan of a step (4 NRT MFMA slots): the 8 NJ dequantised byte pairs
-// spread evenly over the slots (byte b at slot b NRT / 4), the rest in the
-// gaps.  pw_dq_at: the byte pair of slot k, or -1.
-constexpr int pw_dq_at(int k, int nrt, int nbytes) {
+// Slot plan of a step (4 NRT MFMA slots, the barrier before the last 4):
+// the 8 NJ dequantised byte pairs spread evenly over the slots before the
+// barrier, the rest in the gaps.  pw_dq_at: the byte pair of slot k, or -1.
+constexpr int pw_dq_slot(int b, int nslots, int nbytes) { return (b * nslots) / nbytes; }
+constexpr int pw_dq_at(int k, int nslots, int nbytes) {
     for (int b = 0; b < nbytes; b++)
-        if ((b * nrt) / 4 == k) return b;
+        if (pw_dq_slot(b, nslots, nbytes) == k) return b;
     return -1;
 }
 
@@ -830,6 +834,11 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     const int64_t m0 = (int64_t)tt * PW_BM, n0 = (int64_t)rr * R;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: scalar addressing)
+    // the thread id formed again where the loop needs it (wave in a scalar
+    // register, the lane from v_mbcnt): keeping it live costs a register
+    auto tid_now = [&]() -> int {
+        return wave * 64 + (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    };
     const int wm = wave & 3, wn = wave >> 2;
     const int nk = (int)(a.K / PW_BK);
     const int nk64 = (int)(a.K / kPlanBK);
@@ -851,9 +860,8 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // or one XOR from these (the swizzle leaves bits 4 and up of a row alone)
     const int bwo = pw_swz(tid >> 1, (tid & 1) * 2);
     const int awo = pw_swz(tid >> 2, tid & 3);
-    auto qrow_of = [&](int i) -> uint32_t {
-        return min((uint32_t)(n0 + (job(i) >> 1)), (uint32_t)(a.N - 1));
-    };
+    const uint32_t qrow0 = (uint32_t)(n0 + (tid >> 1)), qh = (uint32_t)(tid & 1) * 8;
+    auto qrow_of = [&](int i) -> uint32_t { return min(qrow0 + (uint32_t)(i * (PW_NT / 2)), (uint32_t)(a.N - 1)); };
     const int gshift = a.ngroups == 1 ? 31 : __builtin_ctzll(a.G / PW_BK);
 
     // plan blocks of the row range, their offsets staged in LDS
@@ -899,8 +907,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         for (int i = 0; i < NJ; i++) {
             const uint32_t n = qrow_of(i);
             r.v[i] = __builtin_bit_cast(
-                uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, n * (uint32_t)(a.K >> 1) + (uint32_t)(job(i) & 1) * 8,
-                                                            u * (PW_BK / 2), 0));
+                uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2), 0));
             r.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, n * (uint32_t)(a.ngroups * 2), ((uint32_t)u >> gshift) * 2, 0);
         }
     };
@@ -937,19 +944,20 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // thread tid takes entries tid % 128 (+ 128 e) of block tid / 128 of the
     // row range (the range touches at most 4 blocks): two offset reads, no
     // search
-    const int eb = tid >> 7, ep = tid & 127;
     constexpr int EPB = PW_NT / PW_MAX_BLOCKS;  // threads per block
     auto load_e = [&](int u, PwE &r) {
+        const int eb = tid_now() >> 7, ep = tid_now() & (EPB - 1);
         u = min(u, nk64 - 1);
         const bool vb = eb < nb;
         const int o = (vb ? eb : 0) * (nk64 + 1) + u;
         const int l = offs[o], h = max(l, offs[o + 1]);
-        r.total = vb ? h - l : 0;  // (this thread's block)
+        const int total = vb ? h - l : 0;  // (this thread's block)
 #pragma unroll
         for (int e = 0; e < PW_E; e++) {
             r.e[e] = a.entries[min(max(l + ep + EPB * e, 0), a.nnz - 1)];
-            r.brow[e] = ep + EPB * e < r.total ? (b_lo + eb) * kPlanBN - (int)n0 : -(1 << 20);
+            r.brow[e] = ep + EPB * e < total ? (b_lo + eb) * kPlanBN - (int)n0 : -(1 << 20);
         }
+        r.brow[0] |= total > PW_E * EPB ? 1 : 0;
     };
     // alpha * v of every entry of 64-column step u whose column falls in
     // half `half` into the weight stage Bs (rows of the range only).  The
@@ -958,11 +966,11 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     auto cell = [&](f16 *Bs, int local, int c, uint32_t w, bool ok) {
         const float v = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xffffu));
         uint16_t *p = reinterpret_cast<uint16_t *>(
-            ok ? Bs + pw_swz(min(max(local, 0), R - 1), (c & 31) >> 3) + (c & 7) : trash + tid);
+            ok ? Bs + pw_swz(min(max(local, 0), R - 1), (c & 31) >> 3) + (c & 7) : trash + tid_now());
         *p = fold_add<XB>(*p, a.alpha * v);
     };
     auto one = [&](f16 *Bs, int half, uint32_t w, int brow) {
-        const int local = brow + (int)(w >> 24);
+        const int local = (brow & ~1) + (int)(w >> 24);
         const int c = (int)((w >> 16) & (kPlanBK - 1));
         cell(Bs, local, c, w, local >= 0 && local < R && (c >> 5) == half);
     };
@@ -973,17 +981,19 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     };
     // the rest (uniform branch): entries past the prefetched ones, or the
     // whole step for a plan with duplicate or unsorted columns
-    auto fold_rare = [&](int u, int half, int total, f16 *Bs) {
+    auto fold_rare = [&](int u, int half, f16 *Bs) {
         u = min(u, nk64 - 1);
         if (canonical) {
             // this thread's block holds more entries than the prefetched ones
-            const int l = offs[(eb < nb ? eb : 0) * (nk64 + 1) + u];
+            const int eb = tid_now() >> 7, ep = tid_now() & (EPB - 1);
+            const int o = (eb < nb ? eb : 0) * (nk64 + 1) + u;
+            const int l = offs[o], total = eb < nb ? max(l, offs[o + 1]) - l : 0;
             for (int v = PW_E * EPB + ep; v < total; v += EPB)
                 one(Bs, half, a.entries[min(max(l + v, 0), a.nnz - 1)], (b_lo + eb) * kPlanBN - (int)n0);
         } else {
             // one thread per row applies the row's entries of the step in
             // plan order (the result is reproducible bit for bit)
-            for (int lr = tid; lr < R; lr += PW_NT) {
+            for (int lr = tid_now(); lr < R; lr += PW_NT) {
                 const int64_t n = n0 + lr;
                 if (n >= a.N) break;
                 const int bb = (int)(n / kPlanBN) - b_lo;
@@ -1036,7 +1046,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     __syncthreads();
     if (FOLD) {
         fold_common(0, re, Bst(0));
-        if (!canonical || re.total > PW_E * EPB) fold_rare(0, 0, re.total, Bst(0));
+        if (!canonical || (re.brow[0] & 1)) fold_rare(0, 0, Bst(0));
         load_e(0, re);
     }
     __syncthreads();
@@ -1054,24 +1064,30 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // the two waves of a SIMD in the same phase: 3,600 cycles a step
     // against 1,408 of MFMAs.)
     int b3 = 0;  // t % 3
+    constexpr int PRE = 4 * NRT - 4;  // slots before the step's barrier
     const int aro = pw_swz(lane & 15, lane >> 4);
+    // operand reads: row 16 m + lr, chunk lc sits at aro + 16 m rows (the
+    // swizzle depends on the row's bits 1..3 only).  A step's A operands and
+    // its first B operand are read at the end of the step before (after its
+    // barrier), into the registers its last MFMAs free.
+    f16x8 af[4], bcur, bnext;
+    {
+        const f16 *Ar = Ast(0) + aro + 64 * wm * PW_BK, *Br = Bst(0) + aro + (R / 2) * wn * PW_BK;
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const f16x8 *>(Ar + 16 * i * PW_BK);
+        bnext = *reinterpret_cast<const f16x8 *>(Br);
+    }
     for (int t = 0; t < nk; t++) {
         __builtin_amdgcn_sched_barrier(0);
         const int b3_1 = b3 == 2 ? 0 : b3 + 1, b3_2 = b3 == 0 ? 2 : b3 - 1;
         const int u1 = (t + 1) >> 1, h1 = (t + 1) & 1;
-        const int total1 = FOLD ? re.total : 0;
-        const bool rare = FOLD && (!canonical || total1 > PW_E * EPB);  // (per thread: its block overflows)
-        const f16 *As = Ast(t & 1), *Bs = Bst(b3);
+        const bool rare = FOLD && (!canonical || (re.brow[0] & 1));  // (per thread: its block overflows)
+        const f16 *Bs = Bst(b3);
         f16 *Bw = Bst(b3_2), *Bf = Bst(b3_1), *Aw = Ast((t + 1) & 1);
 
-        // operand reads: row 16 m + lr, chunk lc sits at aro + 16 m rows
-        // (the swizzle depends on the row's bits 1..3 only)
-        f16x8 af[4], bcur, bnext;
-        const f16 *Ar = As + aro + 64 * wm * PW_BK, *Br = Bs + aro + (R / 2) * wn * PW_BK;
-#pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const f16x8 *>(Ar + 16 * i * PW_BK);
-        bnext = *reinterpret_cast<const f16x8 *>(Br);
-        __builtin_amdgcn_sched_barrier(0);
+        const f16 *Br = Bs + aro + (R / 2) * wn * PW_BK;
+        // the next step's operands (read after this step's barrier)
+        const f16 *An = Ast((t + 1) & 1) + aro + 64 * wm * PW_BK, *Bn = Bst(b3_1) + aro + (R / 2) * wn * PW_BK;
 
         // dequantisation state of the current job and word
         f16x2 s2 = {};
@@ -1080,7 +1096,6 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         // fold state
         uint16_t *fp = nullptr;
         uint16_t fold_old = 0;
-        float fold_add_v = 0.f;
 
         pw_static_for([&](auto kc) {
             constexpr int k = decltype(kc)::value;
@@ -1089,13 +1104,24 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                 bcur = bnext;
                 if constexpr (j + 1 < NRT) bnext = *reinterpret_cast<const f16x8 *>(Br + 16 * (j + 1) * PW_BK);
             }
+            if constexpr (k == PRE) {
+                // every LDS write of the step is issued: the rest of an
+                // overflowing fold, then the barrier; the step's last four
+                // MFMAs then cover the next step's first operand reads
+                if (rare) fold_rare(u1, h1, Bf);
+                __syncthreads();
+            }
             if constexpr (XB)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
                                                                     __builtin_bit_cast(bf16x8, bcur), acc[i][j], 0, 0, 0);
             else
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bcur, acc[i][j], 0, 0, 0);
+            if constexpr (k >= PRE) {
+                af[i] = *reinterpret_cast<const f16x8 *>(An + 16 * i * PW_BK);
+                if constexpr (i == 0) bnext = *reinterpret_cast<const f16x8 *>(Bn);
+            }
 
-            constexpr int q = pw_dq_at(k, NRT, 8 * NJ);
+            constexpr int q = pw_dq_at(k, PRE, 8 * NJ);
             if constexpr (q >= 0) {
                 // B(t+2): job q / 8, word (q / 4) % 2, byte q % 4
                 constexpr int jb = q / 8, w = (q / 4) % 2, b = q % 4;
@@ -1132,34 +1158,32 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
             }
             // B(t+3) loads of job c, in the slot after job c's last byte pair
             // (a full step before job 0's first use, most of one for job 1)
-            constexpr int bl = (k == ((8 * 0 + 7) * NRT) / 4 + 1) ? 0 : (NJ > 1 && k == ((8 * 1 + 7) * NRT) / 4 + 1) ? 1 : -1;
+            constexpr int bl = (k == pw_dq_slot(8 * 0 + 7, PRE, 8 * NJ) + 1)              ? 0
+                               : (NJ > 1 && k == pw_dq_slot(8 * 1 + 7, PRE, 8 * NJ) + 1) ? 1
+                                                                                          : -1;
             if constexpr (bl >= 0) {
                 const int u = min(t + 3, nk - 1);
                 const uint32_t n = qrow_of(bl);
                 rb.v[bl] = __builtin_bit_cast(
-                    uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, n * (uint32_t)(a.K >> 1) + (uint32_t)(job(bl) & 1) * 8,
-                                                                u * (PW_BK / 2), 0));
+                    uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2), 0));
                 rb.s[bl] = __builtin_amdgcn_raw_buffer_load_b16(rs, n * (uint32_t)(a.ngroups * 2), ((uint32_t)u >> gshift) * 2, 0);
             }
             if constexpr (FOLD && k == 9) {
                 // fold of B(t+1), prefetched entry: the cell (or the trash cell)
                 const uint32_t w = re.e[0];
-                const int local = (canonical ? re.brow[0] : -(1 << 20)) + (int)(w >> 24);
+                const int local = (canonical ? (re.brow[0] & ~1) : -(1 << 20)) + (int)(w >> 24);
                 const int c = (int)((w >> 16) & (kPlanBK - 1));
                 const bool ok = local >= 0 && local < R && (c >> 5) == h1;
                 fp = reinterpret_cast<uint16_t *>(ok ? Bf + pw_swz(min(max(local, 0), R - 1), (c & 31) >> 3) + (c & 7)
-                                                     : trash + tid);
-                fold_add_v = a.alpha * (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xffffu));
+                                                     : trash + tid_now());
                 fold_old = *fp;
             }
-            if constexpr (FOLD && k == 14) *fp = fold_add<XB>(fold_old, fold_add_v);
+            if constexpr (FOLD && k == 14)  // (the value recomputed here: one register less across the slots)
+                *fp = fold_add<XB>(fold_old, a.alpha * (float)__builtin_bit_cast(f16, (uint16_t)(re.e[0] & 0xffffu)));
             if constexpr (FOLD && k == 25) load_e((t + 2) >> 1, re);  // the next step's entries
             __builtin_amdgcn_sched_barrier(0);
         }, std::make_integer_sequence<int, 4 * NRT>{});
-        static_assert(4 * NRT >= ((8 * NJ - 1) * NRT) / 4 + 2 && 4 * NRT > 25, "every slice of the step needs a slot");
-
-        if (rare) fold_rare(u1, h1, total1, Bf);
-        __syncthreads();
+        static_assert(pw_dq_slot(8 * NJ - 1, PRE, 8 * NJ) + 1 < PRE && PRE > 25, "every slice of the step needs a slot");
         b3 = b3_1;
     }
 
