@@ -81,6 +81,9 @@ def parse():
                          + ", ".join(PROFILE_WORKLOADS))
     ap.add_argument("--profile-steps", type=int, default=50,
                     help="forwards (blocks for c5) per --profile-workload run")
+    ap.add_argument("--profile-replays", type=int, default=0,
+                    help="--profile-workload: capture the steps in one HIP graph and replay it this many "
+                         "times (as the timed bench lines run them); 0: eager launches (counter passes)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two --profile counter runs into profiles/traffic.json")
     return ap.parse_args()
@@ -639,16 +642,58 @@ PROFILE_WORKLOADS = {
     "c1_m1_a0": ("c1", 1, 0.0), "c3_m2048_a1": ("c3", 2048, 1.0), "c3_m2048_a0": ("c3", 2048, 0.0),
     "c4_m8_a1": ("c4", 8, 1.0), "c5_m1": ("c5", 1, 1.0), "c5_m1_grouped": ("c5", 1, 1.0),
     "c5_m32": ("c5", 32, 1.0), "c5_m32_grouped": ("c5", 32, 1.0), "copy": (None, 0, 0.0),
+    # the bench's BF16 / FP32-activation lines and its per-row 4000->11008 layer
+    "c2_m1_bf16": ("c2", 1, 1.0, "bf16"), "c2_m8_bf16": ("c2", 8, 1.0, "bf16"),
+    "c2_m32_bf16": ("c2", 32, 1.0, "bf16"), "c5down_m8_bf16": ("c5down", 8, 1.0, "bf16"),
+    "c2_m2048_bf16": ("c2", 2048, 1.0, "bf16"), "c2_m1_fp32": ("c2", 1, 1.0, "fp32"),
+    "c2_m8_fp32": ("c2", 8, 1.0, "fp32"), "odd_m1": ("odd", 1, 1.0),
 }
 
 
-def profile_workload(torch, name, steps):
-    """Eager forwards of one workload (no graph: a kernel trace or counter
-    pass sees one dispatch per launch), each with its cached plan, weights
-    rotated past the Infinity Cache as in the timed runs; ``copy``: device
-    copies of COPY_BYTES (the FETCH_SIZE / WRITE_SIZE calibration)."""
+def graph_replays(torch, fn, steps, replays):
+    """fn(i), i < steps, captured in one HIP graph on a stream of its own
+    (after one eager call there, which sizes any per-stream buffer), then
+    the graph replayed `replays` times back to back."""
+    global _HIP
+    if _HIP is None:
+        _HIP = _Hip()
+    H, c = _HIP, _HIP.c
+    s = H.new("hipStreamCreate")
+    ts = torch.cuda.ExternalStream(s.value)
+    g, ex = None, None
+    try:
+        with torch.cuda.stream(ts):
+            fn(0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(ts):
+            H("hipStreamBeginCapture", s, 2)
+            for i in range(steps):
+                fn(i)
+            g = c.c_void_p()
+            H("hipStreamEndCapture", s, c.byref(g))
+        ex = H.new("hipGraphInstantiate", g, None, None, 0)
+        for _ in range(replays):
+            H("hipGraphLaunch", ex, s)
+        H("hipStreamSynchronize", s)
+    finally:
+        torch.cuda.synchronize()
+        if ex is not None:
+            H("hipGraphExecDestroy", ex)
+        if g is not None:
+            H("hipGraphDestroy", g)
+        H("hipStreamDestroy", s)
+
+
+def profile_workload(torch, name, steps, replays=0):
+    """Forwards of one workload, each with its cached plan, weights rotated
+    past the Infinity Cache as in the timed runs: eager (a counter pass sees
+    one dispatch per launch), or with ``replays`` captured in one HIP graph
+    and replayed that many times (the launches the timed lines measure);
+    ``copy``: device copies of COPY_BYTES (the FETCH_SIZE / WRITE_SIZE
+    calibration)."""
     from libortho_amd import _C_ops, workloads as W
-    cfg, M, alpha = PROFILE_WORKLOADS[name]
+    cfg, M, alpha = PROFILE_WORKLOADS[name][:3]
+    dtype = {"bf16": torch.bfloat16, "fp32": torch.float32}.get((PROFILE_WORKLOADS[name] + ("",))[3], torch.float16)
     kernels = set()
     if cfg is None:
         src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
@@ -663,7 +708,8 @@ def profile_workload(torch, name, steps):
         xs = {K: torch.from_numpy(W.make_x(M, K, 7100 + K)).cuda() for K in {l.K for l in layers}}
         ys = [torch.empty(M, l.N, dtype=torch.float16, device="cuda") for l in layers]
         groups = [[0, 1, 2], [3], [4, 5], [6]] if name.endswith("grouped") else [[j] for j in range(len(layers))]
-        for i in range(steps):
+
+        def fn(i):
             for g in groups:
                 if len(g) == 1:
                     rots[g[0]].call(i, xs[layers[g[0]].K], ys[g[0]], 1.0)
@@ -671,15 +717,31 @@ def profile_workload(torch, name, steps):
                     _C_ops.forward_group([rots[j].desc(i, 1.0) for j in g], xs[layers[g[0]].K], [ys[j] for j in g],
                                          [rots[j].plans[i % rots[j].n] for j in g])
                 kernels.add(_C_ops.last_kernel())
+        if replays:
+            graph_replays(torch, fn, steps, replays)
+        else:
+            for i in range(steps):
+                fn(i)
     else:
-        layer = W.config_layer(cfg)
-        rot = Rotation(layer, torch, plan=alpha > 0) if M < 2048 else \
+        if cfg == "c5down":
+            layer = {l.name: l for l in W.llama_block()}["down_proj"]
+        elif cfg == "odd":
+            layer = W.make_layer(4000, 11008, None, 0.01, 4000)
+        else:
+            layer = W.config_layer(cfg)
+        rot = Rotation(layer, torch, plan=alpha > 0) if M < 2048 or replays else \
             Rotation(layer, torch, min_copies=2, min_bytes=0, plan=alpha > 0)
-        x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda()
-        y = torch.empty(M, layer.N, dtype=torch.float16, device="cuda")
-        for i in range(steps):
+        x = torch.from_numpy(W.make_x(M, layer.K, 7000 + M)).cuda().to(dtype)
+        y = torch.empty(M, layer.N, dtype=dtype, device="cuda")
+
+        def fn(i):
             rot.call(i, x, y, alpha)
             kernels.add(_C_ops.last_kernel())
+        if replays:
+            graph_replays(torch, fn, steps, replays)
+        else:
+            for i in range(steps):
+                fn(i)
     torch.cuda.synchronize()
     print(json.dumps({"profile_workload": name, "steps": steps, "kernels": sorted(kernels)}), flush=True)
 
@@ -790,7 +852,7 @@ def main():
             print(f"bench.py: unknown workload {args.profile_workload!r}; one of {', '.join(PROFILE_WORKLOADS)}",
                   file=sys.stderr)
             sys.exit(2)
-        profile_workload(torch, args.profile_workload, args.profile_steps)
+        profile_workload(torch, args.profile_workload, args.profile_steps, args.profile_replays)
         return
     if args.profile_prefill:
         import torch
