@@ -103,12 +103,14 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  *   output  [batch_size, out_features] of io_dtype, written in full
  * Picks, for FP16 I/O and the supported shapes, the decode kernel (batch <=
  * 4), the one-launch mid-batch kernel (5..16, K = 4096, a plan or no ortho
- * term), the slice-split kernel (17..32, K % 128 == 0, a plan or no ortho
- * term), the quarter-split kernel (17..32, K = 4096, when the slice-split
- * kernel cannot take the call), the split-K mid-batch kernel (other
- * batches up to 64), the MFMA prefill
- * kernel (above), and a general kernel for shapes and dtypes the fast
- * kernels do not take (orth_hip_last_kernel() names the choice).  BF16 I/O
+ * term), the quarter-split kernel (17..32, K = 4096, a plan or no ortho
+ * term), the slice-split kernel (17..32 at the other K % 128 == 0, a plan
+ * or no ortho term), the split-K mid-batch kernel (other batches up to 64),
+ * the MFMA prefill kernels above (one 256 x 352 tile per workgroup where
+ * that needs fewer rounds of the grid than 256 x 128 tiles, as at
+ * 4096 -> 11008 with 2048 tokens), and a general kernel for shapes and
+ * dtypes the fast kernels do not take (orth_hip_last_kernel() names the
+ * choice).  BF16 I/O
  * takes the decode kernel for 1..4 tokens and the one-launch mid-batch
  * kernel for 5..16 (both K = 4096 with a plan or no ortho term), the
  * slice-split kernel for 17..32 (K % 128 == 0, a plan or no ortho term),
@@ -312,7 +314,8 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info);
  * default), 1 = decode, 2 = prefill, 3 = general, 4 = split-K mid-batch
  * (5..64 tokens), 5 = one-launch mid-batch (5..16 tokens), 6 = K quarters
  * over the grid (17..32 tokens, K = 4096), 7 = 1024-column slices over the
- * grid (1..32 tokens).  A forced kernel that cannot take a call returns
+ * grid (1..32 tokens), 8 = the prefill kernel with one 256 x 352 tile per
+ * workgroup (any batch).  A forced kernel that cannot take a call returns
  * ORTH_ERR_UNSUPPORTED.  Process-wide. */
 int orth_hip_set_kernel_policy(int policy);
 int orth_hip_get_kernel_policy(void);
@@ -321,7 +324,8 @@ int orth_hip_get_kernel_policy(void);
  * 1 decode, 2 prefill, 3 general, 4 split-K mid-batch, 5 decode for a
  * group of layers in one launch (orth_layers_forward_hip), 6 one-launch
  * mid-batch, 7 K quarters over the grid, 8 1024-column slices over the
- * grid, 9 the same for a group of layers in one launch, 0 none. */
+ * grid, 9 the same for a group of layers in one launch, 10 prefill with
+ * one 256 x 352 tile per workgroup, 0 none. */
 int orth_hip_last_kernel(void);
 
 /* Device clock stamp for timing stream-ordered work (benchmarks; no
