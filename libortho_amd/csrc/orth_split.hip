@@ -23,8 +23,9 @@
 //    v_mfma_f32_16x16x32_f16 for both token tiles.  The bias (1032 per even
 //    and 72 per odd column, 136 per column in BF16) times the activation sums
 //    is formed once per launch by MFMAs of the A operands against a constant
-//    B (the conversion of q = 0), kept in a 1 KB LDS table [chunk][token],
-//    and removed from each chunk's partial before its group scale.
+//    B (the conversion of q = 0) and kept, negated, in 16 registers: it
+//    starts each chunk's MFMA chain, so the chain yields the chunk's partial
+//    without the bias and one FMA applies the group scale.
 //  * The four waves of a row half hold the slice's four chunk pairs; their
 //    partials meet in LDS and are added in wave order (deterministic).
 //  * Ortho term (alpha > 0, planned): the same loads are staged a second
@@ -93,7 +94,7 @@ struct SplitArgs {
     int S;              // slices
     int wps;            // workgroups per slice
     int ngrp;           // 64-row groups of all layers
-    int lds_xt, lds_red, lds_sp, lds_rec, lds_bt;  // byte offsets of the LDS regions
+    int lds_xt, lds_red, lds_sp, lds_rec;  // byte offsets of the LDS regions
     int swords;         // record words (every layer)
 };
 
@@ -109,7 +110,6 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     f16 *xs = reinterpret_cast<f16 *>(smem);                    // [32 tokens][kSpXS] row-major (prologue)
     f16 *xt = reinterpret_cast<f16 *>(smem + a.lds_xt);
-    float *bt = reinterpret_cast<float *>(smem + a.lds_bt);      // [8 chunks][32 tokens] bias sums
     float *red = reinterpret_cast<float *>(smem + a.lds_red);    // [4 pairs][64 rows][RS]
     float *sp = reinterpret_cast<float *>(smem + a.lds_sp);      // [64 rows][RS]
     // column c of the transposed slice: its 32 tokens, 16 bytes of padding
@@ -232,10 +232,13 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
                                                           __builtin_bit_cast(f16x8, u32x4{b[0], b[1], b[2], b[3]}),
                                                           c, 0, 0, 0);
     };
-    // the conversion of q = 0: every column's bias; the sums in a table
-    // [chunk of the slice][token], written by one row half's lanes of row 0
+    // the conversion of q = 0: every column's bias.  Its sums per chunk and
+    // token (the same in every column of the product), negated, start each
+    // chunk's MFMA chain below: the chain then yields the partial with the
+    // bias removed, and only the group scale is left to apply.
     const uint32_t kb[4] = {XB ? 0x43084308u : 0x64086408u, XB ? 0x43084308u : 0x54805480u,
                             XB ? 0x43084308u : 0x64086408u, XB ? 0x43084308u : 0x54805480u};
+    f32x4 nbias[2][NTT];
 #pragma unroll
     for (int t = 0; t < NTT; t++)
 #pragma unroll
@@ -243,7 +246,7 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
             f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) z = mfma(afr[t][p][kk], kb, z);
-            if (rh == 0 && nl == 0) *reinterpret_cast<f32x4 *>(bt + (2 * kq + p) * kSpMT + 16 * t + 4 * g) = z;
+            nbias[p][t] = -z;
         }
     __syncthreads();  // every wave has its A operands: the row-major copy's space is reused below
 
@@ -364,7 +367,7 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
         }
 
         // ---- dense term: row tiles x chunks, both token tiles; each chunk's
-        //      partial loses its bias sums and takes its group scale
+        //      chain starts at minus its bias sums and takes its group scale
         f32x4 acc[2][NTT];
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
@@ -378,7 +381,7 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
                     const uint32_t u[4] = {cur.w[rt][p].x, cur.w[rt][p].y, cur.w[rt][p].z, cur.w[rt][p].w};
                     f32x4 part[NTT];
 #pragma unroll
-                    for (int t = 0; t < NTT; t++) part[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int t = 0; t < NTT; t++) part[t] = nbias[p][t];
 #pragma unroll
                     for (int kk = 0; kk < 4; kk++) {
                         uint32_t bw[4];
@@ -389,11 +392,9 @@ __global__ void __launch_bounds__(kSpNT) split_kernel(SplitArgs a) {
                     }
                     const float scl = (float)__builtin_bit_cast(f16, (uint16_t)cur.sc[rt][p]);
 #pragma unroll
-                    for (int t = 0; t < NTT; t++) {
-                        const f32x4 bs = *reinterpret_cast<const f32x4 *>(bt + (2 * kq + p) * kSpMT + 16 * t + 4 * g);
+                    for (int t = 0; t < NTT; t++)
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[rt][t][i] += scl * (part[t][i] - bs[i]);
-                    }
+                        for (int i = 0; i < 4; i++) acc[rt][t][i] = __builtin_fmaf(scl, part[t][i], acc[rt][t][i]);
                 }
             }
         }
@@ -577,8 +578,8 @@ static bool split_shape(const ForwardArgs *as, const void *const *plans, int cou
     const ForwardArgs &a = as[0];
     const int nchunks = (int)(a.K / 128);
     const int S = (nchunks + 7) / 8;
-    // the row-major staging (prologue) at 0, the transposed one after it,
-    // the bias table after those; after the prologue the row-major space
+    // the row-major staging (prologue) at 0, the transposed one after it;
+    // after the prologue the row-major space
     // holds the partials [4][64][RS], the sparse sums [64][RS] and the waves'
     // records
     auto al = [](int64_t v) { return (v + 15) & ~int64_t(15); };
@@ -588,8 +589,7 @@ static bool split_shape(const ForwardArgs *as, const void *const *plans, int cou
     const int64_t lds_rec = lds_sp + (sh.sparse ? al(kSpRows * kSpRS * 4) : 0);
     if (lds_rec + (int64_t)kSpW * sh.swords * 4 > xs_bytes) return false;
     const int64_t lds_xt = xs_bytes;
-    const int64_t lds_bt = lds_xt + (sh.sparse ? al((int64_t)kSpCols * kSpMT * 2 + (kSpCols / 8) * 16) : 0);
-    const int64_t total = lds_bt + 8 * kSpMT * 4;
+    const int64_t total = lds_xt + (sh.sparse ? al((int64_t)kSpCols * kSpMT * 2 + (kSpCols / 8) * 16) : 0);
     if (total > kSpLdsMax) return false;
     sh.lds = (int)total;
     // one workgroup per CU: S slices x wps workgroups, each with >= 1 group
@@ -632,7 +632,6 @@ static bool split_shape(const ForwardArgs *as, const void *const *plans, int cou
         d->lds_red = (int)lds_red;
         d->lds_sp = (int)lds_sp;
         d->lds_rec = (int)lds_rec;
-        d->lds_bt = (int)lds_bt;
         d->swords = sh.swords;
     }
     return true;
