@@ -773,22 +773,24 @@ constexpr int PW_A_BYTES = PW_BM * PW_BK * 2;  // one activation stage (16 KB)
 constexpr int PW_MAX_BLOCKS = 4;               // plan blocks a row range may touch
 constexpr int PW_E = 1;                        // plan entries per thread prefetched per 64-column step
 
-// LDS rows of 4 chunks of 16 bytes; chunk c of row r sits at c ^ g(r),
-// g(r) = (r1 ^ r2 ^ r3) | r2 << 1 (r_i: bit i of r).  Whether a phase of a
-// 16-byte access serves 8 lanes (32 banks) or 16 (64 banks), its lanes fall
-// in distinct bank groups for the three patterns used: 8 / 16 consecutive
-// rows of one chunk (the MFMA operand reads), rows of 4 chunks (activation
-// writes) and row pairs of chunks {w, w + 2} (weight writes).  (A swizzle
-// by (r >> 2) & 3, distinct only for 16-lane phases, measured 43 % of the
-// LDS's active cycles stalled on bank conflicts.)
+// LDS layout of a stage: rows r and r + 1 (r even) share a 128-byte line,
+// chunk c (16 bytes, 8 columns) of row r at slot ((r % 2) * 4 + c) ^ (line
+// % 8) of line r / 2.  Measured with a probe of ds_read_b128 access tables
+// on gfx950 (SQ_LDS_BANK_CONFLICT): conflict-free for the MFMA operand
+// read (16 rows of one chunk per 16 lanes) and for writes of 4 lanes per
+// row (the 4 chunks of a row: the coalesced loads' mapping, used for both
+// stages); row-major 64-byte rows conflicted 2-way on the operand read
+// whatever their XOR swizzle (43 % of the LDS's active cycles stalled),
+// and a chunk-major tile 4-way on these writes.  Result in halves.
 __device__ __forceinline__ int pw_swz(int r, int c) {
-    const int g = (((r >> 1) ^ (r >> 2) ^ (r >> 3)) & 1) | ((r >> 1) & 2);
-    return r * PW_BK + ((c ^ g) << 3);
+    const int line = r >> 1;
+    return line * 64 + (((((r & 1) << 2) | c) ^ (line & 7)) << 3);
 }
 
-// A weight stage holds max(R, 512) rows: a thread's second half-row job
-// lands in rows R .. 511 when it has none (never read; no branch).
-__host__ __device__ constexpr int pw_b_rows(int nrt) { return 32 * nrt > PW_NT ? 32 * nrt : PW_NT; }
+// A weight stage holds the rows the chunk jobs reach (a thread's last job
+// lands in rows past R when there is none: never read; no branch).
+__host__ __device__ constexpr int pw_njobs(int nrt) { return (4 * 32 * nrt + PW_NT - 1) / PW_NT; }
+__host__ __device__ constexpr int pw_b_rows(int nrt) { return pw_njobs(nrt) * PW_NT / 4; }
 __host__ __device__ constexpr int pw_b_bytes(int nrt) { return pw_b_rows(nrt) * PW_BK * 2; }
 __host__ __device__ constexpr int pw_off_at(int nrt) { return 2 * PW_A_BYTES + 3 * pw_b_bytes(nrt); }
 __host__ __device__ constexpr int pw_trash_at(int nrt) {
@@ -797,7 +799,7 @@ __host__ __device__ constexpr int pw_trash_at(int nrt) {
 __host__ __device__ constexpr int pw_lds_bytes(int nrt) { return pw_trash_at(nrt) + PW_NT * 2; }
 
 struct PwA { u32x4 v[2]; };                    // 256 tokens x 64 bytes: 2 x 16 B per thread
-struct PwB { uint2 v[2]; uint32_t s[2]; };     // up to 2 half rows (8 bytes of nibbles) + scale bits
+struct PwB { uint32_t v[3]; uint32_t s[3]; };  // up to 3 chunks (a 4-byte word of nibbles each) + scale bits
 // a thread's plan entries of one 64-column step: the entry words and the
 // row offset of their block in the range (even; bit 0 of brow[0]: the block
 // holds more entries than its threads prefetch)
@@ -810,7 +812,7 @@ __device__ __forceinline__ void pw_static_for(F &&f, std::integer_sequence<int, 
 }
 
 // Slot plan of a step (4 NRT MFMA slots, the barrier before the last 4):
-// the 8 NJ dequantised byte pairs spread evenly over the slots before the
+// the 4 NJ dequantised byte pairs spread evenly over the slots before the
 // barrier, the rest in the gaps.  pw_dq_at: the byte pair of slot k, or -1.
 constexpr int pw_dq_slot(int b, int nslots, int nbytes) { return (b * nslots) / nbytes; }
 constexpr int pw_dq_at(int k, int nslots, int nbytes) {
@@ -822,8 +824,8 @@ constexpr int pw_dq_at(int k, int nslots, int nbytes) {
 template <int NRT, bool FOLD, bool XB>
 __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     constexpr int R = 32 * NRT;                 // rows of the workgroup tile
-    constexpr int NJ = (2 * R + PW_NT - 1) / PW_NT;  // half-row jobs per thread (dequantisation)
-    static_assert(NJ <= 2, "two half-row jobs per thread at most");
+    constexpr int NJ = pw_njobs(NRT);  // chunk jobs per thread (dequantisation: 8 weights each)
+    static_assert(NJ <= 3, "three chunk jobs per thread at most");
     extern __shared__ __align__(16) unsigned char smem[];
     f16 *As0 = reinterpret_cast<f16 *>(smem);
     f16 *Bs0 = reinterpret_cast<f16 *>(smem + 2 * PW_A_BYTES);
@@ -846,22 +848,24 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // per-thread byte offsets (step 0) of the first chunk / job; the others
     // are formed at each load (registers are the limit here).  Rows past M
     // / N repeat the last row.
+    // activation chunk i of this thread: idx = tid + 512 i, row idx / 4,
+    // chunk idx % 4 (4 lanes read a row's 64 contiguous bytes)
     const uint32_t xrow = (uint32_t)(m0 + (tid >> 2));
     const uint32_t xcol = (uint32_t)((tid & 3) * 16);
     auto xoff = [&](int i) -> uint32_t {
-        return min(xrow + (uint32_t)(i * (PW_NT / 4)), (uint32_t)(a.M - 1)) * (uint32_t)(a.K * 2) + xcol;
+        return min(xrow + (uint32_t)(i * (PW_NT / 4)), (uint32_t)(a.M - 1)) * (uint32_t)(a.K * 2) + xcol;  // (+128 rows)
     };
-    // half-row job i of this thread: tid + 512 i (row job / 2, chunks 2 (job
-    // % 2) and 2 (job % 2) + 1); past 2 R it writes the stage's spare rows
+    // weight job i of this thread: j = tid + 512 i, row j / 4, chunk j % 4
+    // (the same mapping as the activations: 4 lanes read a row's 16
+    // contiguous bytes of nibbles); past 4 R it writes the stage's spare rows
     auto job = [&](int i) -> int { return tid + PW_NT * i; };
-    static_assert(PW_NT * NJ / 2 <= pw_b_rows(NRT), "half-row jobs stay inside the stage");
+    static_assert(PW_NT * NJ / 4 <= pw_b_rows(NRT) && pw_b_rows(NRT) >= R, "chunk jobs stay inside the stage");
     // LDS write offsets (halves) of job 0, chunk 2 (tid % 2), and of the
     // thread's first activation chunk: the other writes are fixed offsets
     // or one XOR from these (the swizzle leaves bits 4 and up of a row alone)
-    const int bwo = pw_swz(tid >> 1, (tid & 1) * 2);
-    const int awo = pw_swz(tid >> 2, tid & 3);
-    const uint32_t qrow0 = (uint32_t)(n0 + (tid >> 1)), qh = (uint32_t)(tid & 1) * 8;
-    auto qrow_of = [&](int i) -> uint32_t { return min(qrow0 + (uint32_t)(i * (PW_NT / 2)), (uint32_t)(a.N - 1)); };
+    const int awo = pw_swz(tid >> 2, tid & 3);  // (also job 0's; job / chunk i: + 128 i rows)
+    const uint32_t qrow0 = (uint32_t)(n0 + (tid >> 2)), qh = (uint32_t)(tid & 3) * 4;
+    auto qrow_of = [&](int i) -> uint32_t { return min(qrow0 + (uint32_t)(i * (PW_NT / 4)), (uint32_t)(a.N - 1)); };
     const int gshift = a.ngroups == 1 ? 31 : __builtin_ctzll(a.G / PW_BK);
 
     // plan blocks of the row range, their offsets staged in LDS
@@ -906,38 +910,32 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < NJ; i++) {
             const uint32_t n = qrow_of(i);
-            r.v[i] = __builtin_bit_cast(
-                uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2), 0));
+            r.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2), 0);
             r.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, n * (uint32_t)(a.ngroups * 2), ((uint32_t)u >> gshift) * 2, 0);
+        }
+    };
+    // one chunk (8 weights) of a word of nibbles, fp16(q * s) or bf16(q * s)
+    auto dq_chunk = [&](uint32_t word, uint32_t sbits) -> u32x4 {
+        const f16 sc = __builtin_bit_cast(f16, (uint16_t)sbits);
+        if constexpr (XB) {
+            const float sf = (float)sc;
+            const uint32_t lo = (word & 0x0F0F0F0Fu) ^ 0x08080808u;
+            const uint32_t hi = ((word >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+            auto pair = [&](int b) {
+                return pk_bf16(__builtin_fmaf((float)((lo >> (8 * b)) & 0xFFu), sf, -8.0f * sf),
+                               __builtin_fmaf((float)((hi >> (8 * b)) & 0xFFu), sf, -8.0f * sf));
+            };
+            return u32x4{pair(0), pair(1), pair(2), pair(3)};
+        } else {
+            const f16x2 s2 = {sc, sc};
+            return u32x4{dq_byte(word, s2, 0), dq_byte(word, s2, 1), dq_byte(word, s2, 2), dq_byte(word, s2, 3)};
         }
     };
     auto store_b = [&](const PwB &r, f16 *Bs) {
 #pragma unroll
         for (int i = 0; i < NJ; i++) {
             const int j = job(i);
-            const int row = j >> 1, c0 = (j & 1) * 2;
-            const f16 sc = __builtin_bit_cast(f16, (uint16_t)r.s[i]);
-            const f16x2 s2 = {sc, sc};
-            const float sf = (float)sc;
-            const uint32_t words[2] = {r.v[i].x, r.v[i].y};
-#pragma unroll
-            for (int w = 0; w < 2; w++) {
-                u32x4 o;
-                if constexpr (XB) {
-                    const uint32_t lo = (words[w] & 0x0F0F0F0Fu) ^ 0x08080808u;
-                    const uint32_t hi = ((words[w] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
-                    const float s8 = -8.0f * sf;
-                    auto pair = [&](int b) {
-                        return pk_bf16(__builtin_fmaf((float)((lo >> (8 * b)) & 0xFFu), sf, s8),
-                                       __builtin_fmaf((float)((hi >> (8 * b)) & 0xFFu), sf, s8));
-                    };
-                    o = u32x4{pair(0), pair(1), pair(2), pair(3)};
-                } else {
-                    o = u32x4{dq_byte(words[w], s2, 0), dq_byte(words[w], s2, 1), dq_byte(words[w], s2, 2),
-                              dq_byte(words[w], s2, 3)};
-                }
-                *reinterpret_cast<u32x4 *>(Bs + pw_swz(row, c0 + w)) = o;
-            }
+            *reinterpret_cast<u32x4 *>(Bs + pw_swz(j >> 2, j & 3)) = dq_chunk(r.v[i], r.s[i]);
         }
     };
 
@@ -1121,12 +1119,12 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                 if constexpr (i == 0) bnext = *reinterpret_cast<const f16x8 *>(Bn);
             }
 
-            constexpr int q = pw_dq_at(k, PRE, 8 * NJ);
+            constexpr int q = pw_dq_at(k, PRE, 4 * NJ);
             if constexpr (q >= 0) {
-                // B(t+2): job q / 8, word (q / 4) % 2, byte q % 4
-                constexpr int jb = q / 8, w = (q / 4) % 2, b = q % 4;
-                const uint32_t word = w ? rb.v[jb].y : rb.v[jb].x;
-                if constexpr (w == 0 && b == 0) {
+                // B(t+2): job q / 4, byte pair q % 4 of its word
+                constexpr int jb = q / 4, b = q % 4;
+                const uint32_t word = rb.v[jb];
+                if constexpr (b == 0) {
                     const f16 sc = __builtin_bit_cast(f16, (uint16_t)rb.s[jb]);
                     s2 = f16x2{sc, sc};
                     sf = (float)sc;
@@ -1142,8 +1140,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                     out[b] = dq_byte(word, s2, b);
                 }
                 if constexpr (b == 3)
-                    *reinterpret_cast<u32x4 *>(Bw + (bwo ^ (w << 3)) + jb * (PW_NT / 2) * PW_BK) =
-                        u32x4{out[0], out[1], out[2], out[3]};
+                    *reinterpret_cast<u32x4 *>(Bw + awo + jb * (PW_NT / 4) * PW_BK) = u32x4{out[0], out[1], out[2], out[3]};
             }
             if constexpr (k == 1 || k == 3) {
                 // A(t+1) to LDS
@@ -1157,15 +1154,14 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                                                         rx, xoff(c), min(t + 2, nk - 1) * (PW_BK * 2), 0));
             }
             // B(t+3) loads of job c, in the slot after job c's last byte pair
-            // (a full step before job 0's first use, most of one for job 1)
-            constexpr int bl = (k == pw_dq_slot(8 * 0 + 7, PRE, 8 * NJ) + 1)              ? 0
-                               : (NJ > 1 && k == pw_dq_slot(8 * 1 + 7, PRE, 8 * NJ) + 1) ? 1
+            constexpr int bl = (k == pw_dq_slot(4 * 0 + 3, PRE, 4 * NJ) + 1)              ? 0
+                               : (NJ > 1 && k == pw_dq_slot(4 * 1 + 3, PRE, 4 * NJ) + 1) ? 1
+                               : (NJ > 2 && k == pw_dq_slot(4 * 2 + 3, PRE, 4 * NJ) + 1) ? 2
                                                                                           : -1;
             if constexpr (bl >= 0) {
                 const int u = min(t + 3, nk - 1);
                 const uint32_t n = qrow_of(bl);
-                rb.v[bl] = __builtin_bit_cast(
-                    uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2), 0));
+                rb.v[bl] = __builtin_amdgcn_raw_buffer_load_b32(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2), 0);
                 rb.s[bl] = __builtin_amdgcn_raw_buffer_load_b16(rs, n * (uint32_t)(a.ngroups * 2), ((uint32_t)u >> gshift) * 2, 0);
             }
             if constexpr (FOLD && k == 9) {
@@ -1183,7 +1179,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
             if constexpr (FOLD && k == 25) load_e((t + 2) >> 1, re);  // the next step's entries
             __builtin_amdgcn_sched_barrier(0);
         }, std::make_integer_sequence<int, 4 * NRT>{});
-        static_assert(pw_dq_slot(8 * NJ - 1, PRE, 8 * NJ) + 1 < PRE && PRE > 25, "every slice of the step needs a slot");
+        static_assert(pw_dq_slot(4 * NJ - 1, PRE, 4 * NJ) + 1 < PRE && PRE > 25, "every slice of the step needs a slot");
         b3 = b3_1;
     }
 
