@@ -1109,11 +1109,13 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                 if (rare) fold_rare(u1, h1, Bf);
                 __syncthreads();
             }
+            // (weights as the first operand: a lane's four results are four
+            // adjacent output rows of one token, stored as one 8-byte word)
             if constexpr (XB)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
-                                                                    __builtin_bit_cast(bf16x8, bcur), acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bcur),
+                                                                    __builtin_bit_cast(bf16x8, af[i]), acc[i][j], 0, 0, 0);
             else
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bcur, acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur, af[i], acc[i][j], 0, 0, 0);
             if constexpr (k >= PRE) {
                 af[i] = *reinterpret_cast<const f16x8 *>(An + 16 * i * PW_BK);
                 if constexpr (i == 0) bnext = *reinterpret_cast<const f16x8 *>(Bn);
@@ -1183,21 +1185,31 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         b3 = b3_1;
     }
 
-    // epilogue: lane holds D[token 16 i + 4 (lane / 16) + r][row 16 j + lane % 16]
+    // epilogue: lane holds D[row 16 j + 4 (lane / 16) + r][token 16 i + lane % 16],
+    // four adjacent rows of one token: one 8-byte store where the rows are
+    // whole and aligned (N % 4 == 0), else 2-byte stores
+    const bool vec = (a.N & 3) == 0;
 #pragma unroll
-    for (int j = 0; j < NRT; j++) {
-        const int64_t n = n0 + (R / 2) * wn + 16 * j + (lane & 15);
+    for (int i = 0; i < 4; i++) {
+        const int64_t m = m0 + 64 * wm + 16 * i + (lane & 15);
+        if (m >= a.M) continue;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int j = 0; j < NRT; j++) {
+            const int64_t n = n0 + (R / 2) * wn + 16 * j + 4 * (lane >> 4);
+            uint16_t h[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int64_t m = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
-                if (m < a.M && n < a.N) {
-                    if constexpr (XB)
-                        reinterpret_cast<uint16_t *>(a.y)[m * a.N + n] = out_bf16(acc[i][j][r], a.bias, a.bias_dtype, n);
-                    else
-                        a.y[m * a.N + n] = out_f16(acc[i][j][r], a.bias, a.bias_dtype, n);
-                }
+                const int64_t nb = min(n + r, a.N - 1);  // (a bias read past the last row is not kept)
+                if constexpr (XB) h[r] = out_bf16(acc[i][j][r], a.bias, a.bias_dtype, nb);
+                else h[r] = __builtin_bit_cast(uint16_t, out_f16(acc[i][j][r], a.bias, a.bias_dtype, nb));
+            }
+            uint16_t *yp = reinterpret_cast<uint16_t *>(a.y) + m * a.N + n;
+            if (vec && n + 3 < a.N) {
+                *reinterpret_cast<uint2 *>(yp) = uint2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (n + r < a.N) yp[r] = h[r];
             }
         }
     }
