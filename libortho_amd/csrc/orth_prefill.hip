@@ -872,18 +872,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     const int nblk = (int)((a.N + kPlanBN - 1) / kPlanBN);
     const int b_lo = (int)(n0 / kPlanBN);
     const int nb = FOLD ? max(0, min(PW_MAX_BLOCKS, min(nblk, (int)((n0 + R - 1) / kPlanBN) + 1) - b_lo)) : 0;
-    bool canonical = true;
-    if (FOLD) {
-        const PlanHeader *h = a.plan;
-        const bool ok = h->magic == kPlanMagic && h->version == kPlanVersion && h->n == a.N &&
-                        h->k == a.K && h->nnz == a.nnz;
-        for (int i = tid; i < nb * (nk64 + 1); i += PW_NT) {
-            const int bb = i / (nk64 + 1), u = i - bb * (nk64 + 1);
-            offs[i] = ok ? min(max(a.offsets[(int64_t)(b_lo + bb) * (nk64 + 1) + u], 0), a.nnz) : 0;
-        }
-        canonical = !ok || (h->flags & kPlanNonCanonical) == 0;
-        __syncthreads();
-    }
+    bool canonical = true;  // (set with the offsets' staging, in the prologue)
 
     // buffer loads: a 32-bit lane offset that stays the same for the whole
     // K loop plus the step's offset in a scalar register (one VGPR per
@@ -1031,16 +1020,30 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     auto Ast = [&](int s) { return As0 + s * (PW_A_BYTES / 2); };
 
     // prologue: stage 0 folded, stage 1 dequantised; A(1), B(2) and the
-    // entries of stage 1's fold in flight
-    if (FOLD) load_e(0, re);
+    // entries of stage 1's fold in flight.  The first stages' loads are
+    // issued before the plan offsets are staged, so that their round trips
+    // overlap (one at the start of the kernel instead of three in a row).
+    PwB rb1;  // B(1)
     load_a(0, ra);
     load_b(0, rb);
+    load_b(min(1, nk - 1), rb1);
+    if (FOLD) {
+        const PlanHeader *h = a.plan;
+        const bool ok = h->magic == kPlanMagic && h->version == kPlanVersion && h->n == a.N &&
+                        h->k == a.K && h->nnz == a.nnz;
+        for (int i = tid; i < nb * (nk64 + 1); i += PW_NT) {
+            const int bb = i / (nk64 + 1), u = i - bb * (nk64 + 1);
+            offs[i] = ok ? min(max(a.offsets[(int64_t)(b_lo + bb) * (nk64 + 1) + u], 0), a.nnz) : 0;
+        }
+        canonical = !ok || (h->flags & kPlanNonCanonical) == 0;
+        __syncthreads();
+    }
+    if (FOLD) load_e(0, re);
     store_a(ra, Ast(0));
     load_a(min(1, nk - 1), ra);
     store_b(rb, Bst(0));
-    load_b(min(1, nk - 1), rb);
-    store_b(rb, Bst(1));
     load_b(min(2, nk - 1), rb);
+    store_b(rb1, Bst(1));
     __syncthreads();
     if (FOLD) {
         fold_common(0, re, Bst(0));
