@@ -798,12 +798,17 @@ __host__ __device__ constexpr int pw_trash_at(int nrt) {
 }
 __host__ __device__ constexpr int pw_lds_bytes(int nrt) { return pw_trash_at(nrt) + PW_NT * 2; }
 
-struct PwA { u32x4 v[2]; };                    // 256 tokens x 64 bytes: 2 x 16 B per thread
 struct PwB { uint32_t v[3]; uint32_t s[3]; };  // up to 3 chunks (a 4-byte word of nibbles each) + scale bits
 // a thread's plan entries of one 64-column step: the entry words and the
 // row offset of their block in the range (even; bit 0 of brow[0]: the block
 // holds more entries than its threads prefetch)
 struct PwE { uint32_t e[PW_E]; int brow[PW_E]; };
+
+// 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4
+// ... lds): lane i's land at lds + 16 i (lds the same in every lane)
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, void *lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
+}
 
 // f(integral_constant<int, k>) for k = 0 .. N-1, unrolled at compile time
 template <class F, int... Is>
@@ -848,12 +853,17 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // per-thread byte offsets (step 0) of the first chunk / job; the others
     // are formed at each load (registers are the limit here).  Rows past M
     // / N repeat the last row.
-    // activation chunk i of this thread: idx = tid + 512 i, row idx / 4,
-    // chunk idx % 4 (4 lanes read a row's 64 contiguous bytes)
-    const uint32_t xrow = (uint32_t)(m0 + (tid >> 2));
-    const uint32_t xcol = (uint32_t)((tid & 3) * 16);
-    auto xoff = [&](int i) -> uint32_t {
-        return min(xrow + (uint32_t)(i * (PW_NT / 4)), (uint32_t)(a.M - 1)) * (uint32_t)(a.K * 2) + xcol;  // (+128 rows)
+    // activations: loaded straight into LDS (buffer_load_dwordx4 ... lds:
+    // lane i of a wave's load lands at its base + 16 i).  Load c of wave w
+    // fills rows 16 (2 w + c) .. + 15 (8 lines of the swizzled stage, 1 KB):
+    // lane i takes line i / 8, slot i % 8, i.e. row 2 (i / 8) + (s >> 2),
+    // chunk s & 3 with s = (i % 8) ^ (i / 8), so the two rows of a line are
+    // read as two 64-byte runs (4 lanes each)
+    const int xs = (lane & 7) ^ (lane >> 3);
+    const uint32_t xrow = (uint32_t)(m0 + 32 * wave + 2 * (lane >> 3) + (xs >> 2));
+    const uint32_t xcol = (uint32_t)((xs & 3) * 16);
+    auto xoff = [&](int c) -> uint32_t {
+        return min(xrow + (uint32_t)(16 * c), (uint32_t)(a.M - 1)) * (uint32_t)(a.K * 2) + xcol;
     };
     // weight job i of this thread: j = tid + 512 i, row j / 4, chunk j % 4
     // (the same mapping as the activations: 4 lanes read a row's 16
@@ -884,17 +894,11 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.q), (short)0, (int)(uint32_t)(a.N * (a.K / 2)), 0x00020000);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<f16 *>(a.scales), (short)0, (int)(uint32_t)(a.N * a.ngroups * 2), 0x00020000);
-    auto load_a = [&](int u, PwA &r) {
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            r.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff(i), u * (PW_BK * 2), 0));
-    };
-    auto store_a = [&](const PwA &r, f16 *As) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int idx = tid + PW_NT * i;
-            *reinterpret_cast<u32x4 *>(As + pw_swz(idx >> 2, idx & 3)) = r.v[i];
-        }
+    // load c (0, 1) of A(u) into stage As; no register holds the data, so
+    // the compiler inserts no wait for it: whoever reads the stage waits
+    // for the loads (vmcnt) before the barrier that publishes it
+    auto dma_a = [&](int u, int c, f16 *As) {
+        buffer_load_lds16(rx, As + (PW_A_BYTES / 16) * wave + (PW_A_BYTES / 32) * c, xoff(c), u * (PW_BK * 2));
     };
     auto load_b = [&](int u, PwB &r) {
 #pragma unroll
@@ -1011,10 +1015,9 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         for (int j = 0; j < NRT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 
-    // one register set each for the activations, the raw weights and the
-    // plan entries: a step writes the set it holds to LDS (or folds it), then
-    // loads the next step's into it (a load still has a full step to land)
-    PwA ra;
+    // one register set each for the raw weights and the plan entries: a
+    // step writes the set it holds to LDS (or folds it), then loads the next
+    // step's into it (a load still has a full step to land)
     PwB rb;
     PwE re;
     auto Bst = [&](int s) { return Bs0 + s * (pw_b_bytes(NRT) / 2); };
@@ -1025,7 +1028,12 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // issued before the plan offsets are staged, so that their round trips
     // overlap (one at the start of the kernel instead of three in a row).
     PwB rb1;  // B(1)
-    load_a(0, ra);
+#pragma unroll
+    for (int c = 0; c < 2; c++) dma_a(0, c, Ast(0));
+#pragma unroll
+    for (int c = 0; c < 2; c++) dma_a(min(1, nk - 1), c, Ast(1));
+    // (A(0) and A(1) have landed once B(0)'s loads, issued after them, have:
+    // the memory counter retires in order)
     load_b(0, rb);
     load_b(min(1, nk - 1), rb1);
     if (FOLD) {
@@ -1040,8 +1048,6 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         __syncthreads();
     }
     if (FOLD) load_e(0, re);
-    store_a(ra, Ast(0));
-    load_a(min(1, nk - 1), ra);
     store_b(rb, Bst(0));
     load_b(min(2, nk - 1), rb);
     store_b(rb1, Bst(1));
@@ -1087,7 +1093,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         const int u3 = min(t + 3, nk - 1);                         // B loads of this step: step u3
         const bool sload = ((uint32_t)u3 & gmask) == 0u;           // (uniform) u3 starts a group
         const f16 *Bs = Bst(b3);
-        f16 *Bw = Bst(b3_2), *Bf = Bst(b3_1), *Aw = Ast((t + 1) & 1);
+        f16 *Bw = Bst(b3_2), *Bf = Bst(b3_1), *Aw2 = Ast(t & 1);
 
         const f16 *Br = Bs + aro + (R / 2) * wn * PW_BK;
         // the next step's operands (read after this step's barrier)
@@ -1111,8 +1117,15 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
             if constexpr (k == PRE) {
                 // every LDS write of the step is issued: the rest of an
                 // overflowing fold, then the barrier; the step's last four
-                // MFMAs then cover the next step's first operand reads
+                // MFMAs then cover the next step's first operand reads.
+                // A(t+1) (loaded into LDS in the step before) must have
+                // landed: younger than its loads are this step's weight word
+                // loads, (fold) its entry loads and, at a group's first
+                // step, its scale loads (more in a rare fold: a longer wait)
                 if (rare) fold_rare(u1, h1, Bf);
+                constexpr int younger = NJ + (FOLD ? PW_E : 0), ys = younger + NJ;
+                if (sload) __builtin_amdgcn_s_waitcnt((ys & 15) | (7 << 4) | (15 << 8) | ((ys >> 4) << 14));
+                else __builtin_amdgcn_s_waitcnt((younger & 15) | (7 << 4) | (15 << 8) | ((younger >> 4) << 14));
                 __syncthreads();
             }
             // (weights as the first operand: a lane's four results are four
@@ -1150,16 +1163,10 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                 if constexpr (b == 3)
                     *reinterpret_cast<u32x4 *>(Bw + awo + jb * (PW_NT / 4) * PW_BK) = u32x4{out[0], out[1], out[2], out[3]};
             }
-            if constexpr (k == 1 || k == 3) {
-                // A(t+1) to LDS
-                constexpr int c = (k - 1) / 2;
-                *reinterpret_cast<u32x4 *>(Aw + awo + c * (PW_NT / 4) * PW_BK) = ra.v[c];
-            }
-            if constexpr (k == 4 || k == 6) {
-                // A(t+2) loads (after the writes of the registers they reuse)
-                constexpr int c = (k - 4) / 2;
-                ra.v[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        rx, xoff(c), min(t + 2, nk - 1) * (PW_BK * 2), 0));
+            if constexpr (k == PRE + 1 || k == PRE + 3) {
+                // A(t+2) into the stage A(t) held (every wave read A(t)
+                // before this step's barrier)
+                dma_a(min(t + 2, nk - 1), (k - PRE - 1) / 2, Aw2);
             }
             // B(t+3) loads of job c, in the slot after job c's last byte pair
             constexpr int bl = (k == pw_dq_slot(4 * 0 + 3, PRE, 4 * NJ) + 1)              ? 0
@@ -1200,6 +1207,8 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         static_assert(pw_dq_slot(4 * NJ - 1, PRE, 4 * NJ) + 1 < PRE && PRE > 25, "every slice of the step needs a slot");
         b3 = b3_1;
     }
+
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // (the last activation loads into LDS land first)
 
     // epilogue: lane holds D[row 16 j + 4 (lane / 16) + r][token 16 i + lane % 16],
     // four adjacent rows of one token: one 8-byte store where the rows are
