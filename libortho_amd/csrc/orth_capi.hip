@@ -47,7 +47,7 @@ hipError_t plan_read_flags(const void *plan, hipStream_t stream, uint32_t *flags
 hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream);
 bool prefill_wide_supported(const ForwardArgs &a);
 bool prefill_wide_preferred(const ForwardArgs &a, int cus);
-hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream_t stream);
+hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream_t stream, int cus);
 hipError_t prefill_prepare_device();
 hipError_t plan_prepare_device();
 bool mid_supported(const ForwardArgs &a, const void *plan);
@@ -498,7 +498,7 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
                  : launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
     } else if (kernel == KERNEL_PREFILL || kernel == KERNEL_PREFILL_WIDE) {
         auto pf = [&](const void *p) {
-            return kernel == KERNEL_PREFILL_WIDE ? launch_prefill_wide(a, p, stream) : launch_prefill(a, p, stream);
+            return kernel == KERNEL_PREFILL_WIDE ? launch_prefill_wide(a, p, stream, g_dev[dev].cus) : launch_prefill(a, p, stream);
         };
         if (a.has_ortho && !plan && noalloc) {
             // the prefill part of a plan, built in the scratch array

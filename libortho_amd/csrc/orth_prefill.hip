@@ -787,16 +787,18 @@ __device__ __forceinline__ int pw_swz(int r, int c) {
     return line * 64 + (((((r & 1) << 2) | c) ^ (line & 7)) << 3);
 }
 
-// A weight stage holds the rows the chunk jobs reach (a thread's last job
-// lands in rows past R when there is none: never read; no branch).
-__host__ __device__ constexpr int pw_njobs(int nrt) { return (4 * 32 * nrt + PW_NT - 1) / PW_NT; }
-__host__ __device__ constexpr int pw_b_rows(int nrt) { return pw_njobs(nrt) * PW_NT / 4; }
-__host__ __device__ constexpr int pw_b_bytes(int nrt) { return pw_b_rows(nrt) * PW_BK * 2; }
-__host__ __device__ constexpr int pw_off_at(int nrt) { return 2 * PW_A_BYTES + 3 * pw_b_bytes(nrt); }
-__host__ __device__ constexpr int pw_trash_at(int nrt) {
-    return pw_off_at(nrt) + PW_MAX_BLOCKS * (int)(kPlanMaxK / kPlanBK + 1) * 4;
+// A step is ks sub-steps of 32 columns (ks = 1 or 2); a stage holds ks
+// sub-stages of the layout above.  A weight stage holds the rows the chunk
+// jobs reach (a thread's last job lands in rows past R when there is none:
+// never read; no branch).
+__host__ __device__ constexpr int pw_njobs(int nrt, int ks) { return (4 * ks * 32 * nrt + PW_NT - 1) / PW_NT; }
+__host__ __device__ constexpr int pw_b_rows(int nrt, int ks) { return pw_njobs(nrt, ks) * PW_NT / (4 * ks); }
+__host__ __device__ constexpr int pw_b_bytes(int nrt, int ks) { return pw_b_rows(nrt, ks) * PW_BK * 2 * ks; }
+__host__ __device__ constexpr int pw_off_at(int nrt, int ks) { return 2 * PW_A_BYTES * ks + 3 * pw_b_bytes(nrt, ks); }
+__host__ __device__ constexpr int pw_trash_at(int nrt, int ks) {
+    return pw_off_at(nrt, ks) + PW_MAX_BLOCKS * (int)(kPlanMaxK / kPlanBK + 1) * 4;
 }
-__host__ __device__ constexpr int pw_lds_bytes(int nrt) { return pw_trash_at(nrt) + PW_NT * 2; }
+__host__ __device__ constexpr int pw_lds_bytes(int nrt, int ks) { return pw_trash_at(nrt, ks) + PW_NT * 2; }
 
 struct PwB { uint32_t v[3]; uint32_t s[3]; };  // up to 3 chunks (a 4-byte word of nibbles each) + scale bits
 // a thread's plan entries of one 64-column step: the entry words and the
@@ -826,16 +828,20 @@ constexpr int pw_dq_at(int k, int nslots, int nbytes) {
     return -1;
 }
 
-template <int NRT, bool FOLD, bool XB>
+// KS: 32-column sub-steps per step (1, or 2 for a 128-row tile, whose
+// step would otherwise hold too few MFMAs for its barrier and loads)
+template <int NRT, int KS, bool FOLD, bool XB>
 __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     constexpr int R = 32 * NRT;                 // rows of the workgroup tile
-    constexpr int NJ = pw_njobs(NRT);  // chunk jobs per thread (dequantisation: 8 weights each)
-    static_assert(NJ <= 3, "three chunk jobs per thread at most");
+    constexpr int NJ = pw_njobs(NRT, KS);  // chunk jobs per thread (dequantisation: 8 weights each)
+    constexpr int RS = pw_b_rows(NRT, KS);  // rows of a weight sub-stage
+    constexpr int JW = 4 * KS;              // 4-byte words of a row per step (= threads per row)
+    static_assert(NJ <= 3 && (KS == 1 || KS == 2), "three chunk jobs per thread at most");
     extern __shared__ __align__(16) unsigned char smem[];
     f16 *As0 = reinterpret_cast<f16 *>(smem);
-    f16 *Bs0 = reinterpret_cast<f16 *>(smem + 2 * PW_A_BYTES);
-    int32_t *offs = reinterpret_cast<int32_t *>(smem + pw_off_at(NRT));
-    f16 *trash = reinterpret_cast<f16 *>(smem + pw_trash_at(NRT));
+    f16 *Bs0 = reinterpret_cast<f16 *>(smem + 2 * PW_A_BYTES * KS);
+    int32_t *offs = reinterpret_cast<int32_t *>(smem + pw_off_at(NRT, KS));
+    f16 *trash = reinterpret_cast<f16 *>(smem + pw_trash_at(NRT, KS));
 
     const int tt = (int)(blockIdx.x % (unsigned)a.nbm), rr = (int)(blockIdx.x / (unsigned)a.nbm);
     const int64_t m0 = (int64_t)tt * PW_BM, n0 = (int64_t)rr * R;
@@ -847,8 +853,10 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         return wave * 64 + (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
     };
     const int wm = wave & 3, wn = wave >> 2;
-    const int nk = (int)(a.K / PW_BK);
+    const int nk = (int)(a.K / (PW_BK * KS));
     const int nk64 = (int)(a.K / kPlanBK);
+    // plan step and half (columns 32 h .. + 31 of it, KS == 1) of step v
+    auto pstep = [&](int v) -> int { return KS == 2 ? v : v >> 1; };
 
     // per-thread byte offsets (step 0) of the first chunk / job; the others
     // are formed at each load (registers are the limit here).  Rows past M
@@ -865,18 +873,18 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     auto xoff = [&](int c) -> uint32_t {
         return min(xrow + (uint32_t)(16 * c), (uint32_t)(a.M - 1)) * (uint32_t)(a.K * 2) + xcol;
     };
-    // weight job i of this thread: j = tid + 512 i, row j / 4, chunk j % 4
-    // (the same mapping as the activations: 4 lanes read a row's 16
-    // contiguous bytes of nibbles); past 4 R it writes the stage's spare rows
+    // weight job i of this thread: j = tid + 512 i, row j / JW, word j % JW:
+    // sub-stage word / 4, chunk word % 4 (the same mapping as the
+    // activations: JW lanes read a row's 16 KS contiguous bytes of nibbles);
+    // past R rows it writes the stage's spare rows
     auto job = [&](int i) -> int { return tid + PW_NT * i; };
-    static_assert(PW_NT * NJ / 4 <= pw_b_rows(NRT) && pw_b_rows(NRT) >= R, "chunk jobs stay inside the stage");
-    // LDS write offsets (halves) of job 0, chunk 2 (tid % 2), and of the
-    // thread's first activation chunk: the other writes are fixed offsets
-    // or one XOR from these (the swizzle leaves bits 4 and up of a row alone)
-    const int awo = pw_swz(tid >> 2, tid & 3);  // (also job 0's; job / chunk i: + 128 i rows)
-    const uint32_t qrow0 = (uint32_t)(n0 + (tid >> 2)), qh = (uint32_t)(tid & 3) * 4;
-    auto qrow_of = [&](int i) -> uint32_t { return min(qrow0 + (uint32_t)(i * (PW_NT / 4)), (uint32_t)(a.N - 1)); };
-    const int gshift = a.ngroups == 1 ? 31 : __builtin_ctzll(a.G / PW_BK);
+    static_assert(PW_NT * NJ / JW <= RS && RS >= R, "chunk jobs stay inside the stage");
+    // LDS write offset (halves) of job 0 (job i: + 512 / JW i rows; the
+    // swizzle leaves bits 4 and up of a row alone)
+    const int awo = ((tid % JW) >> 2) * (RS * PW_BK) + pw_swz(tid / JW, tid & 3);
+    const uint32_t qrow0 = (uint32_t)(n0 + tid / JW), qh = (uint32_t)(tid % JW) * 4;
+    auto qrow_of = [&](int i) -> uint32_t { return min(qrow0 + (uint32_t)(i * (PW_NT / JW)), (uint32_t)(a.N - 1)); };
+    const int gshift = a.ngroups == 1 ? 31 : __builtin_ctzll(a.G / (PW_BK * KS));
     const uint32_t gmask = (1u << gshift) - 1u;  // steps u with u & gmask == 0 start a group
 
     // plan blocks of the row range, their offsets staged in LDS
@@ -897,14 +905,16 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // load c (0, 1) of A(u) into stage As; no register holds the data, so
     // the compiler inserts no wait for it: whoever reads the stage waits
     // for the loads (vmcnt) before the barrier that publishes it
+    // (sub-stage c / 2 of the step, half c % 2 of the wave's rows)
     auto dma_a = [&](int u, int c, f16 *As) {
-        buffer_load_lds16(rx, As + (PW_A_BYTES / 16) * wave + (PW_A_BYTES / 32) * c, xoff(c), u * (PW_BK * 2));
+        buffer_load_lds16(rx, As + (c >> 1) * (PW_A_BYTES / 2) + (PW_A_BYTES / 16) * wave + (PW_A_BYTES / 32) * (c & 1),
+                          xoff(c & 1) + (uint32_t)(c >> 1) * (PW_BK * 2), u * (PW_BK * 2 * KS));
     };
     auto load_b = [&](int u, PwB &r) {
 #pragma unroll
         for (int i = 0; i < NJ; i++) {
             const uint32_t n = qrow_of(i);
-            r.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2), 0);
+            r.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2 * KS), 0);
             r.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, n * (uint32_t)(a.ngroups * 2), ((uint32_t)u >> gshift) * 2, 0);
         }
     };
@@ -928,8 +938,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     auto store_b = [&](const PwB &r, f16 *Bs) {
 #pragma unroll
         for (int i = 0; i < NJ; i++) {
-            const int j = job(i);
-            *reinterpret_cast<u32x4 *>(Bs + pw_swz(j >> 2, j & 3)) = dq_chunk(r.v[i], r.s[i]);
+            *reinterpret_cast<u32x4 *>(Bs + awo + i * (PW_NT / JW) * PW_BK) = dq_chunk(r.v[i], r.s[i]);
         }
     };
 
@@ -951,20 +960,24 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
         }
         r.brow[0] |= total > PW_E * EPB ? 1 : 0;
     };
-    // alpha * v of every entry of 64-column step u whose column falls in
-    // half `half` into the weight stage Bs (rows of the range only).  The
-    // cell of (local row, column c of the 64) gets alpha * v; a thread with
-    // nothing to add updates its own trash cell (no branch).
+    // alpha * v of every entry of 64-column plan step u whose column falls
+    // in half `half` (KS == 1; KS == 2: the whole plan step is the stage)
+    // into the weight stage Bs (rows of the range only).  The cell of (local
+    // row, column c of the 64) gets alpha * v; a thread with nothing to add
+    // updates its own trash cell (no branch).
+    auto cell_at = [&](f16 *Bs, int local, int c) -> f16 * {
+        return Bs + (KS == 2 ? (c >> 5) * (RS * PW_BK) : 0) + pw_swz(min(max(local, 0), R - 1), (c & 31) >> 3) + (c & 7);
+    };
+    auto in_half = [&](int c, int half) -> bool { return KS == 2 || (c >> 5) == half; };
     auto cell = [&](f16 *Bs, int local, int c, uint32_t w, bool ok) {
         const float v = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xffffu));
-        uint16_t *p = reinterpret_cast<uint16_t *>(
-            ok ? Bs + pw_swz(min(max(local, 0), R - 1), (c & 31) >> 3) + (c & 7) : trash + tid_now());
+        uint16_t *p = reinterpret_cast<uint16_t *>(ok ? cell_at(Bs, local, c) : trash + tid_now());
         *p = fold_add<XB>(*p, a.alpha * v);
     };
     auto one = [&](f16 *Bs, int half, uint32_t w, int brow) {
         const int local = (brow & ~1) + (int)(w >> 24);
         const int c = (int)((w >> 16) & (kPlanBK - 1));
-        cell(Bs, local, c, w, local >= 0 && local < R && (c >> 5) == half);
+        cell(Bs, local, c, w, local >= 0 && local < R && in_half(c, half));
     };
     // the prefetched entries (canonical plans), no branch
     auto fold_common = [&](int half, const PwE &r, f16 *Bs) {
@@ -1002,7 +1015,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                     const uint32_t w = a.entries[e];
                     if ((int)(w >> 24) != rib) break;
                     const int c = (int)((w >> 16) & (kPlanBK - 1));
-                    if ((c >> 5) == half) cell(Bs, lr, c, w, true);
+                    if (in_half(c, half)) cell(Bs, lr, c, w, true);
                 }
             }
         }
@@ -1020,8 +1033,8 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // step's into it (a load still has a full step to land)
     PwB rb;
     PwE re;
-    auto Bst = [&](int s) { return Bs0 + s * (pw_b_bytes(NRT) / 2); };
-    auto Ast = [&](int s) { return As0 + s * (PW_A_BYTES / 2); };
+    auto Bst = [&](int s) { return Bs0 + s * (pw_b_bytes(NRT, KS) / 2); };
+    auto Ast = [&](int s) { return As0 + s * (PW_A_BYTES / 2 * KS); };
 
     // prologue: stage 0 folded, stage 1 dequantised; A(1), B(2) and the
     // entries of stage 1's fold in flight.  The first stages' loads are
@@ -1029,9 +1042,9 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // overlap (one at the start of the kernel instead of three in a row).
     PwB rb1;  // B(1)
 #pragma unroll
-    for (int c = 0; c < 2; c++) dma_a(0, c, Ast(0));
+    for (int c = 0; c < 2 * KS; c++) dma_a(0, c, Ast(0));
 #pragma unroll
-    for (int c = 0; c < 2; c++) dma_a(min(1, nk - 1), c, Ast(1));
+    for (int c = 0; c < 2 * KS; c++) dma_a(min(1, nk - 1), c, Ast(1));
     // (A(0) and A(1) have landed once B(0)'s loads, issued after them, have:
     // the memory counter retires in order)
     load_b(0, rb);
@@ -1055,7 +1068,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     if (FOLD) {
         fold_common(0, re, Bst(0));
         if (!canonical || (re.brow[0] & 1)) fold_rare(0, 0, Bst(0));
-        load_e(0, re);
+        load_e(pstep(1), re);
     }
     __syncthreads();
 
@@ -1072,7 +1085,8 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // the two waves of a SIMD in the same phase: 3,600 cycles a step
     // against 1,408 of MFMAs.)
     int b3 = 0;  // t % 3
-    constexpr int PRE = 4 * NRT - 4;  // slots before the step's barrier
+    constexpr int NS = 4 * NRT * KS;  // slots of a step
+    constexpr int PRE = NS - 4;       // slots before the step's barrier
     const int aro = pw_swz(lane & 15, lane >> 4);
     // operand reads: row 16 m + lr, chunk lc sits at aro + 16 m rows (the
     // swizzle depends on the row's bits 1..3 only).  A step's A operands and
@@ -1080,7 +1094,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     // barrier), into the registers its last MFMAs free.
     f16x8 af[4], bcur, bnext;
     {
-        const f16 *Ar = Ast(0) + aro + 64 * wm * PW_BK, *Br = Bst(0) + aro + (R / 2) * wn * PW_BK;
+        const f16 *Ar = Ast(0) + aro + 64 * wm * PW_BK, *Br = Bst(0) + aro + (R / 2) * wn * PW_BK;  // (sub-stage 0)
 #pragma unroll
         for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const f16x8 *>(Ar + 16 * i * PW_BK);
         bnext = *reinterpret_cast<const f16x8 *>(Br);
@@ -1088,7 +1102,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     for (int t = 0; t < nk; t++) {
         __builtin_amdgcn_sched_barrier(0);
         const int b3_1 = b3 == 2 ? 0 : b3 + 1, b3_2 = b3 == 0 ? 2 : b3 - 1;
-        const int u1 = (t + 1) >> 1, h1 = (t + 1) & 1;
+        const int u1 = pstep(t + 1), h1 = (t + 1) & 1;
         const bool rare = FOLD && (!canonical || (re.brow[0] & 1));  // (per thread: its block overflows)
         const int u3 = min(t + 3, nk - 1);                         // B loads of this step: step u3
         const bool sload = ((uint32_t)u3 & gmask) == 0u;           // (uniform) u3 starts a group
@@ -1109,10 +1123,13 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
 
         pw_static_for([&](auto kc) {
             constexpr int k = decltype(kc)::value;
-            constexpr int j = k / 4, i = k % 4;
+            constexpr int sub = k / (4 * NRT), j = (k % (4 * NRT)) / 4, i = k % 4;
             if constexpr (i == 0) {
                 bcur = bnext;
-                if constexpr (j + 1 < NRT) bnext = *reinterpret_cast<const f16x8 *>(Br + 16 * (j + 1) * PW_BK);
+                if constexpr (j + 1 < NRT)
+                    bnext = *reinterpret_cast<const f16x8 *>(Br + sub * (RS * PW_BK) + 16 * (j + 1) * PW_BK);
+                else if constexpr (sub + 1 < KS)
+                    bnext = *reinterpret_cast<const f16x8 *>(Br + (sub + 1) * (RS * PW_BK));
             }
             if constexpr (k == PRE) {
                 // every LDS write of the step is issued: the rest of an
@@ -1138,6 +1155,11 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
             if constexpr (k >= PRE) {
                 af[i] = *reinterpret_cast<const f16x8 *>(An + 16 * i * PW_BK);
                 if constexpr (i == 0) bnext = *reinterpret_cast<const f16x8 *>(Bn);
+            } else if constexpr (sub + 1 < KS && j == NRT - 1) {
+                // the next sub-step's A operands, into the registers this
+                // sub-step's last MFMAs free
+                af[i] = *reinterpret_cast<const f16x8 *>(Ast(t & 1) + (sub + 1) * (PW_A_BYTES / 2) + aro + 64 * wm * PW_BK +
+                                                         16 * i * PW_BK);
             }
 
             constexpr int q = pw_dq_at(k, PRE, 4 * NJ);
@@ -1161,13 +1183,12 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                     out[b] = dq_byte(word, s2, b);
                 }
                 if constexpr (b == 3)
-                    *reinterpret_cast<u32x4 *>(Bw + awo + jb * (PW_NT / 4) * PW_BK) = u32x4{out[0], out[1], out[2], out[3]};
+                    *reinterpret_cast<u32x4 *>(Bw + awo + jb * (PW_NT / JW) * PW_BK) = u32x4{out[0], out[1], out[2], out[3]};
             }
-            if constexpr (k == PRE + 1 || k == PRE + 3) {
-                // A(t+2) into the stage A(t) held (every wave read A(t)
-                // before this step's barrier)
-                dma_a(min(t + 2, nk - 1), (k - PRE - 1) / 2, Aw2);
-            }
+            // A(t+2) into the stage A(t) held (every wave read A(t) before
+            // this step's barrier): 2 KS loads in the slots after it
+            constexpr int dd = KS == 1 ? ((k == PRE + 1) ? 0 : (k == PRE + 3) ? 1 : -1) : (k >= PRE ? k - PRE : -1);
+            if constexpr (dd >= 0) dma_a(min(t + 2, nk - 1), dd, Aw2);
             // B(t+3) loads of job c, in the slot after job c's last byte pair
             constexpr int bl = (k == pw_dq_slot(4 * 0 + 3, PRE, 4 * NJ) + 1)              ? 0
                                : (NJ > 1 && k == pw_dq_slot(4 * 1 + 3, PRE, 4 * NJ) + 1) ? 1
@@ -1176,7 +1197,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
             if constexpr (bl >= 0) {
                 const int u = u3;
                 const uint32_t n = qrow_of(bl);
-                rb.v[bl] = __builtin_amdgcn_raw_buffer_load_b32(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2), 0);
+                rb.v[bl] = __builtin_amdgcn_raw_buffer_load_b32(rq, n * (uint32_t)(a.K >> 1) + qh, u * (PW_BK / 2 * KS), 0);
                 if (bl == NJ - 1 && sload) {
                     // the jobs' scales only where step u starts a group (one
                     // uniform branch, after every job of the step has read its
@@ -1189,22 +1210,25 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                                                                        ((uint32_t)u >> gshift) * 2, 0);
                 }
             }
-            if constexpr (FOLD && k == 9) {
+            // the fold late in the step (read, write, then the next step's
+            // entries loaded right after): an entry load has nearly a step
+            // to land, and it comes from the Infinity Cache or HBM
+            constexpr int FR = PRE - 8, FW = PRE - 3, FE = PRE - 2;
+            if constexpr (FOLD && k == FR) {
                 // fold of B(t+1), prefetched entry: the cell (or the trash cell)
                 const uint32_t w = re.e[0];
                 const int local = (canonical ? (re.brow[0] & ~1) : -(1 << 20)) + (int)(w >> 24);
                 const int c = (int)((w >> 16) & (kPlanBK - 1));
-                const bool ok = local >= 0 && local < R && (c >> 5) == h1;
-                fp = reinterpret_cast<uint16_t *>(ok ? Bf + pw_swz(min(max(local, 0), R - 1), (c & 31) >> 3) + (c & 7)
-                                                     : trash + tid_now());
+                const bool ok = local >= 0 && local < R && in_half(c, h1);
+                fp = reinterpret_cast<uint16_t *>(ok ? cell_at(Bf, local, c) : trash + tid_now());
                 fold_old = *fp;
             }
-            if constexpr (FOLD && k == 14)  // (the value recomputed here: one register less across the slots)
+            if constexpr (FOLD && k == FW)  // (the value recomputed here: one register less across the slots)
                 *fp = fold_add<XB>(fold_old, a.alpha * (float)__builtin_bit_cast(f16, (uint16_t)(re.e[0] & 0xffffu)));
-            if constexpr (FOLD && k == 25) load_e((t + 2) >> 1, re);  // the next step's entries
+            if constexpr (FOLD && k == FE) load_e(pstep(t + 2), re);  // the next step's entries
             __builtin_amdgcn_sched_barrier(0);
-        }, std::make_integer_sequence<int, 4 * NRT>{});
-        static_assert(pw_dq_slot(4 * NJ - 1, PRE, 4 * NJ) + 1 < PRE && PRE > 25, "every slice of the step needs a slot");
+        }, std::make_integer_sequence<int, NS>{});
+        static_assert(pw_dq_slot(4 * NJ - 1, PRE, 4 * NJ) + 1 < PRE && PRE > 10, "every slice of the step needs a slot");
         b3 = b3_1;
     }
 
@@ -1289,9 +1313,10 @@ hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t st
 }
 
 // The wide-row tile: rows per workgroup 32 * kPwNrt.  Taken when the layer
-// has at least 16 row ranges (every workgroup a full MFMA load of rows).
-constexpr int kPwNrt = 11;
-static_assert(pw_lds_bytes(kPwNrt) <= 160 * 1024, "wide prefill LDS budget");
+// has at least 16 row ranges (every workgroup a full MFMA load of rows);
+// layers with fewer rows take 128-row tiles (kPwNrtS) in 64-column steps.
+constexpr int kPwNrt = 11, kPwNrtS = 4;
+static_assert(pw_lds_bytes(kPwNrt, 1) <= 160 * 1024 && pw_lds_bytes(kPwNrtS, 2) <= 160 * 1024, "wide prefill LDS budget");
 
 bool prefill_wide_supported(const ForwardArgs &a) {
     if (!prefill_supported(a)) return false;
@@ -1301,7 +1326,7 @@ bool prefill_wide_supported(const ForwardArgs &a) {
 // Wide rows pay where the 256 x 128 tile needs more rounds of the grid than
 // the wide tile: 4096 -> 11008 at 2048 tokens, 688 tiles (2.69 rounds)
 // against 256 (one).
-bool prefill_wide_preferred(const ForwardArgs &a, int cus) {
+static bool wide_rows_pay(const ForwardArgs &a, int cus) {
     if (!prefill_wide_supported(a) || a.M < 512 || a.N < 16 * 32 * kPwNrt) return false;
     const int64_t tt = (a.M + PW_BM - 1) / PW_BM;
     const int64_t wide = tt * ((a.N + 32 * kPwNrt - 1) / (32 * kPwNrt));
@@ -1311,7 +1336,15 @@ bool prefill_wide_preferred(const ForwardArgs &a, int cus) {
     return t_wide <= t_tile;
 }
 
-hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream_t stream) {
+// The wide kernel's 128-row tile has the 256 x 128 kernel's grid and runs
+// faster (c3 at 2048 tokens: 80 against 86 us at alpha = 1, 75 against 77
+// at alpha = 0): it takes the prefill calls of 512 tokens and more.
+bool prefill_wide_preferred(const ForwardArgs &a, int cus) {
+    (void)cus;
+    return prefill_wide_supported(a) && a.M >= 512;
+}
+
+hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream_t stream, int cus) {
     PrefillArgs p;
     p.q = a.q;
     p.scales = static_cast<const f16 *>(a.scales);
@@ -1333,16 +1366,21 @@ hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream
     p.entries = plan ? reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(p.offsets) +
                                                           plan_offsets_bytes(a.N, a.K))
                      : nullptr;
-    p.nbm = (int)((a.M + PW_BM - 1) / PW_BM);
-    p.nbn = (int)((a.N + 32 * kPwNrt - 1) / (32 * kPwNrt));
-    const unsigned blocks = (unsigned)(p.nbm * p.nbn);
     if (p.fold && p.nnz <= 0) return hipErrorInvalidValue;
     const bool xb = a.io_dtype == ORTH_DT_BF16;
-    const int lds = pw_lds_bytes(kPwNrt);
-    if (p.fold && xb) hipLaunchKernelGGL((prefill_wide_kernel<kPwNrt, true, true>), dim3(blocks), dim3(PW_NT), lds, stream, p);
-    else if (p.fold) hipLaunchKernelGGL((prefill_wide_kernel<kPwNrt, true, false>), dim3(blocks), dim3(PW_NT), lds, stream, p);
-    else if (xb) hipLaunchKernelGGL((prefill_wide_kernel<kPwNrt, false, true>), dim3(blocks), dim3(PW_NT), lds, stream, p);
-    else hipLaunchKernelGGL((prefill_wide_kernel<kPwNrt, false, false>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+    p.nbm = (int)((a.M + PW_BM - 1) / PW_BM);
+    auto go = [&](auto nrt, auto ks) {
+        constexpr int NRT = decltype(nrt)::value, KS = decltype(ks)::value;
+        p.nbn = (int)((a.N + 32 * NRT - 1) / (32 * NRT));
+        const unsigned blocks = (unsigned)(p.nbm * p.nbn);
+        const int lds = pw_lds_bytes(NRT, KS);
+        if (p.fold && xb) hipLaunchKernelGGL((prefill_wide_kernel<NRT, KS, true, true>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+        else if (p.fold) hipLaunchKernelGGL((prefill_wide_kernel<NRT, KS, true, false>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+        else if (xb) hipLaunchKernelGGL((prefill_wide_kernel<NRT, KS, false, true>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+        else hipLaunchKernelGGL((prefill_wide_kernel<NRT, KS, false, false>), dim3(blocks), dim3(PW_NT), lds, stream, p);
+    };
+    if (wide_rows_pay(a, cus)) go(std::integral_constant<int, kPwNrt>{}, std::integral_constant<int, 1>{});
+    else go(std::integral_constant<int, kPwNrtS>{}, std::integral_constant<int, 2>{});
     return hipGetLastError();
 }
 
@@ -1360,12 +1398,20 @@ hipError_t prefill_prepare_device() {
         hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS_BYTES);
         if (e != hipSuccess) return e;
     }
-    const void *kw[4] = {reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, true, false>),
-                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, false, false>),
-                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, true, true>),
-                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, false, true>)};
+    const void *kw[4] = {reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, 1, true, false>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, 1, false, false>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, 1, true, true>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrt, 1, false, true>)};
     for (const void *k : kw) {
-        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, pw_lds_bytes(kPwNrt));
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, pw_lds_bytes(kPwNrt, 1));
+        if (e != hipSuccess) return e;
+    }
+    const void *kn[4] = {reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrtS, 2, true, false>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrtS, 2, false, false>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrtS, 2, true, true>),
+                         reinterpret_cast<const void *>(prefill_wide_kernel<kPwNrtS, 2, false, true>)};
+    for (const void *k : kn) {
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, pw_lds_bytes(kPwNrtS, 2));
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -29,7 +29,7 @@ hipError_t launch_quarter(const ForwardArgs &, const void *, float *, hipStream_
 bool split_supported(const ForwardArgs &, const void *) { return false; }
 bool prefill_wide_supported(const ForwardArgs &) { return false; }
 bool prefill_wide_preferred(const ForwardArgs &, int) { return false; }
-hipError_t launch_prefill_wide(const ForwardArgs &, const void *, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t launch_prefill_wide(const ForwardArgs &, const void *, hipStream_t, int) { return hipErrorInvalidValue; }
 int64_t split_workspace_bytes(const ForwardArgs &) { return 0; }
 hipError_t launch_split(const ForwardArgs &, const void *, float *, hipStream_t) { return hipErrorInvalidValue; }
 bool split_group_ok(const ForwardArgs *, const void *const *, int) { return false; }

@@ -103,7 +103,9 @@ def auto_kernel(M, planned=False, K=4096):
         return "quarter"
     if planned and 17 <= M <= 32 and K % 128 == 0:
         return "split"
-    return "skinny" if M <= 64 else "prefill"
+    if M <= 64:
+        return "skinny"
+    return "prefill_wide" if M >= 512 else "prefill"
 
 
 # ---------------------------------------------------------- decode (M <= 16)
@@ -249,9 +251,11 @@ def test_decode_foreign_plan_falls_back_to_the_csr(oracle_mod):
 @pytest.mark.parametrize("alpha", [0.0, 0.5, 1.0])
 @pytest.mark.parametrize("plan", [True, "auto"])
 def test_prefill_c3(oracle_mod, alpha, plan):
+    """The 256 x 128 prefill kernel at c3 (forced: 2048 tokens take the wide
+    kernel's 128-row tile)."""
     L = W.config_layer("c3")
     x = W.make_x(2048, L.K, 3000)
-    y, k = run(L, x, alpha, plan=plan)
+    y, k = run(L, x, alpha, policy="prefill", plan=plan)
     assert k == "prefill"
     rows = np.array([0, 1, 255, 256, 511, 1000, 1023, 1024, 1500, 2046, 2047])
     ref = oracle_y(oracle_mod, L, x[rows], alpha)
@@ -286,8 +290,9 @@ def test_prefill_every_tile(oracle_mod, shape, alpha, plan):
     L = W.config_layer(shape)
     x = W.make_x(2048, L.K, 3100 + L.N)
     y, k = run(L, x, alpha, plan=plan)
-    # (the wide-row kernel takes the metric's shape: one 256 x 352 tile per CU)
-    assert k == ("prefill_wide" if shape == "c2" else "prefill")
+    # (the wide kernel takes both: one 256 x 352 tile per CU at the metric's
+    # shape, 256 x 128 tiles in 64-column steps at c3)
+    assert k == "prefill_wide"
     rows = prefill_rows(2048)
     ref = oracle_y(oracle_mod, L, x[rows], alpha)
     rel = assert_close(y[rows], ref, tol=PREFILL_TOL, what=f"prefill {shape} alpha={alpha} plan={plan}")
@@ -618,10 +623,11 @@ def test_prefill_fold_is_deterministic_with_duplicate_columns():
     vals = rng.normal(0, 0.05, rp[-1]).astype(np.float16)
     lay = W.Layer(K, N, L.q, L.scales, rp, col, vals)
     x = W.make_x(512, K, 3300)
-    ys = [run(lay, x, 1.0, plan=True) for _ in range(4)]
-    assert all(k == "prefill" for _, k in ys)
-    for y, _ in ys[1:]:
-        assert np.array_equal(y.view(np.uint32), ys[0][0].view(np.uint32))
+    for policy, kernel in (("prefill", "prefill"), ("auto", "prefill_wide")):
+        ys = [run(lay, x, 1.0, policy=policy, plan=True) for _ in range(4)]
+        assert all(k == kernel for _, k in ys)
+        for y, _ in ys[1:]:
+            assert np.array_equal(y.view(np.uint32), ys[0][0].view(np.uint32))
 
 
 def test_empty_batch_is_a_no_op():

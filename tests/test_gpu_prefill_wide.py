@@ -1,5 +1,6 @@
 """The wide-row prefill kernel (orth_prefill.hip, prefill_wide_kernel: one
-256-token x 352-row tile per workgroup) against the FP64 oracle and against
+256-token x 352-row tile per workgroup, or 128 rows in 64-column steps for
+layers with too few rows) against the FP64 oracle and against
 the 256 x 128 prefill kernel on the same inputs: the metric's 4096->11008
 shape at 2048 tokens (every token tile, alpha in {0, 0.5, 1}, planned and
 unplanned), ragged token and row counts, a row range that ends inside a
@@ -88,6 +89,24 @@ def test_wide_metric_shape(oracle_mod, alpha, plan):
     y2, k2 = run(lay, x, alpha, policy="prefill", plan=plan)
     assert k2 == "prefill"
     agree(y, y2, f"alpha={alpha} against the 256 x 128 prefill kernel")
+
+
+@pytest.mark.parametrize("alpha", [0.0, 0.5, 1.0])
+@pytest.mark.parametrize("plan", [True, False])
+def test_wide_c3_128_row_tile(oracle_mod, alpha, plan):
+    """c3 (4096 -> 4096 at 2048 tokens): too few rows for 352-row tiles, so
+    the wide kernel takes 128-row tiles in 64-column steps (256 workgroups);
+    every token tile and output column, against the oracle and the 256 x
+    128 kernel."""
+    lay = W.config_layer("c3")
+    x = x_of(2048, lay.K, 9050)
+    y, k = run(lay, x, alpha, plan=plan)
+    assert k == "prefill_wide"
+    rel = check(oracle_mod, lay, x, alpha, y, rows_of(2048), f"c3 alpha={alpha} plan={plan}")
+    print(f"wide 128-row c3 alpha={alpha} plan={plan}: max|err|/||y||_inf = {rel:.3e}")
+    y2, k2 = run(lay, x, alpha, policy="prefill", plan=plan)
+    assert k2 == "prefill"
+    agree(y, y2, f"c3 alpha={alpha} against the 256 x 128 prefill kernel")
 
 
 @pytest.mark.parametrize("K,N,group,M,alpha,density", [
