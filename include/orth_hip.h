@@ -106,9 +106,10 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  * term), the quarter-split kernel (17..32, K = 4096, a plan or no ortho
  * term), the slice-split kernel (17..32 at the other K % 128 == 0, a plan
  * or no ortho term), the split-K mid-batch kernel (other batches up to 64),
- * the MFMA prefill kernels above (one 256 x 352 tile per workgroup where
- * that needs fewer rounds of the grid than 256 x 128 tiles, as at
- * 4096 -> 11008 with 2048 tokens), and a general kernel for shapes and
+ * the MFMA prefill kernels above (from 512 tokens the wide kernel: one
+ * 256 x 352 tile per workgroup where that needs fewer rounds of the grid
+ * than 256 x 128 tiles, as at 4096 -> 11008 with 2048 tokens, else 256 x
+ * 128 tiles in 64-column steps), and a general kernel for shapes and
  * dtypes the fast kernels do not take (orth_hip_last_kernel() names the
  * choice).  BF16 I/O
  * takes the decode kernel for 1..4 tokens and the one-launch mid-batch
@@ -314,8 +315,10 @@ int orth_hip_device_info(int device, orth_hip_device_info_t *info);
  * default), 1 = decode, 2 = prefill, 3 = general, 4 = split-K mid-batch
  * (5..64 tokens), 5 = one-launch mid-batch (5..16 tokens), 6 = K quarters
  * over the grid (17..32 tokens, K = 4096), 7 = 1024-column slices over the
- * grid (1..32 tokens), 8 = the prefill kernel with one 256 x 352 tile per
- * workgroup (any batch).  A forced kernel that cannot take a call returns
+ * grid (1..32 tokens), 8 = the wide prefill kernel (any batch; its 256 x
+ * 352 tile where that needs fewer rounds of the grid than 256 x 128 tiles
+ * at 512 tokens or more, else 256 x 128 tiles in 64-column steps).  A
+ * forced kernel that cannot take a call returns
  * ORTH_ERR_UNSUPPORTED.  Process-wide. */
 int orth_hip_set_kernel_policy(int policy);
 int orth_hip_get_kernel_policy(void);
@@ -324,8 +327,8 @@ int orth_hip_get_kernel_policy(void);
  * 1 decode, 2 prefill, 3 general, 4 split-K mid-batch, 5 decode for a
  * group of layers in one launch (orth_layers_forward_hip), 6 one-launch
  * mid-batch, 7 K quarters over the grid, 8 1024-column slices over the
- * grid, 9 the same for a group of layers in one launch, 10 prefill with
- * one 256 x 352 tile per workgroup, 0 none. */
+ * grid, 9 the same for a group of layers in one launch, 10 the wide
+ * prefill kernel (256 x 352 or 256 x 128 tiles), 0 none. */
 int orth_hip_last_kernel(void);
 
 /* Device clock stamp for timing stream-ordered work (benchmarks; no

@@ -34,7 +34,7 @@ enum KernelId {
     KERNEL_QUARTER = 7,       // K quarters over the grid (17..32 tokens)
     KERNEL_SPLIT = 8,         // 1024-column slices over the grid (17..32 tokens)
     KERNEL_SPLIT_GROUP = 9,   // the same for a group of layers in one launch
-    KERNEL_PREFILL_WIDE = 10  // prefill with one 256 x 352 tile per CU
+    KERNEL_PREFILL_WIDE = 10  // the wide prefill kernel (256 x 352 or 256 x 128 tiles)
 };
 
 // Everything a forward launch needs, resolved on the host.
