@@ -798,7 +798,9 @@ __host__ __device__ constexpr int pw_off_at(int nrt, int ks) { return 2 * PW_A_B
 __host__ __device__ constexpr int pw_trash_at(int nrt, int ks) {
     return pw_off_at(nrt, ks) + PW_MAX_BLOCKS * (int)(kPlanMaxK / kPlanBK + 1) * 4;
 }
-__host__ __device__ constexpr int pw_lds_bytes(int nrt, int ks) { return pw_trash_at(nrt, ks) + PW_NT * 2; }
+// (a thread's trash cell: the low half of its own 4-byte word, so that a
+// wave's trash writes fall in distinct banks)
+__host__ __device__ constexpr int pw_lds_bytes(int nrt, int ks) { return pw_trash_at(nrt, ks) + PW_NT * 4; }
 
 struct PwB { uint32_t v[3]; uint32_t s[3]; };  // up to 3 chunks (a 4-byte word of nibbles each) + scale bits
 // a thread's plan entries of one 64-column step: the entry words and the
@@ -971,7 +973,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
     auto in_half = [&](int c, int half) -> bool { return KS == 2 || (c >> 5) == half; };
     auto cell = [&](f16 *Bs, int local, int c, uint32_t w, bool ok) {
         const float v = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xffffu));
-        uint16_t *p = reinterpret_cast<uint16_t *>(ok ? cell_at(Bs, local, c) : trash + tid_now());
+        uint16_t *p = reinterpret_cast<uint16_t *>(ok ? cell_at(Bs, local, c) : trash + 2 * tid_now());
         *p = fold_add<XB>(*p, a.alpha * v);
     };
     auto one = [&](f16 *Bs, int half, uint32_t w, int brow) {
@@ -1220,7 +1222,7 @@ __global__ void __launch_bounds__(PW_NT, 1) prefill_wide_kernel(PrefillArgs a) {
                 const int local = (canonical ? (re.brow[0] & ~1) : -(1 << 20)) + (int)(w >> 24);
                 const int c = (int)((w >> 16) & (kPlanBK - 1));
                 const bool ok = local >= 0 && local < R && in_half(c, h1);
-                fp = reinterpret_cast<uint16_t *>(ok ? cell_at(Bf, local, c) : trash + tid_now());
+                fp = reinterpret_cast<uint16_t *>(ok ? cell_at(Bf, local, c) : trash + 2 * tid_now());
                 fold_old = *fp;
             }
             if constexpr (FOLD && k == FW)  // (the value recomputed here: one register less across the slots)
