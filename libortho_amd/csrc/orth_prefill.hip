@@ -409,8 +409,8 @@ constexpr int PF_OFF_INTS = (int)(kPlanMaxK / kPlanBK + 1);
 constexpr int PF_A_STAGES = 2, PF_B_STAGES = 3;
 constexpr int PF_B_AT = PF_A_STAGES * PF_A_BYTES;              // LDS byte offsets of the regions
 constexpr int PF_OFF_AT = PF_B_AT + PF_B_STAGES * PF_B_BYTES;  // plan offsets of the tile's block
-constexpr int PF_TRASH_AT = PF_OFF_AT + PF_OFF_INTS * 4;       // one fold cell per thread
-constexpr int PF_LDS_BYTES = PF_TRASH_AT + PF_NT * 2;
+constexpr int PF_TRASH_AT = PF_OFF_AT + PF_OFF_INTS * 4;       // one fold cell per thread (own 4-byte word)
+constexpr int PF_LDS_BYTES = PF_TRASH_AT + PF_NT * 4;
 static_assert(PF_BN == kPlanBN && PF_BK == kPlanBK, "plan tiling must match the kernel");
 static_assert(PF_LDS_BYTES <= 160 * 1024, "prefill LDS budget");
 
@@ -529,7 +529,7 @@ template <bool XB>
 __device__ __forceinline__ void fold_fast(f16 *Bs, f16 *trash, uint32_t e, bool valid, float alpha) {
     const int r = (e >> 24) & (PF_BN - 1), c = (e >> 16) & (PF_BK - 1);  // always inside the tile
     const float v = (float)__builtin_bit_cast(f16, (uint16_t)(e & 0xffffu));
-    uint16_t *p = reinterpret_cast<uint16_t *>(valid ? Bs + pf_swz(r, c >> 3) + (c & 7) : trash + threadIdx.x);
+    uint16_t *p = reinterpret_cast<uint16_t *>(valid ? Bs + pf_swz(r, c >> 3) + (c & 7) : trash + 2 * threadIdx.x);
     *p = fold_add<XB>(*p, alpha * v);
 }
 
