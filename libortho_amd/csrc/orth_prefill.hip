@@ -750,22 +750,27 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
 //
 // For layers wide enough to give every CU one tile in one round (4096 ->
 // 11008 at 2048 tokens: 8 token tiles x 32 row ranges of 352 rows = 256
-// workgroups; the 256 x 128 tile above needs 688 tiles, 2.69 rounds).
+// workgroups; the 256 x 128 tile above needs 688 tiles, 2.69 rounds), and
+// with 128-row tiles in 64-column steps for narrower layers (c3: 256
+// workgroups of 256 x 128).
 //
 //  * Workgroup tile 256 tokens x R = 32 * NRT rows, 8 waves (two per SIMD,
 //    so one's MFMAs run beside the other's dequantisation) in a 4 x 2 grid,
-//    each 64 tokens x 16 NRT rows with v_mfma_f32_16x16x32_f16: 4 x NRT
-//    accumulator tiles, 176 AGPRs at NRT = 11.  Each operand read from LDS
-//    feeds NRT (activations) or 4 (weights) MFMAs: a CU reads 120 KB of
-//    operands per 352 MFMA cycles' worth of one step (the 256 x 128 tile
-//    read 128 KB per 128).
-//  * K advances 32 columns a step: activations in 2 LDS stages of 16 KB,
-//    dequantised weights (the same fp16(q * s) as above, 16 bytes of nibbles
-//    per row and step, two threads per row) in 3 stages of R x 64 bytes.
+//    each 64 tokens x 16 NRT rows with v_mfma_f32_16x16x32_f16, the weights
+//    as the first operand: 4 x NRT accumulator tiles (176 registers at NRT
+//    = 11).  Each operand read from LDS feeds NRT (activations) or 4
+//    (weights) MFMAs.
+//  * K advances 32 KS columns a step: activations in 2 LDS stages, loaded
+//    straight into LDS (buffer_load ... lds); dequantised weights (the same
+//    fp16(q * s) as above, one 4-byte word of nibbles per job, 4 KS threads
+//    per row) in 3 stages; group scales loaded only at the steps that start
+//    a group.
 //  * The ortho plan's (128-row block, 64-column step) entries of the up to
 //    four blocks the row range touches are folded into the weight stage one
-//    step after its dequantisation (each 64-column step in two halves), so
-//    one barrier a step orders everything.
+//    step after its dequantisation (each 64-column plan step in two halves
+//    when KS = 1), late in the step, so one barrier a step orders
+//    everything and an entry load has nearly a step to land.
+//  * Each step is laid out by hand in 4 NRT KS slots, one MFMA each.
 //  * Workgroup b takes token tile b % TT and row range b / TT: with 8 token
 //    tiles each XCD holds one token tile's activations in its L2.
 constexpr int PW_BM = 256, PW_BK = 32, PW_NT = 512;
