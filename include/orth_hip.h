@@ -106,9 +106,9 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  * term), the quarter-split kernel (17..32, K = 4096, a plan or no ortho
  * term), the slice-split kernel (17..32 at the other K % 128 == 0, a plan
  * or no ortho term), the split-K mid-batch kernel (other batches up to 64),
- * the MFMA prefill kernels above (from 512 tokens the wide kernel: one
- * 256 x 352 tile per workgroup where that needs fewer rounds of the grid
- * than 256 x 128 tiles, as at 4096 -> 11008 with 2048 tokens, else 256 x
+ * the MFMA prefill kernels above (the wide kernel where its 256 x 352
+ * tile per workgroup needs fewer rounds of the grid than 256 x 128 tiles,
+ * as at 4096 -> 11008 with 2048 tokens, or from 1024 tokens with 256 x
  * 128 tiles in 64-column steps), and a general kernel for shapes and
  * dtypes the fast kernels do not take (orth_hip_last_kernel() names the
  * choice).  BF16 I/O

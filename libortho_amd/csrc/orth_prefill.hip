@@ -1343,12 +1343,14 @@ static bool wide_rows_pay(const ForwardArgs &a, int cus) {
     return t_wide <= t_tile;
 }
 
-// The wide kernel's 128-row tile has the 256 x 128 kernel's grid and runs
-// faster (c3 at 2048 tokens: 80 against 86 us at alpha = 1, 75 against 77
-// at alpha = 0): it takes the prefill calls of 512 tokens and more.
+// The wide kernel's 128-row tile has the 256 x 128 kernel's grid: faster
+// from 1024 tokens (c3 at 2048: 78-80 against 83-86 us at alpha = 1; at
+// 1536: 73 against 77), level at 1024, 2-4 % slower at 512-768 (c3 70.6
+// against 72.2 us at 512, 70.7 against 73.3 at 768).  So the wide kernel
+// takes a call where its 352-row tile needs fewer rounds of the grid, or
+// from 1024 tokens.
 bool prefill_wide_preferred(const ForwardArgs &a, int cus) {
-    (void)cus;
-    return prefill_wide_supported(a) && a.M >= 512;
+    return prefill_wide_supported(a) && (wide_rows_pay(a, cus) || a.M >= 1024);
 }
 
 hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream_t stream, int cus) {

@@ -56,7 +56,8 @@ def test_mid_batch_split_k_partials_in_scratch(gpu):
 
 
 def test_prefill_plan_in_scratch(gpu):
-    compare(W.config_layer("c3"), (2048, 600), 1.0, "prefill_wide", 8200)
+    compare(W.config_layer("c3"), (2048, 1024), 1.0, "prefill_wide", 8200)
+    compare(W.config_layer("c3"), (600, 300), 1.0, "prefill", 8250)
 
 
 def test_one_launch_mid_batch_needs_no_scratch(gpu):
@@ -159,7 +160,8 @@ def captured_node_types(entry, desc, x, y, warm=False, replay=None):
         h.hipStreamDestroy(s)
 
 
-@pytest.mark.parametrize("cfg,M,alpha,kernel", [("c2", 24, 1.0, "skinny"), ("c3", 600, 1.0, "prefill_wide"),
+@pytest.mark.parametrize("cfg,M,alpha,kernel", [("c2", 24, 1.0, "skinny"), ("c3", 600, 1.0, "prefill"),
+                                                ("c3", 1024, 1.0, "prefill_wide"),
                                                 ("c2", 32, 0.0, "quarter"), ("c2", 1, 1.0, "decode")])
 def test_noalloc_capture_has_kernel_nodes_only(gpu, cfg, M, alpha, kernel):
     layer = W.config_layer(cfg)
