@@ -44,7 +44,8 @@ hipError_t launch_plan_build(const ForwardArgs &a, void *plan, hipStream_t strea
 int64_t plan_prefill_bytes(int64_t N, int64_t K, int64_t nnz);
 hipError_t launch_plan_build_prefill(const ForwardArgs &a, void *plan, hipStream_t stream);
 hipError_t plan_read_flags(const void *plan, hipStream_t stream, uint32_t *flags);
-hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream);
+hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream, float *part, int S);
+int prefill_ksplit(const ForwardArgs &a, int cus);
 bool prefill_wide_supported(const ForwardArgs &a);
 bool prefill_wide_preferred(const ForwardArgs &a, int cus);
 hipError_t launch_prefill_wide(const ForwardArgs &a, const void *plan, hipStream_t stream, int cus);
@@ -336,6 +337,13 @@ int workspace_for(int dev, hipStream_t stream, int64_t part_bytes, float **part)
     return ORTH_OK;
 }
 
+// The K split of a 256 x 128 prefill call: only with a plan or without an
+// ortho term (an unplanned call's temporary plan would share the scratch
+// array with the partials under capture and in no-allocation calls).
+int prefill_split(const ForwardArgs &a, const void *plan, int cus) {
+    return !a.has_ortho || plan ? prefill_ksplit(a, cus) : 1;
+}
+
 // The kernel a forward call takes under `policy` (orth_hip_set_kernel_policy).
 int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int cus, int *kernel) {
     const bool dec_ok = decode_supported(a) || decode_bf16_supported(a, a.has_ortho ? plan : nullptr);
@@ -395,7 +403,11 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int cus, int
             else if (sp_ok && a.M > 16) *kernel = KERNEL_SPLIT;
             else if (sk_pref) *kernel = KERNEL_SKINNY;
             else if (dec_ok) *kernel = KERNEL_DECODE;
-            else if (pre_ok && a.M > 16) *kernel = prefill_wide_preferred(a, cus) ? KERNEL_PREFILL_WIDE : KERNEL_PREFILL;
+            // (the 256 x 128 kernel where it splits K: c3 at 512 or 1024
+            // tokens, where the tile grid alone leaves CUs idle)
+            else if (pre_ok && a.M > 16)
+                *kernel = prefill_split(a, plan, cus) == 1 && prefill_wide_preferred(a, cus) ? KERNEL_PREFILL_WIDE
+                                                                                             : KERNEL_PREFILL;
             else *kernel = KERNEL_GENERAL;
     }
     return ORTH_OK;
@@ -496,9 +508,25 @@ int launch_kernel(const ForwardArgs &a, const void *plan, int kernel, int dev, h
         e = qk ? launch_quarter(a, a.has_ortho ? plan : nullptr, part, stream)
             : sk ? launch_split(a, a.has_ortho ? plan : nullptr, part, stream)
                  : launch_skinny(a, a.has_ortho ? plan : nullptr, cus, part, stream);
+    } else if (kernel == KERNEL_PREFILL && prefill_split(a, plan, g_dev[dev].cus) > 1) {
+        // K split: FP32 partials in the stream's workspace, or the scratch
+        // array (prefill_ksplit keeps them within it)
+        const int S = prefill_split(a, plan, g_dev[dev].cus);
+        const int64_t pbytes = (int64_t)S * a.M * a.N * 4;
+        float *part = nullptr;
+        if (noalloc) {
+            if (pbytes > (int64_t)ORTH_NOALLOC_SCRATCH_BYTES)
+                return fail(ORTH_ERR_UNSUPPORTED, "prefill K split needs %lld bytes of scratch", (long long)pbytes);
+            part = static_cast<float *>(g_dev[dev].scratch);
+        } else {
+            rc = workspace_for(dev, stream, pbytes, &part);
+            if (rc != ORTH_OK) return rc;
+        }
+        e = launch_prefill(a, a.has_ortho ? plan : nullptr, stream, part, S);
     } else if (kernel == KERNEL_PREFILL || kernel == KERNEL_PREFILL_WIDE) {
         auto pf = [&](const void *p) {
-            return kernel == KERNEL_PREFILL_WIDE ? launch_prefill_wide(a, p, stream, g_dev[dev].cus) : launch_prefill(a, p, stream);
+            return kernel == KERNEL_PREFILL_WIDE ? launch_prefill_wide(a, p, stream, g_dev[dev].cus)
+                                                 : launch_prefill(a, p, stream, nullptr, 1);
         };
         if (a.has_ortho && !plan && noalloc) {
             // the prefill part of a plan, built in the scratch array

@@ -398,6 +398,11 @@ struct PrefillArgs {
     int nbm, nbn;             // tile grid
     const void *bias;  // [N] added after rounding (out_f16), or null
     int bias_dtype;
+    // K split over the grid (256 x 128 kernel): workgroup row y takes the
+    // 64-column steps [y * sps, y * sps + sps) and, when part is set, writes
+    // its FP32 sums to part[y][M][N] for split_reduce_kernel; else sps = K / 64
+    int sps = 1 << 30;
+    float *part = nullptr;
 };
 
 constexpr int PF_BM = 256, PF_BN = 128, PF_BK = 64;
@@ -434,7 +439,8 @@ struct PfLane {
     uint32_t xoff[4];  // byte offsets of this thread's activation chunks (step 0)
     uint32_t qoff;     // byte offset of this thread's weight bytes (step 0)
     uint32_t soff;     // element offset of this thread's weight row scales
-    int gshift;        // scale group of step u: u >> gshift (G = 64 << gshift; G = K: 31)
+    int gshift;        // scale group of step u: (u0 + u) >> gshift (G = 64 << gshift; G = K: 31)
+    int u0;            // the workgroup's first step (K split)
     int arow[4], achunk[4];
 };
 
@@ -447,7 +453,7 @@ __device__ __forceinline__ void pf_load_a(const PrefillArgs &a, const PfLane &L,
 __device__ __forceinline__ void pf_load_b(const PrefillArgs &a, const PfLane &L, int u, PfB &r) {
     const char *base = reinterpret_cast<const char *>(a.q) + (int64_t)u * (PF_BK / 2);
     r.v = *reinterpret_cast<const uint2 *>(base + L.qoff);
-    r.s = reinterpret_cast<const uint16_t *>(a.scales)[L.soff + ((uint32_t)u >> L.gshift)];
+    r.s = reinterpret_cast<const uint16_t *>(a.scales)[L.soff + ((uint32_t)(L.u0 + u) >> L.gshift)];
 }
 
 // This thread's plan entry for step u (the range comes from the offsets
@@ -645,7 +651,11 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
 
     const int tid = threadIdx.x, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int nk = (int)(a.K / PF_BK);
+    // this workgroup's steps of K (the host sizes the grid so that every
+    // workgroup row has at least one)
+    const int nk_all = (int)(a.K / PF_BK);
+    const int u0 = (int)blockIdx.y * a.sps;
+    const int nk = min(a.sps, nk_all - u0);
 
     // per-thread offsets, fixed for the whole K loop (rows past M / N repeat
     // the last row; their outputs are never stored)
@@ -656,13 +666,14 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
         L.arow[i] = idx >> 3;
         L.achunk[i] = idx & 7;
         const int64_t m = min(m0 + L.arow[i], a.M - 1);
-        L.xoff[i] = (uint32_t)((m * a.K + L.achunk[i] * 8) * 2);
+        L.xoff[i] = (uint32_t)((m * a.K + (int64_t)u0 * PF_BK + L.achunk[i] * 8) * 2);
     }
     {
         const int64_t n = min(n0 + (tid >> 2), a.N - 1);
-        L.qoff = (uint32_t)(n * (a.K >> 1) + (tid & 3) * 8);
+        L.qoff = (uint32_t)(n * (a.K >> 1) + (int64_t)u0 * (PF_BK / 2) + (tid & 3) * 8);
         L.soff = (uint32_t)(n * a.ngroups);
         L.gshift = a.ngroups == 1 ? 31 : __builtin_ctzll(a.G / PF_BK);
+        L.u0 = u0;
     }
 
     bool canonical = true;
@@ -676,7 +687,7 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
         const bool ok = h->magic == kPlanMagic && h->version == kPlanVersion && h->n == a.N &&
                         h->k == a.K && h->nnz == a.nnz;
         for (int i = tid; i <= nk; i += PF_NT)
-            offs[i] = ok ? min(max(a.offsets[(int64_t)bn_i * (nk + 1) + i], 0), a.nnz) : 0;
+            offs[i] = ok ? min(max(a.offsets[(int64_t)bn_i * (nk_all + 1) + u0 + i], 0), a.nnz) : 0;
         canonical = !ok || (h->flags & kPlanNonCanonical) == 0;
         __syncthreads();
     }
@@ -727,6 +738,7 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
 
     // epilogue: lane holds D[token 8(i/4) + 4(lane/32) + i%4][row lane%32]
     const int lane = tid & 63;
+    float *part = a.part ? a.part + (int64_t)blockIdx.y * a.M * a.N : nullptr;
 #pragma unroll
     for (int bm = 0; bm < 2; bm++) {
 #pragma unroll
@@ -736,7 +748,9 @@ __global__ void __launch_bounds__(PF_NT) prefill_kernel(PrefillArgs a) {
             for (int i = 0; i < 16; i++) {
                 const int64_t m = m0 + wm * 64 + bm * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
                 if (m < a.M && n < a.N) {
-                    if constexpr (XB)
+                    if (part)
+                        part[m * a.N + n] = acc[bm][bn][i];
+                    else if constexpr (XB)
                         reinterpret_cast<uint16_t *>(a.y)[m * a.N + n] = out_bf16(acc[bm][bn][i], a.bias, a.bias_dtype, n);
                     else
                         a.y[m * a.N + n] = out_f16(acc[bm][bn][i], a.bias, a.bias_dtype, n);
@@ -1285,7 +1299,41 @@ bool prefill_supported(const ForwardArgs &a) {
     return true;
 }
 
-hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream) {
+// K split of the 256 x 128 kernel: a grid of tiles that leaves CUs idle
+// (c3 at 512 tokens: 64 tiles for 256 CUs) gives each tile S workgroups over
+// slices of K, their FP32 sums added in slice order by split_reduce_kernel.
+// S minimises a cost measured on MI355X (kernel traces of c3 at 65, 512
+// and 1024 tokens and c2 at 65): a round of the grid takes ~12 us (the
+// workgroup's latency chain: plan offsets, first loads) plus ~0.95 us per
+// 64-column step, and the reduction ~3 us plus its partials at ~6 TB/s;
+// the smallest S on a tie.  Slices keep at least 4 steps, and the partials
+// fit the no-allocation scratch array, so that both entry points split a
+// call alike.
+int prefill_ksplit(const ForwardArgs &a, int cus) {
+    if (!prefill_supported(a) || cus <= 0) return 1;
+    const int64_t tiles = ((a.M + PF_BM - 1) / PF_BM) * ((a.N + PF_BN - 1) / PF_BN);
+    const int nk = (int)(a.K / PF_BK);
+    auto cost = [&](int s) {
+        const int64_t rounds = (tiles * s + cus - 1) / cus;
+        const int steps = (nk + s - 1) / s;
+        double t = (double)rounds * (12.0 + 0.95 * steps);
+        if (s > 1) t += 3.0 + (double)s * a.M * a.N * 4 / 6.0e6;
+        return t;
+    };
+    int best = 1;
+    double best_t = cost(1);
+    for (int s = 2; s <= 8; s++) {
+        if (nk / s < 4 || (int64_t)s * a.M * a.N * 4 > (int64_t)ORTH_NOALLOC_SCRATCH_BYTES) break;
+        const double t = cost(s);
+        if (t < best_t) best = s, best_t = t;
+    }
+    return best;
+}
+
+hipError_t launch_slice_reduce(const ForwardArgs &a, const float *part, int S, hipStream_t stream);  // orth_split.hip
+
+// part: S * M * N floats when S > 1 (the K split), else unused
+hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t stream, float *part, int S) {
     PrefillArgs p;
     p.q = a.q;
     p.scales = static_cast<const f16 *>(a.scales);
@@ -1311,12 +1359,21 @@ hipError_t launch_prefill(const ForwardArgs &a, const void *plan, hipStream_t st
     p.nbn = (int)((a.N + PF_BN - 1) / PF_BN);
     const unsigned blocks = (unsigned)(p.nbm * p.nbn);
     if (p.fold && p.nnz <= 0) return hipErrorInvalidValue;
+    // slices of sps steps, every one non-empty (ny <= S)
+    const int nk = (int)(a.K / PF_BK);
+    if (S > 1 && !part) return hipErrorInvalidValue;
+    p.sps = S > 1 ? (nk + S - 1) / S : nk;
+    p.part = S > 1 ? part : nullptr;
+    const unsigned ny = (unsigned)((nk + p.sps - 1) / p.sps);
     const bool xb = a.io_dtype == ORTH_DT_BF16;
-    if (p.fold && xb) hipLaunchKernelGGL((prefill_kernel<true, true>), dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
-    else if (p.fold) hipLaunchKernelGGL((prefill_kernel<true, false>), dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
-    else if (xb) hipLaunchKernelGGL((prefill_kernel<false, true>), dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
-    else hipLaunchKernelGGL((prefill_kernel<false, false>), dim3(blocks), dim3(PF_NT), PF_LDS_BYTES, stream, p);
-    return hipGetLastError();
+    const dim3 grid(blocks, ny);
+    if (p.fold && xb) hipLaunchKernelGGL((prefill_kernel<true, true>), grid, dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    else if (p.fold) hipLaunchKernelGGL((prefill_kernel<true, false>), grid, dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    else if (xb) hipLaunchKernelGGL((prefill_kernel<false, true>), grid, dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<false, false>), grid, dim3(PF_NT), PF_LDS_BYTES, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ny == 1) return e;
+    return launch_slice_reduce(a, part, (int)ny, stream);
 }
 
 // The wide-row tile: rows per workgroup 32 * kPwNrt.  Taken when the layer

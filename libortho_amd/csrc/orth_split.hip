@@ -730,6 +730,31 @@ hipError_t launch_split_group(const ForwardArgs *as, const void *const *plans, i
     return hipGetLastError();
 }
 
+// y = part[0] + ... + part[S - 1] for one layer (the prefill kernel's K
+// split), rounded (+ bias) as above
+hipError_t launch_slice_reduce(const ForwardArgs &a, const float *part, int S, hipStream_t stream) {
+    SplitReduceArgs r;
+    r.nlayers = 1;
+    r.M = (int)a.M;
+    r.S = S;
+    r.xb = a.io_dtype == ORTH_DT_BF16 ? 1 : 0;
+    const int vec4 = a.N % 4 == 0 && (reinterpret_cast<uintptr_t>(a.y) & 7) == 0 ? 1 : 0;
+    const int64_t threads = vec4 ? a.M * a.N / 4 : a.M * a.N;
+    const int64_t blocks = (threads + 255) / 256;
+    for (int l = 0; l < kSpMaxLayers; l++) {
+        r.part[l] = part;
+        r.y[l] = a.y;
+        r.bias[l] = a.bias;
+        r.bias_dtype[l] = a.bias_dtype;
+        r.N[l] = a.N;
+        r.vec4[l] = vec4;
+        r.rb0[l] = l == 0 ? 0 : (int)blocks;
+    }
+    r.rb0[kSpMaxLayers] = (int)blocks;
+    hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, r);
+    return hipGetLastError();
+}
+
 hipError_t launch_split(const ForwardArgs &a, const void *plan, float *part, hipStream_t stream) {
     return launch_split_group(&a, &plan, 1, part, stream);
 }

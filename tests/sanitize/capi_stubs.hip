@@ -48,7 +48,8 @@ hipError_t launch_plan_build(const ForwardArgs &, void *, hipStream_t) { return 
 int64_t plan_prefill_bytes(int64_t N, int64_t K, int64_t nnz) { return nnz > 0 ? 64 + 4 * nnz + N + K : 0; }
 hipError_t launch_plan_build_prefill(const ForwardArgs &, void *, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t plan_read_flags(const void *, hipStream_t, uint32_t *) { return hipErrorInvalidValue; }
-hipError_t launch_prefill(const ForwardArgs &, const void *, hipStream_t) { return hipErrorInvalidValue; }
+hipError_t launch_prefill(const ForwardArgs &, const void *, hipStream_t, float *, int) { return hipErrorInvalidValue; }
+int prefill_ksplit(const ForwardArgs &, int) { return 1; }
 hipError_t prefill_prepare_device() { return hipSuccess; }
 hipError_t plan_prepare_device() { return hipSuccess; }
 bool skinny_supported(const ForwardArgs &) { return false; }

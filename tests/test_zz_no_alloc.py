@@ -2,8 +2,8 @@
 device array) against orth_layer_forward_hip_ex (per-stream workspace and
 stream-ordered allocations), through the C ABI: same bits, on two calls in
 a row with the second smaller, for each kernel that uses scratch (the
-mid-batch split-K partials; the prefill plan built for an unplanned
-alpha > 0 call) and for decode; and a request beyond the scratch size is
+mid-batch split-K partials; the prefill K split's partials; the prefill
+plan built for an unplanned alpha > 0 call) and for decode; and a request beyond the scratch size is
 refused before anything is launched.  Captured into a graph, a call of
 either entry adds kernel nodes only (no allocation node), and a captured
 call beyond the scratch size needs an eager call on its stream first; calls
@@ -53,6 +53,12 @@ def test_scratch_size_is_exported(gpu):
 
 def test_mid_batch_split_k_partials_in_scratch(gpu):
     compare(W.config_layer("c2"), (24, 12), 1.0, "skinny", 8100)
+
+
+def test_prefill_k_split_partials_in_scratch(gpu):
+    # no ortho term (no plan needed): c3's K in 4 slices at 512 tokens (32 MB
+    # of FP32 partials, the whole scratch array) and at 300
+    compare(W.config_layer("c3"), (512, 300), 0.0, "prefill", 8150)
 
 
 def test_prefill_plan_in_scratch(gpu):
@@ -161,7 +167,7 @@ def captured_node_types(entry, desc, x, y, warm=False, replay=None):
 
 
 @pytest.mark.parametrize("cfg,M,alpha,kernel", [("c2", 24, 1.0, "skinny"), ("c3", 600, 1.0, "prefill"),
-                                                ("c3", 1024, 1.0, "prefill_wide"),
+                                                ("c3", 1024, 1.0, "prefill_wide"), ("c3", 512, 0.0, "prefill"),
                                                 ("c2", 32, 0.0, "quarter"), ("c2", 1, 1.0, "decode")])
 def test_noalloc_capture_has_kernel_nodes_only(gpu, cfg, M, alpha, kernel):
     layer = W.config_layer(cfg)
