@@ -24,6 +24,10 @@
 //    dequant entry point gives the bit-exact FP32 weights.)
 //  * Tiles are mapped XCD-aware: consecutive workgroup ids land on different
 //    XCDs, so the tile order is remapped to give each XCD a contiguous run.
+//  * Where the tiles alone leave CUs idle (fewer tokens than the grid needs),
+//    K is split over the grid: each tile's workgroups take slices of the
+//    64-column steps and write FP32 partials, which split_reduce_kernel
+//    (orth_split.hip) adds in slice order (prefill_ksplit).
 #include <type_traits>
 
 #include "orth_common.h"
