@@ -641,6 +641,9 @@ PROFILE_WORKLOADS = {
     "c1_m1_a1": ("c1", 1, 1.0),
     "c1_m1_a0": ("c1", 1, 0.0), "c3_m2048_a1": ("c3", 2048, 1.0), "c3_m2048_a0": ("c3", 2048, 0.0),
     "c4_m8_a1": ("c4", 8, 1.0), "c5_m1": ("c5", 1, 1.0), "c5_m1_grouped": ("c5", 1, 1.0),
+    # prefill below one round of the tile grid (the K split)
+    "c3_m65_a1": ("c3", 65, 1.0), "c3_m512_a1": ("c3", 512, 1.0), "c3_m1024_a1": ("c3", 1024, 1.0),
+    "c2_m65_a1": ("c2", 65, 1.0),
     "c5_m32": ("c5", 32, 1.0), "c5_m32_grouped": ("c5", 32, 1.0), "copy": (None, 0, 0.0),
     # the bench's BF16 / FP32-activation lines and its per-row 4000->11008 layer
     "c2_m1_bf16": ("c2", 1, 1.0, "bf16"), "c2_m8_bf16": ("c2", 8, 1.0, "bf16"),
@@ -928,6 +931,14 @@ def main():
                                   "TFLOP/s": round(tf, 1),
                                   "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
                 log(f"  {secondary[-1]}")
+        # c3 at 512 tokens: 64 tiles for 256 CUs, so K is split over the grid
+        c3 = W.config_layer("c3")
+        rr = time_workload(torch, c3, 512, 1.0, 200, 3, plan=True)
+        tf = W.algorithmic_flops(c3, 512, 1.0) / (rr["ms_per_step"] * 1e-3) / 1e12
+        secondary.append({"workload": "prefill 4096->4096 (c3) M=512 alpha=1.0", "kernel": rr["kernel"],
+                          "us_per_step": round(rr["ms_per_step"] * 1e3, 2), "TFLOP/s": round(tf, 1),
+                          "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
+        log(f"  {secondary[-1]}")
         for cfg, m, a in (("c1", 1, 1.0), ("c1", 1, 0.0), ("c4", 8, 1.0)):
             lay = W.config_layer(cfg)
             rr = time_workload(torch, lay, m, a, SECONDARY_STEPS, 10, plan=True)
