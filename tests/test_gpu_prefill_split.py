@@ -6,7 +6,8 @@ without an ortho term.  Checked against the FP64 oracle and against the
 unsplit wide kernel on the same inputs: slices that start inside a scale
 group, K = 11,008, group-256 and per-row scales, N % 4 != 0 (the scalar
 reduction), plan steps with more entries than one per thread, duplicate
-columns, BF16, the fused bias, no ortho term."""
+columns, BF16, the fused bias, no ortho term, and a captured graph replayed
+between eager calls."""
 import numpy as np
 import pytest
 import torch
@@ -178,3 +179,32 @@ def test_unplanned_calls_stay_unsplit(oracle_mod):
     check(oracle_mod, lay, x, 1.0, y, rows_of(512), "c3 M=512 unplanned")
     y2, _ = run(lay, x, 1.0, plan=False)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+
+
+def test_split_forward_captured_on_a_fresh_stream():
+    """A split prefill forward captured in a HIP graph on a stream that never
+    ran it eagerly (its partials in the GPU's scratch array, 32 MB at c3 with
+    512 tokens), replayed several times with eager split forwards of another
+    shape between the replays: every replay equals the eager result bit for
+    bit."""
+    lay = W.config_layer("c3")
+    d = W.to_device(lay)
+    plan = _C_ops.build_plan(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], lay.K)
+    x = torch.from_numpy(W.make_x(512, lay.K, 9780)).cuda()
+    y_eager = torch.empty(512, lay.N, dtype=torch.float16, device="cuda")
+    _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y_eager, 1.0, plan)
+    assert _C_ops.last_kernel() == "prefill"
+    torch.cuda.synchronize()
+    y = torch.empty_like(y_eager)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=s):
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x, y, 1.0, plan)
+    x2 = torch.from_numpy(W.make_x(300, lay.K, 9781)).cuda()
+    y2 = torch.empty(300, lay.N, dtype=torch.float16, device="cuda")
+    for r in range(4):
+        y.fill_(float("nan"))
+        g.replay()
+        _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x2, y2, 1.0, plan)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y_eager.view(torch.int16)), f"replay {r}"
