@@ -105,7 +105,9 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  * 4), the one-launch mid-batch kernel (5..16, K = 4096, a plan or no ortho
  * term), the quarter-split kernel (17..32, K = 4096, a plan or no ortho
  * term), the slice-split kernel (17..32 at the other K % 128 == 0, a plan
- * or no ortho term), the split-K mid-batch kernel (other batches up to 64),
+ * or no ortho term), the split-K mid-batch kernel (other batches up to 64;
+ * 33..64 at K > 4096 with a plan or no ortho term: the prefill kernel with
+ * K split over the grid),
  * the MFMA prefill kernels above (the wide kernel where its 256 x 352
  * tile per workgroup needs fewer rounds of the grid than 256 x 128 tiles,
  * as at 4096 -> 11008 with 2048 tokens, or from 1024 tokens with 256 x

@@ -401,6 +401,11 @@ int pick_kernel(const ForwardArgs &a, const void *plan, int policy, int cus, int
             // BF16 with 512-word records): c5 down_proj M=32 23.7 against
             // 35.5 us for the split-K kernel
             else if (sp_ok && a.M > 16) *kernel = KERNEL_SPLIT;
+            // 33..64 tokens at K > 4096: the prefill kernel with K split
+            // over the grid (c5 down_proj, K = 11008: 35-37 against 44-53
+            // us on the split-K kernel at 33-64 tokens; at K = 4096 the
+            // split-K kernel is level or ahead: c2 M=48 35.8 against 42.4)
+            else if (pre_ok && a.M > 32 && a.K > 4096 && prefill_split(a, plan, cus) > 1) *kernel = KERNEL_PREFILL;
             else if (sk_pref) *kernel = KERNEL_SKINNY;
             else if (dec_ok) *kernel = KERNEL_DECODE;
             // (the 256 x 128 kernel where it splits K: c3 at 512 or 1024

@@ -104,7 +104,8 @@ def auto_kernel(M, planned=False, K=4096):
     if planned and 17 <= M <= 32 and K % 128 == 0:
         return "split"
     if M <= 64:
-        return "skinny"
+        # (33..64 tokens at K > 4096 with a plan: the prefill kernel, K split)
+        return "prefill" if planned and M > 32 and K > 4096 else "skinny"
     # (the wide kernel from 1024 tokens, or where its 352-row tile needs
     # fewer rounds of the grid: N >= 5632 layers from 512 tokens, not the
     # shapes this helper serves below 1024)

@@ -208,3 +208,19 @@ def test_split_forward_captured_on_a_fresh_stream():
         _C_ops.forward_planned(d["q"], d["scales"], d["vals"], d["col"], d["row_ptr"], x2, y2, 1.0, plan)
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), y_eager.view(torch.int16)), f"replay {r}"
+
+
+@pytest.mark.parametrize("M,dtype", [(33, torch.float16), (64, torch.float16), (40, torch.bfloat16)])
+def test_split_takes_33_to_64_tokens_at_wide_k(oracle_mod, M, dtype):
+    """c5's down projection (K = 11,008) at 33..64 tokens: the split prefill
+    kernel (8 slices), against the oracle and the split-K mid-batch kernel
+    that took these calls before."""
+    lay = {l.name: l for l in W.llama_block()}["down_proj"]
+    x = x_of(M, lay.K, 9790 + M, dtype)
+    y, k = run(lay, x, 1.0, dtype=dtype)
+    assert k == "prefill"
+    tol = TOL if dtype == torch.float16 else 1e-2
+    check(oracle_mod, lay, x, 1.0, y, rows_of(M), f"down_proj M={M} {dtype}", tol=tol)
+    y2, k2 = run(lay, x, 1.0, policy="skinny", dtype=dtype)
+    assert k2 == "skinny"
+    agree(y, y2, f"down_proj M={M} against the split-K mid-batch kernel", rel=2e-3 if dtype == torch.float16 else 1e-2)
