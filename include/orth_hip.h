@@ -151,13 +151,16 @@ int orth_layer_forward_hip_ex(const orth_hip_layer_t *layer, const void *plan, i
  * hipMalloc, hipFree or stream-ordered allocation, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid it).  No counterpart in the reference.  The scratch memory the
- * kernels need (the mid-batch kernel's split-K partials, the prefill part of
- * an ortho plan when the caller passes none) comes from a static device
- * array of ORTH_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends;
- * a call that would need more returns ORTH_ERR_UNSUPPORTED before launching
- * anything.  Every call on one GPU shares that GPU's array: calls that
- * overlap in time on one GPU (two streams, or two threads) race and give
- * wrong results; calls ordered on one stream are safe.  Each call writes all
+ * kernels need (the mid-batch kernels' split-K, quarter and slice partials,
+ * the prefill K split's partials, the prefill part of an ortho plan when
+ * the caller passes none) comes from a static device array of
+ * ORTH_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call
+ * that would need more returns ORTH_ERR_UNSUPPORTED before launching
+ * anything.  Every call on one GPU shares that GPU's array: an eager call on
+ * a stream other than the previous call's first waits for that call (an
+ * event the library records), so eager calls on several streams or threads
+ * do not race; calls captured into graphs, and their replays, are not
+ * ordered that way and must be ordered by the caller.  Each call writes all
  * the scratch it reads, so nothing carries over from an earlier call. */
 #define ORTH_NOALLOC_SCRATCH_BYTES (32u << 20)
 int orth_layer_forward_hip_noalloc(const orth_hip_layer_t *layer, const void *plan, int64_t plan_bytes,
