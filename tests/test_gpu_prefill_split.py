@@ -96,6 +96,7 @@ def test_split_c3_512_tokens(oracle_mod, alpha):
     (11008, 4096, 128, 512, 1.0, 0.02),   # down projection: 4 slices of 43 steps (odd: inside group-128 scales)
     (3072, 1030, None, 100, 1.0, 0.01),   # per-row scales, N % 4 != 0 (the scalar reduction)
     (512, 1000, 128, 300, 1.0, 0.02),     # K = 512: 2 slices of 4 steps, ragged N
+    (4096, 4608, 128, 200, 1.0, 0.01),    # 36 tiles: 7 slices, 6 of 10 steps and a last one of 4
     (4096, 2048, 128, 100, 0.0, 0.0),     # no ortho term
 ])
 def test_split_shapes(oracle_mod, K, N, group, M, alpha, density):
