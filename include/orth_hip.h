@@ -108,12 +108,12 @@ int orth_layer_check_hip(const orth_hip_layer_t *layer, const void *input, void 
  * or no ortho term), the split-K mid-batch kernel (other batches up to 64;
  * 33..64 at K > 4096 with a plan or no ortho term: the prefill kernel with
  * K split over the grid),
- * the MFMA prefill kernels above (the wide kernel where its 256 x 352
+ * the MFMA prefill kernels above (256 x 128 tiles with K split over the
+ * grid and a reduction launch where the tiles alone leave CUs idle and a
+ * plan or no ortho term is given; else the wide kernel where its 256 x 352
  * tile per workgroup needs fewer rounds of the grid than 256 x 128 tiles,
  * as at 4096 -> 11008 with 2048 tokens, or from 1024 tokens with 256 x
- * 128 tiles in 64-column steps; else 256 x 128 tiles, with K split over
- * the grid and a reduction launch where the tiles alone leave CUs idle and
- * a plan or no ortho term is given), and a general kernel for shapes and
+ * 128 tiles in 64-column steps; else 256 x 128 tiles), and a general kernel for shapes and
  * dtypes the fast kernels do not take (orth_hip_last_kernel() names the
  * choice).  BF16 I/O
  * takes the decode kernel for 1..4 tokens and the one-launch mid-batch

@@ -1446,7 +1446,8 @@ static bool wide_rows_pay(const ForwardArgs &a, int cus) {
 // 1536: 73 against 77), level at 1024, 2-4 % slower at 512-768 (c3 70.6
 // against 72.2 us at 512, 70.7 against 73.3 at 768).  So the wide kernel
 // takes a call where its 352-row tile needs fewer rounds of the grid, or
-// from 1024 tokens.
+// from 1024 tokens (the dispatcher asks only for calls that the K split of
+// the 256 x 128 kernel does not take: c3 up to 1024 tokens is split).
 bool prefill_wide_preferred(const ForwardArgs &a, int cus) {
     return prefill_wide_supported(a) && (wide_rows_pay(a, cus) || a.M >= 1024);
 }
