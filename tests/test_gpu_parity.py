@@ -108,7 +108,9 @@ def auto_kernel(M, planned=False, K=4096):
         return "prefill" if planned and M > 32 and K > 4096 else "skinny"
     # (the wide kernel from 1024 tokens, or where its 352-row tile needs
     # fewer rounds of the grid: N >= 5632 layers from 512 tokens, not the
-    # shapes this helper serves below 1024)
+    # shapes this helper serves below 1024; planned calls whose tile grid
+    # leaves CUs idle, c3 up to 1024 tokens, take the 256 x 128 kernel with
+    # K split, "prefill": no caller here asks for those)
     return "prefill_wide" if M >= 1024 else "prefill"
 
 
